@@ -1,0 +1,265 @@
+"""CPU oracle for the int8 dynamic-quantized linear path — TEST INFRASTRUCTURE ONLY.
+
+numpy-facing wrappers over ``liboracle.so`` (``oracle.c``), a single-threaded C
+restatement of the reference's CPU operators.  Only ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
+checker; the product (``iconnx_amd``) never calls it.
+
+Each wrapper mirrors the reference operator's ``forward`` (argument meaning and the
+conditions under which it panics — raised here as :class:`OracleError`):
+
+* :func:`dynamic_quantize_linear` — ``src/operators/dynamic_quantize_linear.rs:32-112``
+* :func:`matmul_integer` — ``src/operators/matmul_integer.rs:52-267``
+* :func:`cast_i32_f32` — ``src/operators/cast.rs:46-49``
+* :func:`add`/:func:`sub`/:func:`mul`/:func:`div` — ``src/operators/{add,mul,div}.rs``
+* :func:`dequantize_linear` — ``src/operators/dequantize_linear.rs:32-214``
+
+Parity pins (tests/test_oracle.py): the ONNX 1.18 node goldens the reference vendors
+(tests/golden/onnx_node_goldens.json), the reference's unit-test literals, brute-force
+int64/float64 checks and closed forms.  The per-column ``b_zero_point`` form of
+:func:`matmul_integer` is an extension the reference rejects; it is pinned only by the
+ONNX definition (closed form + brute force) — reference parity unpinned for it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+DT_I8, DT_U8, DT_I32 = 0, 1, 2
+ADD, SUB, MUL, DIV = 0, 1, 2, 3
+
+
+class OracleError(RuntimeError):
+    """Raised where the reference CPU operator panics."""
+
+
+def build():
+    """Compile liboracle.so with the committed Makefile."""
+    subprocess.check_call(["make", "-s", "-C", _HERE, "-B", "liboracle.so"])
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        build()
+    lib = ctypes.CDLL(_LIB_PATH)
+    P = ctypes.c_void_p
+    S = ctypes.c_size_t
+    lib.orc_dql_u8.argtypes = [P, S, P, P, P, P]
+    lib.orc_dql_u8.restype = None
+    lib.orc_matmul_integer_rows.argtypes = [P, ctypes.c_int, P, ctypes.c_int, S, S, S,
+                                            ctypes.c_int32, P, S, S, S, P]
+    lib.orc_matmul_integer_rows.restype = ctypes.c_int
+    lib.orc_cast_i32_f32.argtypes = [P, S, P]
+    lib.orc_cast_i32_f32.restype = None
+    lib.orc_binary_f32.argtypes = [ctypes.c_int, P, P, ctypes.c_int, P, P, ctypes.c_int,
+                                   P, P, P]
+    lib.orc_binary_f32.restype = ctypes.c_int
+    lib.orc_dequantize_linear.argtypes = [P, ctypes.c_int, P, P, S, S, S, P]
+    lib.orc_dequantize_linear.restype = None
+    _lib = lib
+    return lib
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _dt(a):
+    if a.dtype == np.int8:
+        return DT_I8
+    if a.dtype == np.uint8:
+        return DT_U8
+    if a.dtype == np.int32:
+        return DT_I32
+    raise OracleError("unsupported dtype %s" % a.dtype)
+
+
+def dynamic_quantize_linear(x, return_scale64=False):
+    """(y u8 same shape, y_scale f32 scalar, y_zero_point u8 scalar)."""
+    x = np.asarray(x)
+    if x.dtype != np.float32:
+        raise OracleError("DynamicQuantizeLinear: input must be Float32, got %s" % x.dtype)
+    x = np.ascontiguousarray(x)
+    y = np.empty(x.shape, np.uint8)
+    s = np.zeros((), np.float32)
+    zp = np.zeros((), np.uint8)
+    s64 = np.zeros((), np.float64)
+    _load().orc_dql_u8(_ptr(x), x.size, _ptr(y), _ptr(s), _ptr(zp), _ptr(s64))
+    if return_scale64:
+        return y, s, zp, float(s64)
+    return y, s, zp
+
+
+def _extract_zp(zp, operand_dtype, label, n_cols=None):
+    """extract_scalar_zp (matmul_integer.rs:189-223); n_cols enables the per-column form."""
+    if zp is None:
+        return np.zeros(1, np.int32)
+    zp = np.asarray(zp)
+    if zp.dtype != operand_dtype:
+        raise OracleError("MatMulInteger: %s_zero_point dtype %s must match operand dtype %s"
+                          % (label, zp.dtype, operand_dtype))
+    if zp.ndim == 0 or (zp.ndim == 1 and zp.shape[0] == 1):
+        return zp.reshape(1).astype(np.int32)
+    if n_cols is not None and zp.ndim == 1 and zp.shape[0] == n_cols:
+        return zp.astype(np.int32)
+    raise OracleError("MatMulInteger: %s_zero_point must be scalar (got shape %s); "
+                      "per-axis zp is not supported" % (label, list(zp.shape)))
+
+
+def matmul_integer(a, b, a_zp=None, b_zp=None, per_column_b_zp=False, rows=None):
+    """int32 [M,N].  ``per_column_b_zp`` admits a [N] b_zero_point (ONNX form; not in the
+    reference).  ``rows=(r0, r1)`` computes only those output rows (others left 0)."""
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    for t, lab in ((a, "a"), (b, "b")):
+        if t.dtype not in (np.int8, np.uint8):
+            raise OracleError("MatMulInteger: input %s must be Int8 or UInt8, got %s"
+                              % (lab, t.dtype))
+    if a.ndim != 2 or b.ndim != 2:
+        raise OracleError("MatMulInteger: a and b must be 2-D (got ranks %d, %d)"
+                          % (a.ndim, b.ndim))
+    M, K = a.shape
+    if b.shape[0] != K:
+        raise OracleError("MatMulInteger: K mismatch — a is %s, b is %s"
+                          % (list(a.shape), list(b.shape)))
+    N = b.shape[1]
+    azp = _extract_zp(a_zp, a.dtype, "a")
+    bzp = _extract_zp(b_zp, b.dtype, "b", N if per_column_b_zp else None)
+    out = np.zeros((M, N), np.int32)
+    r0, r1 = (0, M) if rows is None else rows
+    rc = _load().orc_matmul_integer_rows(_ptr(a), _dt(a), _ptr(b), _dt(b), M, K, N,
+                                         int(azp[0]), _ptr(bzp), bzp.size, r0, r1, _ptr(out))
+    if rc == 1:
+        raise OracleError("MatMulInteger: i32 overflow")
+    if rc != 0:
+        raise OracleError("MatMulInteger: invalid arguments")
+    return out
+
+
+def cast_i32_f32(x):
+    x = np.asarray(x)
+    if x.dtype != np.int32:
+        raise OracleError("Cast: only Int32 -> Float32 is on this path")
+    x = np.ascontiguousarray(x)
+    y = np.empty(x.shape, np.float32)
+    _load().orc_cast_i32_f32(_ptr(x), x.size, _ptr(y))
+    return y
+
+
+def _binary(op, a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    r = max(a.ndim, b.ndim)
+    out_shape = np.zeros(8, np.uintp)
+    out_rank = ctypes.c_int(0)
+    shp = np.broadcast_shapes(a.shape, b.shape) if _broadcastable(a.shape, b.shape) else None
+    if shp is None:
+        raise OracleError("Failed to broadcast %s with %s" % (list(a.shape), list(b.shape)))
+    out = np.empty(shp, np.float32)
+    ash = np.array(a.shape or [1], np.uintp)
+    bsh = np.array(b.shape or [1], np.uintp)
+    rc = _load().orc_binary_f32(op, _ptr(a), _ptr(ash), a.ndim, _ptr(b), _ptr(bsh), b.ndim,
+                                _ptr(out), _ptr(out_shape), ctypes.byref(out_rank))
+    if rc != 0 or out_rank.value != r:
+        raise OracleError("broadcast failed")
+    return out
+
+
+def _broadcastable(s1, s2):
+    for x, y in zip(reversed(s1), reversed(s2)):
+        if x != y and x != 1 and y != 1:
+            return False
+    return True
+
+
+def add(a, b):
+    return _binary(ADD, a, b)
+
+
+def sub(a, b):
+    return _binary(SUB, a, b)
+
+
+def mul(a, b):
+    return _binary(MUL, a, b)
+
+
+def div(a, b):
+    return _binary(DIV, a, b)
+
+
+def dequantize_linear(x, scale, zp=None, axis=1):
+    """DequantizeLinear::forward; ``axis`` only consulted for a per-axis (1-D) scale."""
+    x = np.ascontiguousarray(x)
+    if x.dtype not in (np.int8, np.uint8, np.int32):
+        raise OracleError("DequantizeLinear: input dtype %s unsupported" % x.dtype)
+    scale = np.asarray(scale)
+    if scale.dtype != np.float32:
+        raise OracleError("DequantizeLinear: scale must be Float32, got %s" % scale.dtype)
+    per_tensor = scale.ndim == 0 or (scale.ndim == 1 and scale.size == 1)
+    if per_tensor:
+        axis_size, inner = 1, max(x.size, 1)
+    else:
+        ax = axis + x.ndim if axis < 0 else axis
+        if not 0 <= ax < x.ndim:
+            raise OracleError("DequantizeLinear: axis %d out of range for ndim %d"
+                              % (axis, x.ndim))
+        if scale.size != x.shape[ax]:
+            raise OracleError("DequantizeLinear: per-axis scale length %d doesn't match "
+                              "input shape[%d] = %d" % (scale.size, ax, x.shape[ax]))
+        axis_size = x.shape[ax]
+        inner = int(np.prod(x.shape[ax + 1:])) if ax + 1 < x.ndim else 1
+    zpp = None
+    if zp is not None:
+        zp = np.asarray(zp)
+        if zp.dtype != x.dtype:
+            raise OracleError("DequantizeLinear: zero_point dtype %s must match input dtype %s"
+                              % (zp.dtype, x.dtype))
+        if zp.shape != scale.shape:
+            raise OracleError("DequantizeLinear: zero_point shape %s must match scale shape %s"
+                              % (list(zp.shape), list(scale.shape)))
+        zpp = np.ascontiguousarray(zp.reshape(-1))
+    sc = np.ascontiguousarray(scale.reshape(-1), dtype=np.float32)
+    y = np.empty(x.shape, np.float32)
+    _load().orc_dequantize_linear(_ptr(x), _dt(x), _ptr(sc),
+                                  _ptr(zpp) if zpp is not None else None,
+                                  x.size, axis_size, inner, _ptr(y))
+    return y
+
+
+def qlinear_graph(x, w, w_zp, x_scale_times_w_scale_inputs, bias, chain=(), rows=None):
+    """Run the quantized-linear subgraph op by op in graph order, as the reference
+    GraphExecutor does (src/graph_executor.rs:205-216 for DQL's three outputs, :356-432):
+
+        DynamicQuantizeLinear(x) -> (xq, xs, xzp)
+        MatMulInteger(xq, w, xzp, w_zp) -> acc i32
+        Cast(acc) -> f32;  Mul(xs, w_scale) -> s;  Mul(cast, s);  Add(., bias)
+        then each (op, operand, operand_is_lhs) of ``chain`` in order.
+
+    ``x`` is [..., K] (flattened to 2-D like the GPU executor's 3-D x 2-D arm,
+    src/cuda/executor/layout.rs:1058-1090).  ``x_scale_times_w_scale_inputs`` is the
+    w_scale tensor (scalar or [N]).  Returns a dict of every intermediate.
+    """
+    x2 = np.ascontiguousarray(x).reshape(-1, x.shape[-1])
+    xq, xs, xzp = dynamic_quantize_linear(x2)
+    per_col = np.asarray(w_zp).ndim == 1 and np.asarray(w_zp).size > 1
+    acc = matmul_integer(xq, w, xzp, w_zp, per_column_b_zp=per_col, rows=rows)
+    cast = cast_i32_f32(acc)
+    s = mul(xs, x_scale_times_w_scale_inputs)
+    y = mul(cast, s)
+    y = add(y, bias)
+    out = {"xq": xq, "x_scale": xs, "x_zp": xzp, "acc": acc, "cast": cast, "scale": s,
+           "linear": y}
+    for op, operand, operand_is_lhs in chain:
+        fn = {"Mul": mul, "Add": add, "Div": div, "Sub": sub}[op]
+        y = fn(operand, y) if operand_is_lhs else fn(y, operand)
+    out["y"] = y
+    return out
