@@ -1,0 +1,374 @@
+"""Benchmark of the int8 dynamic-quantized linear hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
+
+A step is one pass of the hot path over one batch of synthetic, HBM-resident input.  The
+default workload is BASELINE configs[1] (cfg2): x [32,128,768] f32 ->
+DynamicQuantizeLinear -> MatMulInteger with W int8 [768,3072] -> Cast -> Mul(x_scale *
+w_scale) -> Add(bias) -> Mul/Add/Div/Mul chain, i.e. three kernel launches (DQL min/max,
+DQL quantize + row sums, fused GEMM).  Other configs (--config cfg1|cfg4|cfg5a|cfg5b) are
+for the per-kernel roofline figures.
+
+Timing: W untimed warmup steps, then exactly K steps, each a replay of a HIP graph that
+holds one step (so host launch overhead is not measured), bracketed by synchronize.  The
+dominant kernel's average duration is measured live with HIP events around a graph of R
+back-to-back launches of that kernel on the same stream.  Prints ONE JSON line.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MatMulInteger int8 TOPS (% MFMA peak); encoder seq/s, DistilBERT-int8 shape b32 s128"
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+PEAK_INT8_TOPS = 5000.0       # MI355X dense int8 MFMA (no sparsity)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg4", "cfg5a", "cfg5b"])
+    ap.add_argument("--kernel-reps", type=int, default=100,
+                    help="back-to-back launches of the dominant kernel for its average duration")
+    ap.add_argument("--cpu-rows", type=int, default=None,
+                    help="rows of the CPU-baseline sample (default: config-specific)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------------------
+# GPU runners: buffers allocated once, C entry points called directly (no per-step alloc)
+# ---------------------------------------------------------------------------------------
+class Runner:
+    def __init__(self, cfg):
+        import numpy as np
+        import torch
+
+        from iconnx_amd import configs, ops
+        from iconnx_amd._lib import ICX_I8, ICX_U8, check, lib
+
+        self.cfg = cfg
+        self.torch = torch
+        self.L = lib()
+        self.check = check
+        d = configs.make(cfg)
+        self.d = d
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+        self.keep = []
+        if cfg in ("cfg1", "cfg2", "cfg4"):
+            x = d["x"].reshape(-1, d["x"].shape[-1])
+            self.M, self.K = x.shape
+            self.N = d["w"].shape[1]
+            self.x = dev(x)
+            self.w = ops.PackedWeight(dev(d["w"]))
+            self.w_zp = dev(d["w_zp"])
+            self.bzp_len = int(np.asarray(d["w_zp"]).size)
+            self.xq = torch.empty((self.M, self.K), dtype=torch.uint8, device="cuda")
+            self.xs = torch.empty((), dtype=torch.float32, device="cuda")
+            self.xzp = torch.empty((), dtype=torch.uint8, device="cuda")
+            self.rs = torch.empty(self.M, dtype=torch.int32, device="cuda")
+            self.y = torch.empty((self.M, self.N), dtype=torch.float32, device="cuda")
+            self.dql_ws = torch.empty(self.L.icx_dql_workspace_size(self.x.numel()), dtype=torch.uint8, device="cuda")
+            self.gemm_ws = torch.empty(max(1, self.L.icx_matmul_integer_workspace_size(self.M, self.K, self.N, 1)),
+                                       dtype=torch.uint8, device="cuda")
+            epi = [("Mul", (self.xs, dev(d["w_scale"])), False), ("Add", dev(d["bias"]), False)]
+            epi += [(op, dev(c), False) for op, c in d["chain"]]
+            self.chain, k = ops.build_chain(epi, self.M, self.N)
+            self.keep += k
+            self.a_dtype, self.b_dtype = ICX_U8, ICX_I8
+            self.ops_count = 2.0 * self.M * self.N * self.K
+            self.dominant = "gemm_i8_kernel"
+        elif cfg == "cfg5a":
+            self.M, self.K = d["a"].shape
+            self.N = d["b"].shape[1]
+            self.a = dev(d["a"])
+            self.a_zp = dev(d["a_zp"])
+            self.w = ops.PackedWeight(dev(d["b"]))
+            self.w_zp = dev(d["b_zp"])
+            self.bzp_len = 1
+            self.y = torch.empty((self.M, self.N), dtype=torch.float32, device="cuda")
+            self.gemm_ws = torch.empty(max(1, self.L.icx_matmul_integer_workspace_size(self.M, self.K, self.N, 1)),
+                                       dtype=torch.uint8, device="cuda")
+            self.chain, k = ops.build_chain([("Mul", (dev(d["a_scale"]), dev(d["b_scale"])), False)],
+                                            self.M, self.N)
+            self.keep += k
+            self.a_dtype, self.b_dtype = ICX_U8, ICX_I8
+            self.ops_count = 2.0 * self.M * self.N * self.K
+            self.dominant = "gemm_i8_kernel"
+        else:  # cfg5b
+            self.x = dev(d["x"])
+            self.M, self.N = d["x"].shape
+            self.y = torch.empty_like(self.x)
+            self.chain, k = ops.build_chain([(op, dev(c), False) for op, c in d["chain"]], self.M, self.N)
+            self.keep += k
+            self.ops_count = None
+            self.dominant = "chain_vec4_kernel"
+        torch.cuda.synchronize()
+
+    def _p(self, t):
+        return ctypes.c_void_p(t.data_ptr())
+
+    def dql(self, stream):
+        self.check(self.L.icx_dynamic_quantize_linear(
+            stream, self._p(self.x), self.x.numel(), self._p(self.xq), self._p(self.xs),
+            self._p(self.xzp), self._p(self.rs), self.K, self._p(self.dql_ws), self.dql_ws.numel()))
+
+    def gemm(self, stream):
+        if self.cfg == "cfg5a":
+            a, azp, rs = self.a, self.a_zp, None
+        else:
+            a, azp, rs = self.xq, self.xzp, self.rs
+        self.check(self.L.icx_qlinear_f32(
+            stream, self._p(a), self.a_dtype, self._p(self.w.packed), self.b_dtype, 1,
+            self._p(self.w.colsum), self.M, self.K, self.N, self._p(azp), self._p(self.w_zp),
+            self.bzp_len, self._p(rs) if rs is not None else None, ctypes.byref(self.chain),
+            self._p(self.y), self._p(self.gemm_ws), self.gemm_ws.numel()))
+
+    def chain_only(self, stream):
+        self.check(self.L.icx_fused_chain_f32(stream, self._p(self.x), self.M, self.N,
+                                              ctypes.byref(self.chain), self._p(self.y)))
+
+    def step(self, stream):
+        if self.cfg == "cfg5b":
+            self.chain_only(stream)
+        elif self.cfg == "cfg5a":
+            self.gemm(stream)
+        else:
+            self.dql(stream)
+            self.gemm(stream)
+
+    def dominant_launch(self, stream):
+        if self.cfg == "cfg5b":
+            self.chain_only(stream)
+        else:
+            self.gemm(stream)
+
+    def algorithmic_bytes(self):
+        """HBM bytes one launch of the dominant kernel must move at minimum."""
+        import numpy as np
+
+        M, N = self.M, self.N
+        if self.cfg == "cfg5b":
+            return 8.0 * M * N + sum(4.0 * N for _ in self.d["chain"])
+        K = self.K
+        b = M * K + K * N + 4.0 * M * N  # A u8, packed B i8, Y f32
+        b += 4.0 * N  # colsum
+        if self.cfg != "cfg5a":
+            b += 4.0 * M  # row sums from DQL
+            b += 4.0 * N * (1 + len(self.d["chain"])) + 4.0 * N * (self.bzp_len > 1)  # bias, chain, per-col zp
+            b += 4.0 * N if np.size(self.d["w_scale"]) > 1 else 0
+        return b
+
+
+def graph_of(fn, reps, torch):
+    """Capture `reps` calls of fn(stream) into one HIP graph (default-priority stream)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(ctypes.c_void_p(s.cuda_stream))  # warm the path on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for _ in range(reps):
+            fn(h)
+    torch.cuda.synchronize()
+    return g
+
+
+# ---------------------------------------------------------------------------------------
+# CPU baseline: the oracle (single-threaded C restatement of the reference CPU ops)
+# ---------------------------------------------------------------------------------------
+def cpu_baseline(cfg, rows_arg):
+    import numpy as npx
+
+    import oracle
+    from iconnx_amd import configs
+
+    d = configs.make(cfg)
+    t = {}
+    if cfg == "cfg5b":
+        rows = rows_arg or 16384
+        x = d["x"][:rows]
+        t0 = time.perf_counter()
+        y = x
+        for op, c in d["chain"]:
+            y = {"Mul": oracle.mul, "Add": oracle.add, "Div": oracle.div}[op](y, c)
+        dt = time.perf_counter() - t0
+        full = dt * d["x"].shape[0] / rows
+        gbs = 8.0 * d["x"].size / full / 1e9
+        return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": "Mul/Add/Div/Mul op by op on rows [0,%d) of 65536, extrapolated linearly"
+                          " in rows (%.2f s measured)" % (rows, dt)}
+    if cfg == "cfg5a":
+        rows = rows_arg or 16
+        a, b = d["a"], d["b"]
+        M, K = a.shape
+        N = b.shape[1]
+        t0 = time.perf_counter()
+        acc = oracle.matmul_integer(a[:rows], b, d["a_zp"], d["b_zp"])
+        t["MatMulInteger"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        s = oracle.mul(d["a_scale"], d["b_scale"])
+        oracle.mul(oracle.cast_i32_f32(acc), s)
+        t["Cast+Mul"] = time.perf_counter() - t0
+        full = sum(t.values()) * M / rows
+        return {"value": round(2.0 * M * N * K / full / 1e12, 6), "unit": "TOPS", "cores": 1,
+                "kind": "port", "per_op_s": {k: round(v * M / rows, 3) for k, v in t.items()},
+                "sample": "MatMulInteger + Cast + Mul on rows [0,%d) of %d, extrapolated linearly "
+                          "in M (%.2f s measured)" % (rows, M, sum(t.values()))}
+    rows = rows_arg or {"cfg1": 128, "cfg2": 1024, "cfg4": 192}[cfg]
+    x = d["x"].reshape(-1, d["x"].shape[-1])
+    M, K = x.shape
+    N = d["w"].shape[1]
+    rows = min(rows, M)
+    t0 = time.perf_counter()
+    xq, xs, xzp = oracle.dynamic_quantize_linear(x)  # needs the whole tensor (global min/max)
+    t_dql = time.perf_counter() - t0
+    per_col = npx.asarray(d["w_zp"]).ndim == 1
+    t0 = time.perf_counter()
+    acc = oracle.matmul_integer(xq[:rows], d["w"], xzp, d["w_zp"], per_column_b_zp=per_col)
+    t["MatMulInteger"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    c = oracle.cast_i32_f32(acc)
+    t["Cast"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    s = oracle.mul(xs, d["w_scale"])
+    y = oracle.mul(c, s)
+    t["Mul"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    y = oracle.add(y, d["bias"])
+    t["Add"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for op, cc in d["chain"]:
+        y = {"Mul": oracle.mul, "Add": oracle.add, "Div": oracle.div}[op](y, cc)
+    if d["chain"]:
+        t["chain"] = time.perf_counter() - t0
+    scale = M / rows
+    per_op = {"DynamicQuantizeLinear": round(t_dql, 4)}
+    per_op.update({k: round(v * scale, 3) for k, v in t.items()})
+    full = t_dql + sum(t.values()) * scale
+    return {"value": round(2.0 * M * N * K / full / 1e12, 6), "unit": "TOPS", "cores": 1,
+            "kind": "port", "per_op_s": per_op,
+            "sample": "DynamicQuantizeLinear on all %d rows; MatMulInteger + epilogue on rows [0,%d),"
+                      " extrapolated linearly in M (%.2f s measured)" % (M, rows, t_dql + sum(t.values()))}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU only (no multi-GPU path); --gpus %d is not "
+              "supported" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    torch.cuda.set_device(0)
+    r = Runner(args.config)
+    sync = torch.cuda.synchronize
+
+    # ---- timed steps -------------------------------------------------------------------
+    if args.no_graph:
+        run_step = lambda: r.step(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))  # noqa: E731
+    else:
+        g_step = graph_of(r.step, 1, torch)
+        run_step = g_step.replay
+    for _ in range(args.warmup):
+        run_step()
+    sync()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        run_step()
+    ev1.record()
+    sync()
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+
+    # ---- dominant kernel: average launch duration over R back-to-back launches --------
+    reps = args.kernel_reps
+    g_k = graph_of(r.dominant_launch, reps, torch)
+    g_k.replay()
+    sync()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record()
+    g_k.replay()
+    k1.record()
+    sync()
+    k_us = k0.elapsed_time(k1) * 1e3 / reps
+
+    # DQL (two launches) on its own, for the breakdown
+    extra = {}
+    if args.config in ("cfg1", "cfg2", "cfg4"):
+        g_d = graph_of(r.dql, reps, torch)
+        g_d.replay()
+        sync()
+        k0.record()
+        g_d.replay()
+        k1.record()
+        sync()
+        dql_us = k0.elapsed_time(k1) * 1e3 / reps
+        n = r.x.numel()
+        extra["dql_us"] = round(dql_us, 3)
+        extra["dql_algorithmic_GBps"] = round(5.0 * n / (dql_us * 1e-6) / 1e9, 1)
+
+    alg_bytes = r.algorithmic_bytes()
+    if r.ops_count is not None:
+        value = r.ops_count / (ms_step * 1e-3) / 1e12
+        unit = "TOPS"
+    else:
+        value = 8.0 * r.M * r.N / (ms_step * 1e-3) / 1e9
+        unit = "GB/s"
+    if args.config == "cfg5a":
+        ach = r.ops_count / (k_us * 1e-6) / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS,
+                "unit": "TFLOP/s", "op_kind": "int8 ops (2*M*N*K)", "frac": round(ach / PEAK_INT8_TOPS, 4),
+                "traffic": None, "kernel": r.dominant, "kernel_avg_us": round(k_us, 3),
+                "algorithmic_bytes": alg_bytes}
+    else:
+        ach = alg_bytes / (k_us * 1e-6) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": r.dominant,
+                "kernel_avg_us": round(k_us, 3), "algorithmic_bytes": alg_bytes}
+        if r.ops_count is not None:
+            roof["kernel_int8_TOPS"] = round(r.ops_count / (k_us * 1e-6) / 1e12, 2)
+
+    workload = {
+        "cfg1": "cfg1: DQL + quantized linear x[1,128,768] W[768,768] + bias",
+        "cfg2": "cfg2: DQL + MatMulInteger + dequant Mul + bias Add + Mul/Add/Div/Mul chain, "
+                "x[32,128,768] W[768,3072] (DistilBERT-int8 FFN-up shape, b32 s128)",
+        "cfg4": "cfg4: DQL + per-channel quantized linear x[64,384,1024] W[1024,4096]",
+        "cfg5a": "cfg5a: MatMulInteger A u8[16384,4096] x B i8[4096,4096] + fused fp32 dequant",
+        "cfg5b": "cfg5b: fused Mul/Add/Div/Mul chain on f32[65536,768] with [768] operands",
+    }[args.config]
+    cfg = {"workload": workload, "M": r.M, "N": r.N}
+    if hasattr(r, "K"):
+        cfg["K"] = r.K
+    out = {
+        "metric": METRIC, "value": round(value, 4), "unit": unit, "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: seeded N(0,1) activations (SplitMix64 + Box-Muller), random-init int8 weights",
+        "config": cfg, "roofline": roof,
+        "timing": {"graph_replay": not args.no_graph, "wall_s": round(wall, 4), **extra},
+    }
+    if args.config == "cfg5b":
+        out["dtype"] = "f32"
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(args.config, args.cpu_rows)
+        cb["cores"] = 1
+        out["cpu_baseline"] = cb
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,86 @@
+"""ctypes binding of libiconnx_hip.so (the C ABI declared in include/iconnx_hip.h).
+
+The library is built ahead of time (``python -m iconnx_amd.build``).  Loading fails loudly
+when it is missing: there is no fallback implementation anywhere in this package.
+"""
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libiconnx_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "iconnx_hip.h")
+
+ICX_I8, ICX_U8, ICX_I32, ICX_F32 = 0, 1, 2, 3
+OP_ADD, OP_SUB, OP_MUL, OP_DIV = 0, 1, 2, 3
+BCAST_SCALAR, BCAST_COL, BCAST_ROW, BCAST_FULL = 0, 1, 2, 3
+MAX_CHAIN = 8
+
+
+class IconnxError(RuntimeError):
+    """A failed library call (the reference's CudaError::Kernel(String))."""
+
+    def __init__(self, status, message):
+        super().__init__(message)
+        self.status = status
+
+
+class ChainOp(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_int32), ("operand_is_lhs", ctypes.c_int32),
+                ("kind0", ctypes.c_int32), ("kind1", ctypes.c_int32),
+                ("p0", ctypes.c_void_p), ("p1", ctypes.c_void_p)]
+
+
+class Chain(ctypes.Structure):
+    _fields_ = [("n_ops", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("ops", ChainOp * MAX_CHAIN)]
+
+
+_lib = None
+
+P, S, I = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+SIGNATURES = {
+    "icx_status_str": ([I], ctypes.c_char_p),
+    "icx_last_error": ([], ctypes.c_char_p),
+    "icx_version": ([], ctypes.c_char_p),
+    "icx_dql_workspace_size": ([S], S),
+    "icx_dynamic_quantize_linear": ([P, P, S, P, P, P, P, S, P, S], I),
+    "icx_packed_weight_bytes": ([S, S], S),
+    "icx_pack_weight": ([P, P, I, S, S, P, P], I),
+    "icx_matmul_integer_workspace_size": ([S, S, S, I], S),
+    "icx_matmul_integer": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, P, P, S], I),
+    "icx_fused_chain_f32": ([P, P, S, S, ctypes.POINTER(Chain), P], I),
+    "icx_qlinear_f32": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, ctypes.POINTER(Chain), P, P, S], I),
+    "icx_cast_i32_f32": ([P, P, S, P], I),
+    "icx_dequantize_linear_f32": ([P, P, I, P, P, S, S, S, P], I),
+}
+
+
+def header_symbols():
+    """Function names declared in include/iconnx_hip.h."""
+    with open(HEADER) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"\b(icx_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError("libiconnx_hip.so is not built (%s); run `python -m iconnx_amd.build`"
+                          % LIB_PATH)
+    L = ctypes.CDLL(LIB_PATH)
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def check(status):
+    if status != 0:
+        L = lib()
+        msg = L.icx_last_error().decode() or L.icx_status_str(status).decode()
+        raise IconnxError(status, msg)

@@ -1,0 +1,145 @@
+/*
+ * iconnx_hip — MI355X (gfx950) kernels for iconnx's dynamically-quantized linear path.
+ *
+ * C ABI: plain device pointers and sizes, no framework types.  Every compute entry point
+ * enqueues on `stream` and returns an icx_status; nothing synchronises the host unless
+ * stated.  Device pointers are caller-owned.  Scalars that live on the device in the
+ * reference (DQL's y_scale / y_zero_point outputs, MatMulInteger zero points) are device
+ * pointers here too, so a DQL -> MatMulInteger chain never round-trips through the host.
+ *
+ * Each declaration names the reference interface (path:line in ryanoneill/iconnx) whose
+ * role it takes over.  The reference's Rust wrappers would bind these through an
+ * `extern "C"` block (see INTEGRATION.md in this repository).
+ */
+#ifndef ICONNX_HIP_H
+#define ICONNX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* icx_stream_t; /* == hipStream_t */
+
+/* ---- status / errors (mirrors CudaError::Kernel(String), src/cuda/context.rs) ------- */
+typedef enum {
+    ICX_OK = 0,
+    ICX_ERR_INVALID_ARG = 1, /* null pointer, zero-sized where not allowed */
+    ICX_ERR_SHAPE = 2,       /* shape contract violated (K mismatch, zp length, ...) */
+    ICX_ERR_DTYPE = 3,       /* dtype contract violated (non-f32 DQL input, ...) */
+    ICX_ERR_WORKSPACE = 4,   /* workspace missing or smaller than the *_workspace_size */
+    ICX_ERR_HIP = 5,         /* a HIP runtime call failed */
+    ICX_ERR_UNSUPPORTED = 6, /* outside what this build implements */
+} icx_status;
+
+typedef enum { ICX_I8 = 0, ICX_U8 = 1, ICX_I32 = 2, ICX_F32 = 3 } icx_dtype;
+
+const char* icx_status_str(int status);
+/* Message of the last failing call on this host thread ("" if none). */
+const char* icx_last_error(void);
+/* Library / build identification, e.g. "iconnx_hip gfx950 ...". */
+const char* icx_version(void);
+
+/* ---- DynamicQuantizeLinear ------------------------------------------------------------
+ * Replaces gpu_dynamic_quantize_linear (src/cuda/ops/quantize.rs:296-377), which copies x to
+ * the host; semantics of DynamicQuantizeLinear::forward
+ * (src/operators/dynamic_quantize_linear.rs:32-112): min/max over x with 0 included and NaN
+ * skipped, scale = (max-min)/255 and the zero point in f64, y = clamp(rne(x/scale) + zp)
+ * with the division in f64; min == max gives y = 0, scale 0, zp 0.
+ * Outputs y[n] (u8), *y_scale (f32, device), *y_zp (u8, device).
+ * opt_rowsum (nullable): when given, rowsum[r] = sum of y over row r of an [n/row_len,
+ * row_len] view (u8 values summed as int32) — the row term a downstream MatMulInteger
+ * needs for a non-zero b zero point.  row_len must divide n.
+ * ws: device workspace of icx_dql_workspace_size(n) bytes (no initialisation needed). */
+size_t icx_dql_workspace_size(size_t n);
+int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, size_t n, uint8_t* y,
+                                float* y_scale, uint8_t* y_zp, int32_t* opt_rowsum,
+                                size_t row_len, void* ws, size_t ws_bytes);
+
+/* ---- weight packing (once per weight; part of initializer upload in the reference,
+ * src/ir/lowering.rs:292-297) -----------------------------------------------------------
+ * B [K,N] row-major (i8 or u8) -> packed [N,K] i8 (u8 shifted by -128) + colsum[N] of the
+ * packed values.  packed needs icx_packed_weight_bytes(K,N) bytes. */
+size_t icx_packed_weight_bytes(size_t K, size_t N);
+int icx_pack_weight(icx_stream_t stream, const void* B, int b_dtype, size_t K, size_t N,
+                    int8_t* packed, int32_t* colsum);
+
+/* ---- MatMulInteger -------------------------------------------------------------------
+ * Replaces gpu_matmul_integer (src/cuda/ops/quantize.rs:398-615) and its naive kernels
+ * (src/cuda/ops/quantize_kernels.rs:116-194); semantics of MatMulInteger::forward
+ * (src/operators/matmul_integer.rs:52-267): C[m,n] = sum_k (A[m,k]-a_zp)(B[k,n]-b_zp)
+ * in int32 (wrapping).  A [M,K] row-major i8/u8.  B either row-major [K,N]
+ * (b_packed = 0; packed into the workspace on every call) or the output of
+ * icx_pack_weight (b_packed = 1, colsum required).  a_zp: device scalar in A's dtype or
+ * NULL (0).  b_zp: device array in B's dtype of length b_zp_len (1 = per-tensor, as in the
+ * reference; N = per-column, the ONNX form the reference rejects) or NULL.
+ * a_rowsum (nullable): sum of raw A over each row (e.g. from icx_dynamic_quantize_linear);
+ * computed into the workspace when needed and absent.
+ * ws: icx_matmul_integer_workspace_size(...) bytes. */
+size_t icx_matmul_integer_workspace_size(size_t M, size_t K, size_t N, int b_packed);
+int icx_matmul_integer(icx_stream_t stream, const void* A, int a_dtype, const void* B,
+                       int b_dtype, int b_packed, const int32_t* b_colsum, size_t M,
+                       size_t K, size_t N, const void* a_zp, const void* b_zp,
+                       size_t b_zp_len, const int32_t* a_rowsum, int32_t* C, void* ws,
+                       size_t ws_bytes);
+
+/* ---- elementwise epilogue / fused chain -----------------------------------------------
+ * An ordered list of f32 binary ops applied to a running value v, each rounding once,
+ * exactly like separate ONNX Mul/Add/Sub/Div nodes (src/operators/{mul,add,div}.rs):
+ *   v = op(v, operand)   or, with operand_is_lhs, v = op(operand, v).
+ * An operand broadcasts over the [rows, cols] output: a device scalar, a [cols] vector, a
+ * [rows] vector or a full [rows, cols] tensor.  It may be the product of two such factors
+ * (p1 != NULL), rounded once — the Mul(x_scale, w_scale) node feeding the dequant Mul.
+ * Replaces the reference's MulAdd / AddMul / SubMul / DivMul fused kernels
+ * (src/cuda/kernels/fused/mod.rs:290-378, wrappers.rs:495-683) and the unfused
+ * Mul/Add/Div broadcast path (src/cuda/executor/elementwise.rs:54-200), with [cols]
+ * broadcast allowed everywhere (the reference DivMul requires equal shapes). */
+enum { ICX_OP_ADD = 0, ICX_OP_SUB = 1, ICX_OP_MUL = 2, ICX_OP_DIV = 3 };
+enum { ICX_BCAST_SCALAR = 0, ICX_BCAST_COL = 1, ICX_BCAST_ROW = 2, ICX_BCAST_FULL = 3 };
+#define ICX_MAX_CHAIN 8
+
+typedef struct {
+    int32_t op;             /* ICX_OP_* */
+    int32_t operand_is_lhs; /* 1: v = operand op v */
+    int32_t kind0, kind1;   /* ICX_BCAST_* of p0 / p1 */
+    const float* p0;        /* device pointer */
+    const float* p1;        /* optional second factor (device) or NULL */
+} icx_chain_op;
+
+typedef struct {
+    int32_t n_ops; /* 0..ICX_MAX_CHAIN */
+    int32_t reserved;
+    icx_chain_op ops[ICX_MAX_CHAIN];
+} icx_chain;
+
+/* Y[rows,cols] = chain(X).  X and Y may alias. */
+int icx_fused_chain_f32(icx_stream_t stream, const float* X, size_t rows, size_t cols,
+                        const icx_chain* chain, float* Y);
+
+/* Quantized linear with the epilogue fused into the GEMM store:
+ * Y = chain(Cast<float>(MatMulInteger(A, B, a_zp, b_zp))).  Arguments as for
+ * icx_matmul_integer; chain may be NULL (plain Cast). */
+int icx_qlinear_f32(icx_stream_t stream, const void* A, int a_dtype, const void* B,
+                    int b_dtype, int b_packed, const int32_t* b_colsum, size_t M, size_t K,
+                    size_t N, const void* a_zp, const void* b_zp, size_t b_zp_len,
+                    const int32_t* a_rowsum, const icx_chain* chain, float* Y, void* ws,
+                    size_t ws_bytes);
+
+/* Cast INT32 -> FLOAT (src/operators/cast.rs:46-49; GPU src/cuda/ops/cast.rs:134-148). */
+int icx_cast_i32_f32(icx_stream_t stream, const int32_t* x, size_t n, float* y);
+
+/* ---- DequantizeLinear ---------------------------------------------------------------
+ * Replaces gpu_dequantize_linear (src/cuda/ops/quantize.rs:24-267); semantics of the CPU
+ * DequantizeLinear::forward (src/operators/dequantize_linear.rs:32-180):
+ * y = (x as f32 - zp as f32) * scale with the per-axis index (i / inner) % axis_size.
+ * x: i8/u8/i32; zp: same dtype, length axis_size, or NULL. */
+int icx_dequantize_linear_f32(icx_stream_t stream, const void* x, int x_dtype,
+                              const float* scale, const void* zp, size_t n,
+                              size_t axis_size, size_t inner, float* y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ICONNX_HIP_H */

@@ -1,0 +1,56 @@
+"""CPU-side checks of the C ABI: the library loads and exports every declared symbol.
+No compute entry point is called here (there is no GPU in the build container)."""
+import ctypes
+import os
+
+import pytest
+
+from iconnx_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libiconnx_hip.so not built; run `python -m iconnx_amd.build`")
+    return _lib.lib()
+
+
+def test_every_header_symbol_is_exported(L):
+    names = _lib.header_symbols()
+    assert len(names) >= 13
+    for name in names:
+        assert hasattr(L, name), name
+    # and every exported entry point has a ctypes signature
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+
+
+def test_status_strings_and_version(L):
+    assert L.icx_status_str(0) == b"ok"
+    assert L.icx_status_str(4) == b"workspace too small"
+    assert b"gfx950" in L.icx_version()
+    assert L.icx_last_error() == b""
+
+
+def test_chain_struct_layout_matches_header():
+    # icx_chain_op: 4 x int32 + 2 pointers; icx_chain: 2 x int32 + 8 ops
+    assert ctypes.sizeof(_lib.ChainOp) == 32
+    assert ctypes.sizeof(_lib.Chain) == 8 + 8 * 32
+
+
+def test_workspace_queries_are_host_only(L):
+    assert L.icx_dql_workspace_size(1 << 20) >= 8
+    assert L.icx_packed_weight_bytes(768, 3072) == 768 * 3072
+    ws_packed = L.icx_matmul_integer_workspace_size(4096, 768, 3072, 1)
+    ws_raw = L.icx_matmul_integer_workspace_size(4096, 768, 3072, 0)
+    assert ws_raw >= ws_packed + 768 * 3072 + 4 * 3072
+
+
+def test_library_is_gfx950_only():
+    """The shared object carries a gfx950 code object and no other GPU target."""
+    with open(_lib.LIB_PATH, "rb") as f:
+        blob = f.read()
+    assert b"gfx950" in blob
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert other not in blob

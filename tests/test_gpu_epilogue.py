@@ -1,0 +1,190 @@
+"""GPU parity: the fused quantized linear (MatMulInteger + Cast + dequant Mul + bias Add +
+Mul/Add/Div/Mul chain in the GEMM store), the standalone fused chain, Cast and
+DequantizeLinear — against the oracle run op by op in graph order.
+
+The north star's bar for the fp32 outputs is max-abs error <= 1e-5 relative to the output
+magnitude; every op here rounds once in IEEE single precision exactly like the separate
+reference nodes, so the tests assert the stronger bit-exact equality and report the
+relative error when it fails.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from iconnx_amd import configs, ops
+from iconnx_amd._lib import IconnxError
+from tests.golden_util import bits, tensor
+
+pytestmark = pytest.mark.gpu
+REL_TOL = 1e-5  # north-star tolerance for dequantized fp32 outputs
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def assert_f32_equal(got, want, what):
+    if np.array_equal(bits(got), bits(want)):
+        return
+    scale = max(float(np.max(np.abs(want))), 1e-30)
+    err = float(np.max(np.abs(got.astype(np.float64) - want.astype(np.float64)))) / scale
+    n = int(np.count_nonzero(bits(got) != bits(want)))
+    assert err <= REL_TOL, "%s: %d elements differ, max rel err %.3g" % (what, n, err)
+    pytest.fail("%s: %d elements differ in the last bits (max rel err %.3g <= tol)"
+                % (what, n, err))
+
+
+def run_linear_config(cfg, sample_rows):
+    d = configs.make(cfg)
+    x = d["x"].reshape(-1, d["x"].shape[-1])
+    M, K = x.shape
+    xq, xs, xzp, rs = ops.gpu_dynamic_quantize_linear(dev(x), rowsum_row_len=K)
+    w = ops.PackedWeight(dev(d["w"]))
+    epi = [("Mul", (xs, dev(d["w_scale"])), False), ("Add", dev(d["bias"]), False)]
+    epi += [(op, dev(c), False) for op, c in d["chain"]]
+    y = ops.gpu_qlinear(xq, w, xzp, dev(d["w_zp"]), epilogue=epi, a_rowsum=rs)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    chain = [(op, c, False) for op, c in d["chain"]]
+    for r0, r1 in sample_rows(M):
+        ref = oracle.qlinear_graph(x[:, :], d["w"], d["w_zp"], d["w_scale"], d["bias"], chain,
+                                   rows=(r0, r1))
+        assert_f32_equal(y[r0:r1], ref["y"][r0:r1], "%s rows %d:%d" % (cfg, r0, r1))
+    return y
+
+
+def test_cfg1_single_linear_all_rows():
+    run_linear_config("cfg1", lambda M: [(0, M)])
+
+
+def test_cfg2_ffn_up_with_chain():
+    run_linear_config("cfg2", lambda M: [(0, 40), (M // 2, M // 2 + 8), (M - 24, M)])
+
+
+def test_cfg4_per_channel():
+    run_linear_config("cfg4", lambda M: [(0, 16), (M // 3, M // 3 + 8), (M - 16, M)])
+
+
+def test_cfg5a_fused_dequant_full_size():
+    d = configs.make("cfg5a")
+    a, b = d["a"], d["b"]
+    w = ops.PackedWeight(dev(b))
+    epi = [("Mul", (dev(d["a_scale"]), dev(d["b_scale"])), False)]
+    y = ops.gpu_qlinear(dev(a), w, dev(d["a_zp"]), dev(d["b_zp"]), epilogue=epi)
+    acc = ops.gpu_matmul_integer(dev(a), w, dev(d["a_zp"]), dev(d["b_zp"]))
+    torch.cuda.synchronize()
+    acc = acc.cpu().numpy()
+    # accumulators: row sample vs the oracle
+    for r in (0, 4097, 16383):
+        want = oracle.matmul_integer(a[r:r + 1], b, d["a_zp"], d["b_zp"])
+        assert np.array_equal(acc[r:r + 1], want)
+    # epilogue over every element: Cast -> Mul(a_scale * b_scale), via the oracle ops
+    s = oracle.mul(d["a_scale"], d["b_scale"])
+    want = oracle.mul(oracle.cast_i32_f32(acc), s)
+    assert_f32_equal(y.cpu().numpy(), want, "cfg5a epilogue")
+
+
+def test_chain_cfg5b_full_size():
+    d = configs.make("cfg5b")
+    x = d["x"]
+    y = ops.gpu_fused_chain(dev(x), [(op, dev(c), False) for op, c in d["chain"]])
+    torch.cuda.synchronize()
+    want = x
+    for op, c in d["chain"]:
+        want = {"Mul": oracle.mul, "Add": oracle.add, "Div": oracle.div}[op](want, c)
+    assert_f32_equal(y.cpu().numpy(), want, "cfg5b chain")
+
+
+def test_chain_operand_kinds_and_order():
+    rng = np.random.default_rng(2)
+    rows, cols = 37, 45  # not a multiple of 4: scalar kernel
+    for rows, cols in ((37, 45), (64, 256)):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        col = (rng.random(cols) + 0.5).astype(np.float32)
+        row = (rng.random((rows, 1)) + 0.5).astype(np.float32)
+        full = (rng.random((rows, cols)) + 0.5).astype(np.float32)
+        s = np.array(1.75, np.float32)
+        chain = [("Div", col, True), ("Sub", row, False), ("Mul", full, False),
+                 ("Add", s, True), ("Div", (s, col), False), ("Sub", full, True)]
+        y = ops.gpu_fused_chain(dev(x), [(op, tuple(dev(t) for t in c) if isinstance(c, tuple)
+                                          else dev(c), lhs) for op, c, lhs in chain])
+        want = x
+        for op, c, lhs in chain:
+            c = oracle.mul(*c) if isinstance(c, tuple) else c
+            f = {"Mul": oracle.mul, "Add": oracle.add, "Div": oracle.div, "Sub": oracle.sub}[op]
+            want = f(c, want) if lhs else f(want, c)
+        assert_f32_equal(y.cpu().numpy(), want, "chain %dx%d" % (rows, cols))
+
+
+def test_fused_pattern_wrappers(goldens):
+    """MulAdd / AddMul / SubMul / DivMul: same-shape and [last-dim] broadcast, and the
+    ONNX *_bcast goldens through the single-op binary path."""
+    rng = np.random.default_rng(8)
+    a = rng.standard_normal((3, 4, 5)).astype(np.float32)
+    b = (rng.random(5) + 0.5).astype(np.float32)
+    c = rng.standard_normal(5).astype(np.float32)
+    cases = [(ops.gpu_fused_mul_add, lambda: oracle.add(oracle.mul(a, b), c)),
+             (ops.gpu_fused_add_mul, lambda: oracle.mul(oracle.add(a, b), c)),
+             (ops.gpu_fused_sub_mul, lambda: oracle.mul(oracle.sub(a, b), c)),
+             (ops.gpu_fused_div_mul, lambda: oracle.mul(oracle.div(a, b), c))]
+    for fn, ref in cases:
+        assert_f32_equal(fn(dev(a), dev(b), dev(c)).cpu().numpy(), ref(), fn.__name__)
+        bf, cf = np.broadcast_to(b, a.shape).copy(), np.broadcast_to(c, a.shape).copy()
+        assert_f32_equal(fn(dev(a), dev(bf), dev(cf)).cpu().numpy(), ref(), fn.__name__ + " same")
+    for case, name in (("test_mul_bcast", "Mul"), ("test_add_bcast", "Add"),
+                       ("test_div_bcast", "Div"), ("test_mul", "Mul"), ("test_div", "Div")):
+        g = goldens[case]
+        x0, x1 = (tensor(t) for t in g["inputs"])
+        got = ops.gpu_binary(name, dev(x0), dev(x1)).cpu().numpy()
+        assert_f32_equal(got, tensor(g["outputs"][0]), case)
+
+
+def test_div_ieee_special_values():
+    a = np.array([0.0, 0.0, 1.0, 6.0, -8.0, 10.0], np.float32)
+    b = np.array([0.0, 1e-12, 0.0, 2.0, 4.0, -5.0], np.float32)
+    got = ops.gpu_binary("Div", dev(a), dev(b)).cpu().numpy()
+    assert np.isnan(got[0]) and got[1] == 0.0 and got[2] == np.inf
+    assert got[3:].tolist() == [3.0, -2.0, -2.0]
+
+
+def test_cast_i32_f32():
+    x = np.array([0, 1, -7, 2**24 + 1, 2**24 + 3, -(2**31), 2**31 - 1, 67108865], np.int32)
+    rng = np.random.default_rng(1)
+    x = np.concatenate([x, rng.integers(-2**31, 2**31 - 1, 100000).astype(np.int32)])
+    got = ops.gpu_cast_i32_f32(dev(x)).cpu().numpy()
+    np.testing.assert_array_equal(bits(got), bits(oracle.cast_i32_f32(x)))
+
+
+@pytest.mark.parametrize("case", ["test_dequantizelinear", "test_dequantizelinear_axis"])
+def test_dequantize_goldens(goldens, case):
+    g = goldens[case]
+    x, s, zp = (tensor(t) for t in g["inputs"])
+    got = ops.gpu_dequantize_linear(dev(x), dev(s), dev(zp), axis=g["attributes"].get("axis", 1))
+    np.testing.assert_array_equal(bits(got.cpu().numpy()), bits(tensor(g["outputs"][0])))
+
+
+def test_dequantize_reference_literals(literals):
+    from tests.golden_util import NP
+    for lit in literals["dequantize_linear"]:
+        x = np.array(lit["x"], NP[lit["x_dtype"]]).reshape(lit["x_shape"])
+        s = np.array(lit["scale"], np.float32).reshape(lit["scale_shape"])
+        zp = np.array(lit["zp"], NP[lit["x_dtype"]]).reshape(lit["scale_shape"]) if "zp" in lit else None
+        axis = lit.get("axis", 1)
+        got = ops.gpu_dequantize_linear(dev(x), dev(s), None if zp is None else dev(zp), axis)
+        want = oracle.dequantize_linear(x, s, zp, axis)
+        np.testing.assert_array_equal(bits(got.cpu().numpy()), bits(want))
+    for lit in literals["dequantize_linear_rejects"]:
+        x = np.array(lit["x"], NP[lit["x_dtype"]]).reshape(lit["x_shape"])
+        s = np.array(lit["scale"], np.float32).reshape(lit["scale_shape"])
+        zp = np.array(lit["zp"], NP[lit["zp_dtype"]]).reshape(lit["zp_shape"])
+        with pytest.raises(IconnxError):
+            ops.gpu_dequantize_linear(dev(x), dev(s), dev(zp))
+
+
+def test_dequantize_i32_large_values_follow_cpu_semantics():
+    x = np.array([2**24 + 1, 2**25 + 3, -5, 123456789], np.int32)
+    zp = np.array(1, np.int32)
+    s = np.array(0.5, np.float32)
+    got = ops.gpu_dequantize_linear(dev(x), dev(s), dev(zp)).cpu().numpy()
+    np.testing.assert_array_equal(bits(got), bits(oracle.dequantize_linear(x, s, zp)))
