@@ -110,7 +110,7 @@ class Runner:
             self.chain, k = ops.build_chain([(op, dev(c), False) for op, c in d["chain"]], self.M, self.N)
             self.keep += k
             self.ops_count = None
-            self.dominant = "chain_vec4_kernel"
+            self.dominant = "chain_cols_kernel"
         torch.cuda.synchronize()
 
     def _p(self, t):

@@ -2,9 +2,19 @@
 // rounding each (explicit *_rn intrinsics, and the library is built with
 // -ffp-contract=off), matching separate ONNX Mul / Add / Sub / Div nodes evaluated one at a
 // time (src/operators/{mul,add,div}.rs).
+//
+// Two evaluation forms:
+//  * apply_chain      — general: every operand fetched per element (any broadcast kind);
+//  * load_col_operands + apply_loaded — when every factor is a scalar or a [cols] vector
+//    (the dequant-scale / bias / per-channel chain case): the operands of one column are
+//    fetched once, as independent loads issued together, and the per-element work is pure
+//    arithmetic.  Loops run over the fixed ICX_MAX_CHAIN bound with predication so the
+//    operand array stays in registers.
 #pragma once
 
 #include "icx_common.hpp"
+
+#include <cstdint>
 
 namespace icx {
 
@@ -34,14 +44,94 @@ __device__ __forceinline__ float apply_binary(int op, float lhs, float rhs) {
     }
 }
 
+__device__ __forceinline__ float apply_one(const icx_chain_op& op, float v, float o) {
+    return op.operand_is_lhs ? apply_binary(op.op, o, v) : apply_binary(op.op, v, o);
+}
+
 __device__ __forceinline__ float apply_chain(const icx_chain& ch, float v, size_t r, size_t c,
                                              size_t cols) {
-    for (int i = 0; i < ch.n_ops; ++i) {
-        const icx_chain_op& op = ch.ops[i];
-        const float o = chain_operand(op, r, c, cols);
-        v = op.operand_is_lhs ? apply_binary(op.op, o, v) : apply_binary(op.op, v, o);
-    }
+#pragma unroll
+    for (int i = 0; i < ICX_MAX_CHAIN; ++i)
+        if (i < ch.n_ops) v = apply_one(ch.ops[i], v, chain_operand(ch.ops[i], r, c, cols));
     return v;
+}
+
+// Column-only chains: operands of column c (scalar or [cols] factors).
+__device__ __forceinline__ float col_factor(const float* p, int kind, size_t c) {
+    return kind == ICX_BCAST_SCALAR ? p[0] : p[c];
+}
+
+__device__ __forceinline__ void load_col_operands(const icx_chain& ch, size_t c,
+                                                  float (&o)[ICX_MAX_CHAIN]) {
+#pragma unroll
+    for (int i = 0; i < ICX_MAX_CHAIN; ++i) {
+        if (i < ch.n_ops) {
+            const icx_chain_op& op = ch.ops[i];
+            float a = col_factor(op.p0, op.kind0, c);
+            if (op.p1) a = __fmul_rn(a, col_factor(op.p1, op.kind1, c));
+            o[i] = a;
+        } else {
+            o[i] = 0.0f;
+        }
+    }
+}
+
+__device__ __forceinline__ float apply_loaded(const icx_chain& ch, float v,
+                                              const float (&o)[ICX_MAX_CHAIN]) {
+#pragma unroll
+    for (int i = 0; i < ICX_MAX_CHAIN; ++i)
+        if (i < ch.n_ops) v = apply_one(ch.ops[i], v, o[i]);
+    return v;
+}
+
+// ---- op-major evaluation over a register block of float4 values ------------------------
+// The op codes of a chain packed 4 bits per op: bits [1:0] = ICX_OP_*, bit 2 = operand on
+// the left.  One uniform switch per op, then straight-line IEEE ops over every value the
+// lane holds — no per-element branching.  `opnd(k)` returns the float4 operand of op k for
+// the lane's 4 columns.
+__host__ __device__ inline uint32_t chain_codes(const icx_chain& ch) {
+    uint32_t c = 0;
+    for (int i = 0; i < ch.n_ops; ++i)
+        c |= (uint32_t)((ch.ops[i].op & 3) | (ch.ops[i].operand_is_lhs ? 4 : 0)) << (4 * i);
+    return c;
+}
+
+#define ICX_EW4(expr)                                   \
+    _Pragma("unroll") for (int u = 0; u < NV; ++u) {    \
+        { float& x = v[u].x; const float y = o.x; x = (expr); } \
+        { float& x = v[u].y; const float y = o.y; x = (expr); } \
+        { float& x = v[u].z; const float y = o.z; x = (expr); } \
+        { float& x = v[u].w; const float y = o.w; x = (expr); } \
+    }
+
+template <int NV, typename OpndFn>
+__device__ __forceinline__ void run_chain4(uint32_t codes, int n_ops, float4 (&v)[NV],
+                                           OpndFn opnd) {
+#pragma unroll 1
+    for (int k = 0; k < n_ops; ++k) {
+        const float4 o = opnd(k);
+        switch ((codes >> (4 * k)) & 7u) {
+            case ICX_OP_ADD: ICX_EW4(__fadd_rn(x, y)) break;
+            case ICX_OP_ADD | 4: ICX_EW4(__fadd_rn(y, x)) break;
+            case ICX_OP_SUB: ICX_EW4(__fsub_rn(x, y)) break;
+            case ICX_OP_SUB | 4: ICX_EW4(__fsub_rn(y, x)) break;
+            case ICX_OP_MUL: ICX_EW4(__fmul_rn(x, y)) break;
+            case ICX_OP_MUL | 4: ICX_EW4(__fmul_rn(y, x)) break;
+            case ICX_OP_DIV: ICX_EW4(__fdiv_rn(x, y)) break;
+            default: ICX_EW4(__fdiv_rn(y, x)) break;
+        }
+    }
+}
+#undef ICX_EW4
+
+// Host side: true when every operand factor is a scalar or a [cols] vector.
+inline bool chain_is_col_only(const icx_chain& ch) {
+    for (int i = 0; i < ch.n_ops; ++i) {
+        const icx_chain_op& o = ch.ops[i];
+        if (o.kind0 != ICX_BCAST_SCALAR && o.kind0 != ICX_BCAST_COL) return false;
+        if (o.p1 && o.kind1 != ICX_BCAST_SCALAR && o.kind1 != ICX_BCAST_COL) return false;
+    }
+    return true;
 }
 
 // Host-side validation shared by every entry point taking a chain.

@@ -203,6 +203,7 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
         if (vec) {
             const float4* x4 = reinterpret_cast<const float4*>(xr);
             uint32_t* y4 = reinterpret_cast<uint32_t*>(yr);
+#pragma unroll 4
             for (size_t i = lane; i < row_len / 4; i += 64) {
                 uint32_t q = p.zero ? 0u : quant4(x4[i], p);
                 y4[i] = q;
@@ -242,7 +243,7 @@ extern "C" int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, 
     float2* part = reinterpret_cast<float2*>(ws);
     const int vec = icx::aligned16(x) ? 1 : 0;
     // Launch 1: enough blocks for ~16 float4 per lane, capped at kMaxPartials.
-    int G = (int)std::min<size_t>(kMaxPartials, std::max<size_t>(1, icx::cdiv(n, (size_t)kThreads * 64)));
+    int G = (int)std::min<size_t>(kMaxPartials, std::max<size_t>(1, icx::cdiv(n, (size_t)kThreads * 16)));
     hipLaunchKernelGGL(dql_minmax_kernel, dim3(G), dim3(kThreads), 0, s, x, n, vec, part);
     ICX_LAUNCH_CHECK("dql_minmax_kernel");
     if (opt_rowsum) {

@@ -1,5 +1,6 @@
 // HBM-bound elementwise kernels: the standalone fused chain, Cast INT32 -> FLOAT and
 // DequantizeLinear, plus the library's error / version plumbing.
+#include <algorithm>
 #include <cstring>
 
 #include "chain.hpp"
@@ -39,24 +40,44 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// rows x cols, cols % 4 == 0, 16-byte aligned X / Y: one float4 per lane per step, four
-// steps in flight.  Column operands are read through L1/L2 (a few KB, reused by every row).
+// rows x cols with cols % 4 == 0 and 16-byte aligned X / Y.  The grid stride (in float4)
+// is a multiple of cols / 4, so each thread always works on the same 4 columns: their
+// chain operands are computed once into a thread-private LDS slot, and each step is four
+// float4 loads in flight, the chain applied op by op (one uniform branch per op, straight
+// IEEE arithmetic over the 16 values) and four float4 stores.
 __global__ void __launch_bounds__(kThreads)
-chain_vec4_kernel(const float4* __restrict__ X, uint32_t n4, uint32_t cols4, size_t cols,
-                  icx_chain ch, float4* __restrict__ Y) {
+chain_cols_kernel(const float4* __restrict__ X, uint32_t n4, uint32_t cols4, icx_chain ch,
+                  uint32_t codes, float4* __restrict__ Y) {
+    __shared__ float4 sop[ICX_MAX_CHAIN][kThreads];
+    const uint32_t i0 = blockIdx.x * kThreads + threadIdx.x;
     const uint32_t stride = gridDim.x * kThreads;
-    for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
-        const uint32_t r = i / cols4;
-        const size_t c = (size_t)(i - r * cols4) * 4;
-        float4 v = X[i];
-        v.x = icx::apply_chain(ch, v.x, r, c + 0, cols);
-        v.y = icx::apply_chain(ch, v.y, r, c + 1, cols);
-        v.z = icx::apply_chain(ch, v.z, r, c + 2, cols);
-        v.w = icx::apply_chain(ch, v.w, r, c + 3, cols);
-        Y[i] = v;
+    const size_t c = (size_t)(i0 % cols4) * 4;
+    {
+        float o[4][ICX_MAX_CHAIN];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) icx::load_col_operands(ch, c + e, o[e]);
+#pragma unroll
+        for (int k = 0; k < ICX_MAX_CHAIN; ++k)
+            if (k < ch.n_ops) sop[k][threadIdx.x] = make_float4(o[0][k], o[1][k], o[2][k], o[3][k]);
+    }
+    auto opnd = [&](int k) { return sop[k][threadIdx.x]; };
+    uint32_t i = i0;
+    for (; i + 3 * stride < n4; i += 4 * stride) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = X[i + u * stride];
+        icx::run_chain4(codes, ch.n_ops, v, opnd);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) Y[i + u * stride] = v[u];
+    }
+    for (; i < n4; i += stride) {
+        float4 v[1] = {X[i]};
+        icx::run_chain4(codes, ch.n_ops, v, opnd);
+        Y[i] = v[0];
     }
 }
 
+// General layout: every operand fetched per element.
 __global__ void __launch_bounds__(kThreads)
 chain_scalar_kernel(const float* __restrict__ X, size_t n, size_t cols, icx_chain ch,
                     float* __restrict__ Y) {
@@ -112,7 +133,7 @@ extern "C" const char* icx_status_str(int status) {
 extern "C" const char* icx_last_error(void) { return icx::g_err; }
 
 extern "C" const char* icx_version(void) {
-    return "iconnx_hip 0.1 gfx950 (int8 MFMA 32x32x32, LDS double-buffered)";
+    return "iconnx_hip 0.2 gfx950 (int8 MFMA 32x32x32, LDS-DMA multistage)";
 }
 
 extern "C" int icx_fused_chain_f32(icx_stream_t stream, const float* X, size_t rows,
@@ -124,12 +145,18 @@ extern "C" int icx_fused_chain_f32(icx_stream_t stream, const float* X, size_t r
     const size_t n = rows * cols;
     if (n == 0) return ICX_OK;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (cols % 4 == 0 && icx::aligned16(X) && icx::aligned16(Y) && n / 4 < 0xffffffffull) {
-        const uint32_t n4 = (uint32_t)(n / 4);
-        hipLaunchKernelGGL(chain_vec4_kernel, dim3(grid_for(n4, kThreads * 4, 8192)), dim3(kThreads),
-                           0, s, reinterpret_cast<const float4*>(X), n4, (uint32_t)(cols / 4), cols,
-                           *chain, reinterpret_cast<float4*>(Y));
-        ICX_LAUNCH_CHECK("chain_vec4_kernel");
+    const size_t cols4 = cols / 4;
+    // grid: a multiple of lcm(256, cols4) threads so the stride keeps each thread's columns
+    size_t g = 1, a = kThreads, bq = cols4;
+    while (bq) { size_t tt = a % bq; a = bq; bq = tt; }  // a = gcd(256, cols4)
+    const size_t unit_blocks = cols4 ? cols4 / a : 1;    // lcm(256, cols4) / 256
+    if (cols4) g = std::max<size_t>(1, 2048 / unit_blocks) * unit_blocks;
+    if (cols % 4 == 0 && cols4 > 0 && icx::aligned16(X) && icx::aligned16(Y) &&
+        n / 4 < 0x7fffffffull && icx::chain_is_col_only(*chain) && unit_blocks <= 8192) {
+        hipLaunchKernelGGL(chain_cols_kernel, dim3((unsigned)g), dim3(kThreads), 0, s,
+                           reinterpret_cast<const float4*>(X), (uint32_t)(n / 4), (uint32_t)cols4,
+                           *chain, icx::chain_codes(*chain), reinterpret_cast<float4*>(Y));
+        ICX_LAUNCH_CHECK("chain_cols_kernel");
     } else {
         hipLaunchKernelGGL(chain_scalar_kernel, dim3(grid_for(n, kThreads * 4, 8192)), dim3(kThreads),
                            0, s, X, n, cols, *chain, Y);

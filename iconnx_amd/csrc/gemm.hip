@@ -18,10 +18,12 @@
 // shape: the kernel is an "NT" GEMM whose 16-byte global loads and 16-byte LDS fragment
 // reads are all contiguous.
 //
-// Tiling (v1): 256 threads = 4 waves (2x2), block tile 128x128, K step 64, LDS double
-// buffered (2 x 2 x 128 x 80 B = 40 KB, rows padded by 16 B), each wave a 64x64 sub-tile
-// of 2x2 v_mfma_i32_32x32x32_i8.  Blocks are remapped so each XCD (blockIdx % 8) works on
-// a contiguous, M-grouped range of tiles that shares A/B panels in its own L2.
+// Tiling: 256 threads = 4 waves (2x2), K step 64, LDS double buffered with rows padded by
+// 16 B.  Two block tiles: 128x128 (wave 64x64 = 2x2 v_mfma_i32_32x32x32_i8, 40 KB LDS) for
+// shapes with few tiles, and 256x256 (wave 128x128 = 4x4 MFMA tiles, accumulators in
+// AGPRs, 80 KB LDS) for large ones, where the bigger wave tile halves the LDS bytes read
+// per MFMA.  Blocks are remapped so each XCD (blockIdx % 8) works on a contiguous,
+// M-grouped range of tiles that shares A/B panels in its own L2.
 #include "chain.hpp"
 
 namespace {
@@ -30,7 +32,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
-constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BK = 64;
 constexpr int LDS_STRIDE = BK + 16;  // bytes per LDS row (padding against bank conflicts)
 constexpr int GROUP_M = 8;
 
@@ -49,6 +51,7 @@ struct GemmArgs {
     uint32_t a_xor;  // 0x80808080 when A is u8
     int alpha, beta;
     int a_zp_u8, b_zp_u8, b_zp_len;
+    uint32_t codes;  // icx::chain_codes(chain)
     icx_chain chain;
 };
 
@@ -58,38 +61,45 @@ __device__ __forceinline__ int load_zp(const void* p, int is_u8, int idx) {
                  : (int)reinterpret_cast<const int8_t*>(p)[idx];
 }
 
-// 16 bytes of row `row` starting at column `k` of a [rows, K] byte matrix; zero outside.
+// 16 bytes of row `row` starting at column `k` of a [rows, K] byte matrix.  Branch-free
+// for VEC (K % 16 == 0, so K >= 16): the address is clamped into the matrix and `keep`
+// records whether the chunk is real, so every load of a K step stays in flight; the shift
+// and the zeroing of out-of-range chunks happen in fix16() when the chunk is written to
+// LDS, after the MFMAs of the current step.
 template <bool VEC>
 __device__ __forceinline__ uint4 load16(const int8_t* base, int rows, int K, int row, int k,
-                                        uint32_t xr) {
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (row >= rows) return v;
-    const int8_t* p = base + (size_t)row * K + k;
+                                        uint32_t xr, uint32_t& keep) {
     if (VEC) {
-        if (k < K) {
-            v = *reinterpret_cast<const uint4*>(p);
-            v.x ^= xr; v.y ^= xr; v.z ^= xr; v.w ^= xr;
-        }
+        keep = (row < rows && k < K) ? 0xFFFFFFFFu : 0u;
+        const int8_t* p = base + (size_t)min(row, rows - 1) * K + min(k, K - 16);
+        return *reinterpret_cast<const uint4*>(p);
     } else {
+        keep = 0xFFFFFFFFu;
         uint32_t w[4] = {0, 0, 0, 0};
+        if (row < rows) {
+            const int8_t* p = base + (size_t)row * K;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            if (k + j < K) {
-                uint32_t b = (uint8_t)p[j] ^ (xr & 0xFFu);
-                w[j >> 2] |= b << (8 * (j & 3));
+            for (int j = 0; j < 16; ++j) {
+                if (k + j < K) {
+                    uint32_t b = (uint8_t)p[k + j] ^ (xr & 0xFFu);
+                    w[j >> 2] |= b << (8 * (j & 3));
+                }
             }
         }
-        v = make_uint4(w[0], w[1], w[2], w[3]);
+        return make_uint4(w[0], w[1], w[2], w[3]);
     }
-    return v;
 }
 
-template <bool VEC, int OUT>
-__global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * LDS_STRIDE];
-    __shared__ __attribute__((aligned(16))) int8_t sB[2][BN * LDS_STRIDE];
+template <bool VEC>
+__device__ __forceinline__ uint4 fix16(uint4 v, uint32_t xr, uint32_t keep) {
+    if (!VEC) return v;  // already shifted and zero-filled
+    return make_uint4((v.x ^ xr) & keep, (v.y ^ xr) & keep, (v.z ^ xr) & keep, (v.w ^ xr) & keep);
+}
 
-    // ---- tile assignment: XCD-contiguous, then GROUP_M-grouped ------------------------
+// Logical tile of this block: XCD-contiguous, then GROUP_M-grouped.  The hardware places
+// workgroup i on XCD i % 8; remapping gives each XCD a contiguous run of tiles, and the
+// grouping makes consecutive tiles share A row panels, so panels stay in that XCD's L2.
+__device__ __forceinline__ void tile_coords(const GemmArgs& g, int& tm, int& tn) {
     int bid = blockIdx.x;
     const int nb = gridDim.x;
     if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
@@ -98,38 +108,182 @@ __global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
     const int first_m = group * GROUP_M;
     const int gsz = min(g.tiles_m - first_m, GROUP_M);
     const int in_group = bid - group * per_group;
-    const int tm = first_m + in_group % gsz;
-    const int tn = in_group / gsz;
-    const int m0 = tm * BM, n0 = tn * BN;
+    tm = first_m + in_group % gsz;
+    tn = in_group / gsz;
+}
 
+template <int BM, int BN>
+struct EpiLayout {
+    static constexpr int WN = BN / 2;
+    static constexpr int SROW = WN + 8;  // floats per staged row (4-row offset = 32 banks)
+    static constexpr int STAGE_BYTES = 4 * 32 * SROW * 4;
+    static constexpr int BYTES = STAGE_BYTES + ICX_MAX_CHAIN * BN * 4;  // + column operands
+};
+
+// ---- epilogue ---------------------------------------------------------------------------
+// Each wave stages one 32-row slab of its sub-tile at a time through LDS: the MFMA layout
+// (lane = column, registers = rows) is written with the zero-point correction and the Cast
+// applied, then read back row-major as float4 / int4 so that the chain runs on 4
+// consecutive columns per lane with its column operands in LDS, and the global stores are
+// 16-byte and contiguous along rows.  `smem` must not be in use by the main loop any more.
+template <int BM, int BN, int OUT, bool COLCHAIN>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, v16i (&acc)[BM / 64][BN / 64],
+                                              int8_t* smem, int m0, int n0) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TI = WM / 32, TJ = WN / 32;
+    using EL = EpiLayout<BM, BN>;
+    constexpr int SROW = EL::SROW;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wid = t >> 6;
+    const int wm = wid >> 1, wn = wid & 1;
+    const int lr = lane & 31;
+
+    const int azp = load_zp(g.a_zp, g.a_zp_u8, 0);
+    const uint32_t amz = (uint32_t)(g.alpha - azp);
+    const uint32_t aK = (uint32_t)g.alpha * (uint32_t)g.K;
+    uint32_t colterm[TJ], colfac[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = min(n0 + wn * WN + j * 32 + lr, g.N - 1);
+        const int bzp = load_zp(g.b_zp, g.b_zp_u8, g.b_zp_len == 1 ? 0 : col);
+        colfac[j] = (uint32_t)(g.beta - bzp);
+        colterm[j] = amz * (uint32_t)g.colsum[col] + (uint32_t)g.K * amz * colfac[j];
+    }
+    constexpr int LPR = WN / 4;       // lanes per staged row in the read phase
+    constexpr int RPI = 64 / LPR;     // rows per read iteration
+    const int cc = (lane % LPR) * 4;  // this lane's 4 columns within the wave tile
+    const int rsub = lane / LPR;
+    const int gcol = n0 + wn * WN + cc;
+    float* sop = reinterpret_cast<float*>(smem + EL::STAGE_BYTES);
+    if (OUT == OUT_F32 && COLCHAIN) {
+#pragma unroll
+        for (int k = 0; k < ICX_MAX_CHAIN; ++k) {
+            if (k < g.chain.n_ops) {
+                const icx_chain_op& op = g.chain.ops[k];
+                for (int c = t; c < BN; c += kThreads) {
+                    const int col = min(n0 + c, g.N - 1);
+                    float a = icx::col_factor(op.p0, op.kind0, col);
+                    if (op.p1) a = __fmul_rn(a, icx::col_factor(op.p1, op.kind1, col));
+                    sop[k * BN + c] = a;
+                }
+            }
+        }
+    }
+    const bool vec_out = (g.N % 4 == 0) && ((reinterpret_cast<uintptr_t>(g.C) & 15u) == 0);
+    float* stage = reinterpret_cast<float*>(smem) + wid * 32 * SROW;
+
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const int rbase = m0 + wm * WM + i * 32;
+        uint32_t rterm[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = min(rbase + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), g.M - 1);
+            rterm[r] = g.rowsum_raw ? (uint32_t)g.rowsum_raw[row] - aK : 0u;
+        }
+        __syncthreads();  // previous slab read back; column operands written
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int lrow = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const uint32_t v = (uint32_t)acc[i][j][r] + colterm[j] + colfac[j] * rterm[r];
+                float* dst = &stage[lrow * SROW + j * 32 + lr];
+                if (OUT == OUT_I32) *reinterpret_cast<int32_t*>(dst) = (int32_t)v;
+                else *dst = (float)(int32_t)v;  // Cast INT32 -> FLOAT, round to nearest even
+            }
+        }
+        __syncthreads();
+        constexpr int NQ = 32 / RPI;  // float4 values per lane in this slab
+        float4 v[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+            v[q] = *reinterpret_cast<const float4*>(&stage[(q * RPI + rsub) * SROW + cc]);
+        if (OUT == OUT_F32) {
+            if (COLCHAIN) {
+                icx::run_chain4(g.codes, g.chain.n_ops, v, [&](int k) {
+                    return *reinterpret_cast<const float4*>(&sop[k * BN + wn * WN + cc]);
+                });
+            } else {
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) {
+                    const int grow = min(rbase + q * RPI + rsub, g.M - 1);
+                    float* w = reinterpret_cast<float*>(&v[q]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        w[e] = icx::apply_chain(g.chain, w[e], grow, min(gcol + e, g.N - 1), g.N);
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int grow = rbase + q * RPI + rsub;
+            if (grow >= g.M || gcol >= g.N) continue;
+            const size_t off = (size_t)grow * g.N + gcol;
+            if (vec_out && gcol + 3 < g.N) {
+                *reinterpret_cast<float4*>(reinterpret_cast<float*>(g.C) + off) = v[q];
+            } else {
+                const float* w = reinterpret_cast<const float*>(&v[q]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (gcol + e < g.N) reinterpret_cast<float*>(g.C)[off + e] = w[e];
+            }
+        }
+    }
+}
+
+// ---- main loop A: register-staged (any K, any alignment) -------------------------------
+// Block tile BM x BN, 4 waves in 2x2, each wave a (BM/2) x (BN/2) sub-tile made of
+// TI x TJ v_mfma_i32_32x32x32_i8 tiles; two LDS stages with rows padded by 16 B.
+template <int BM, int BN, bool VEC, int OUT, bool COLCHAIN>
+__global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TI = WM / 32, TJ = WN / 32;
+    constexpr int AQ = BM * BK / 16 / kThreads;  // 16-byte chunks per thread per stage
+    constexpr int BQ = BN * BK / 16 / kThreads;
+    constexpr int TILE_BYTES = 2 * (BM + BN) * LDS_STRIDE;
+    constexpr int EPI_BYTES = EpiLayout<BM, BN>::BYTES;
+    __shared__ __attribute__((aligned(16)))
+        int8_t smem[TILE_BYTES > EPI_BYTES ? TILE_BYTES : EPI_BYTES];
+    int8_t (*sA)[BM * LDS_STRIDE] = reinterpret_cast<int8_t (*)[BM * LDS_STRIDE]>(smem);
+    int8_t (*sB)[BN * LDS_STRIDE] =
+        reinterpret_cast<int8_t (*)[BN * LDS_STRIDE]>(smem + 2 * BM * LDS_STRIDE);
+
+    int tm, tn;
+    tile_coords(g, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
     const int t = threadIdx.x;
     const int lane = t & 63, wid = t >> 6;
     const int wm = wid >> 1, wn = wid & 1;
     const int lr = lane & 31, lk = (lane >> 5) * 16;
+    const int crow = t >> 2, ccol = (t & 3) * 16;  // this thread's chunk: row crow + 64q
 
-    // global -> register staging: 2 chunks of 16 B per operand per thread
-    const int r0 = t >> 2, c0 = (t & 3) * 16;  // chunk t
-    const int r1 = r0 + 64;                     // chunk t + 256
-    uint4 ra0, ra1, rb0, rb1;
-
+    uint4 ra[AQ], rb[BQ];
+    uint32_t ka[AQ], kb[BQ];
     auto gload = [&](int k0) {
-        ra0 = load16<VEC>(g.A, g.M, g.K, m0 + r0, k0 + c0, g.a_xor);
-        ra1 = load16<VEC>(g.A, g.M, g.K, m0 + r1, k0 + c0, g.a_xor);
-        rb0 = load16<VEC>(g.Bp, g.N, g.K, n0 + r0, k0 + c0, 0u);
-        rb1 = load16<VEC>(g.Bp, g.N, g.K, n0 + r1, k0 + c0, 0u);
+#pragma unroll
+        for (int q = 0; q < AQ; ++q)
+            ra[q] = load16<VEC>(g.A, g.M, g.K, m0 + crow + 64 * q, k0 + ccol, g.a_xor, ka[q]);
+#pragma unroll
+        for (int q = 0; q < BQ; ++q)
+            rb[q] = load16<VEC>(g.Bp, g.N, g.K, n0 + crow + 64 * q, k0 + ccol, 0u, kb[q]);
     };
     auto sstore = [&](int st) {
-        *reinterpret_cast<uint4*>(&sA[st][r0 * LDS_STRIDE + c0]) = ra0;
-        *reinterpret_cast<uint4*>(&sA[st][r1 * LDS_STRIDE + c0]) = ra1;
-        *reinterpret_cast<uint4*>(&sB[st][r0 * LDS_STRIDE + c0]) = rb0;
-        *reinterpret_cast<uint4*>(&sB[st][r1 * LDS_STRIDE + c0]) = rb1;
+#pragma unroll
+        for (int q = 0; q < AQ; ++q)
+            *reinterpret_cast<uint4*>(&sA[st][(crow + 64 * q) * LDS_STRIDE + ccol]) =
+                fix16<VEC>(ra[q], g.a_xor, ka[q]);
+#pragma unroll
+        for (int q = 0; q < BQ; ++q)
+            *reinterpret_cast<uint4*>(&sB[st][(crow + 64 * q) * LDS_STRIDE + ccol]) =
+                fix16<VEC>(rb[q], 0u, kb[q]);
     };
 
-    v16i acc[2][2];
+    v16i acc[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
@@ -143,54 +297,150 @@ __global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
         if (kt + 1 < KT) gload((kt + 1) * BK);
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ++ks) {
-            const int8_t* pa = &sA[cur][(wm * 64 + lr) * LDS_STRIDE + ks * 32 + lk];
-            const int8_t* pb = &sB[cur][(wn * 64 + lr) * LDS_STRIDE + ks * 32 + lk];
-            v4i a0 = *reinterpret_cast<const v4i*>(pa);
-            v4i a1 = *reinterpret_cast<const v4i*>(pa + 32 * LDS_STRIDE);
-            v4i b0 = *reinterpret_cast<const v4i*>(pb);
-            v4i b1 = *reinterpret_cast<const v4i*>(pb + 32 * LDS_STRIDE);
-            acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc[1][1], 0, 0, 0);
+            v4i a[TI], b[TJ];
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+                a[i] = *reinterpret_cast<const v4i*>(
+                    &sA[cur][(wm * WM + i * 32 + lr) * LDS_STRIDE + ks * 32 + lk]);
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                b[j] = *reinterpret_cast<const v4i*>(
+                    &sB[cur][(wn * WN + j * 32 + lr) * LDS_STRIDE + ks * 32 + lk]);
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
         }
         if (kt + 1 < KT) sstore(cur ^ 1);
         __syncthreads();
     }
 
-    // ---- epilogue: zero-point correction, then int32 store or Cast + chain ------------
-    const int azp = load_zp(g.a_zp, g.a_zp_u8, 0);
-    const uint32_t amz = (uint32_t)(g.alpha - azp);
+    gemm_epilogue<BM, BN, OUT, COLCHAIN>(g, acc, smem, m0, n0);
+}
+
+// ---- main loop B: LDS DMA (K % 64 == 0, 16-byte aligned operands) ---------------------
+// gfx950's global_load_lds_dwordx4 copies 16 bytes per lane from global memory straight
+// into LDS (lane i of a wave lands at M0 + 16 i), so no VGPRs hold tiles in flight and
+// NS-1 K steps are kept outstanding.  Each stage holds the A and B tiles as 64-byte rows
+// (no padding, so one wave instruction fills 16 whole rows); the 16-byte chunk c of row r
+// sits at physical slot c ^ ((r >> 2) & 3), which keeps the MFMA fragment reads (32 rows,
+// one chunk each) free of bank conflicts.  The copies are issued from inline assembly so
+// the compiler does not serialise every LDS read behind them; completion is tracked with
+// explicit vmcnt waits: every K step issues exactly P = (BM + BN) / 64 copies per wave, so
+// "stage kt has landed" is "at most P * (NS - 2) copies outstanding".  Rows past M / N
+// are clamped onto the last real row: they only feed outputs that are never stored.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gptr), "s"(lds_addr)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int BM, int BN, int NS, int OUT, bool COLCHAIN>
+__global__ void __launch_bounds__(kThreads) gemm_i8_dma_kernel(GemmArgs g) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TI = WM / 32, TJ = WN / 32;
+    constexpr int ROWB = 64;                        // bytes per LDS row (= K step)
+    constexpr int STAGE = (BM + BN) * ROWB;
+    constexpr int PA = BM / 64, PB = BN / 64;       // copies per wave per stage
+    constexpr int P = PA + PB;
+    constexpr int TILE_BYTES = NS * STAGE;
+    constexpr int EPI_BYTES = EpiLayout<BM, BN>::BYTES;
+    __shared__ __attribute__((aligned(1024)))
+        int8_t smem[TILE_BYTES > EPI_BYTES ? TILE_BYTES : EPI_BYTES];
+
+    int tm, tn;
+    tile_coords(g, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wid = t >> 6;
+    const int wm = wid >> 1, wn = wid & 1;
+    const int lr = lane & 31;
+    const uint32_t base = lds_addr_of(smem);
+
+    // This lane's source rows / chunks for each of its copies (fixed across K steps).
+    const int8_t* srcA[PA];
+    const int8_t* srcB[PB];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int col = n0 + wn * 64 + j * 32 + lr;
-        if (col >= g.N) continue;
-        const int bzp = load_zp(g.b_zp, g.b_zp_u8, g.b_zp_len == 1 ? 0 : col);
-        const uint32_t colfac = (uint32_t)(g.beta - bzp);
-        const uint32_t colterm =
-            amz * (uint32_t)g.colsum[col] + (uint32_t)g.K * amz * colfac;
+    for (int i = 0; i < PA; ++i) {
+        const int row = wid * (BM / 4) + 16 * i + (lane >> 2);
+        const int kc = (lane & 3) ^ ((row >> 2) & 3);
+        srcA[i] = g.A + (size_t)min(m0 + row, g.M - 1) * g.K + 16 * kc;
+    }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < PB; ++i) {
+        const int row = wid * (BN / 4) + 16 * i + (lane >> 2);
+        const int kc = (lane & 3) ^ ((row >> 2) & 3);
+        srcB[i] = g.Bp + (size_t)min(n0 + row, g.N - 1) * g.K + 16 * kc;
+    }
+    auto issue = [&](int buf, int kt) {
+        const uint32_t sa = base + buf * STAGE;
+        const uint32_t sb = sa + BM * ROWB;
+        const int k0 = kt * ROWB;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row >= g.M) continue;
-                uint32_t v = (uint32_t)acc[i][j][r] + colterm;
-                if (g.rowsum_raw) {
-                    const uint32_t ra = (uint32_t)g.rowsum_raw[row] - (uint32_t)g.alpha * (uint32_t)g.K;
-                    v += colfac * ra;
-                }
-                const size_t off = (size_t)row * g.N + col;
-                if (OUT == OUT_I32) {
-                    reinterpret_cast<int32_t*>(g.C)[off] = (int32_t)v;
-                } else {
-                    float f = (float)(int32_t)v;  // Cast INT32 -> FLOAT, round to nearest even
-                    f = icx::apply_chain(g.chain, f, row, col, g.N);
-                    reinterpret_cast<float*>(g.C)[off] = f;
-                }
+        for (int i = 0; i < PA; ++i)
+            dma16(srcA[i] + k0, __builtin_amdgcn_readfirstlane(sa + (wid * (BM / 4) + 16 * i) * ROWB));
+#pragma unroll
+        for (int i = 0; i < PB; ++i)
+            dma16(srcB[i] + k0, __builtin_amdgcn_readfirstlane(sb + (wid * (BN / 4) + 16 * i) * ROWB));
+    };
+
+    v16i acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    const int KT = g.K / ROWB;
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(s, min(s, KT - 1));
+
+    const uint32_t axr = g.a_xor;
+    for (int kt = 0; kt < KT; ++kt) {
+        wait_vmcnt<P * (NS - 2)>();  // this wave's copies for step kt have landed
+        __syncthreads();             // ... everyone's, and step kt-1's buffer is free
+        issue((kt + NS - 1) % NS, min(kt + NS - 1, KT - 1));
+        const int8_t* sa = smem + (kt % NS) * STAGE;
+        const int8_t* sb = sa + BM * ROWB;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            v4i a[TI], b[TJ];
+            const int kc = ks * 2 + (lane >> 5);
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const int row = wm * WM + i * 32 + lr;
+                v4i v = *reinterpret_cast<const v4i*>(sa + row * ROWB + 16 * (kc ^ ((row >> 2) & 3)));
+                a[i] = v ^ (int)axr;
             }
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const int row = wn * WN + j * 32 + lr;
+                b[j] = *reinterpret_cast<const v4i*>(sb + row * ROWB + 16 * (kc ^ ((row >> 2) & 3)));
+            }
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
         }
     }
+    wait_vmcnt<0>();
+    __syncthreads();  // all copies landed and all fragment reads done: LDS is free
+    gemm_epilogue<BM, BN, OUT, COLCHAIN>(g, acc, smem, m0, n0);
 }
 
 // ---- weight packing -------------------------------------------------------------------
@@ -296,6 +546,33 @@ int pack_weight_impl(hipStream_t s, const void* B, int b_dtype, size_t K, size_t
     return ICX_OK;
 }
 
+template <int BM, int BN>
+void launch_reg(bool vec, int out_kind, bool colchain, unsigned blocks, hipStream_t s,
+                const GemmArgs& g) {
+    const dim3 grid(blocks), block(kThreads);
+    if (out_kind == OUT_I32) {
+        if (vec) hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, true, OUT_I32, false>), grid, block, 0, s, g);
+        else hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, false, OUT_I32, false>), grid, block, 0, s, g);
+    } else if (colchain) {
+        if (vec) hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, true, OUT_F32, true>), grid, block, 0, s, g);
+        else hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, false, OUT_F32, true>), grid, block, 0, s, g);
+    } else {
+        if (vec) hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, true, OUT_F32, false>), grid, block, 0, s, g);
+        else hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, false, OUT_F32, false>), grid, block, 0, s, g);
+    }
+}
+
+template <int BM, int BN, int NS>
+void launch_dma(int out_kind, bool colchain, unsigned blocks, hipStream_t s, const GemmArgs& g) {
+    const dim3 grid(blocks), block(kThreads);
+    if (out_kind == OUT_I32)
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, NS, OUT_I32, false>), grid, block, 0, s, g);
+    else if (colchain)
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, NS, OUT_F32, true>), grid, block, 0, s, g);
+    else
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, NS, OUT_F32, false>), grid, block, 0, s, g);
+}
+
 int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,
                 int b_packed, const int32_t* b_colsum, size_t M, size_t K, size_t N,
                 const void* a_zp, const void* b_zp, size_t b_zp_len, const int32_t* a_rowsum,
@@ -362,8 +639,8 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     g.M = (int)M;
     g.N = (int)N;
     g.K = (int)K;
-    g.tiles_m = (int)icx::cdiv(M, BM);
-    g.tiles_n = (int)icx::cdiv(N, BN);
+    g.tiles_m = (int)icx::cdiv(M, 128);
+    g.tiles_n = (int)icx::cdiv(N, 128);
     g.a_xor = a_dtype == ICX_U8 ? 0x80808080u : 0u;
     g.alpha = alpha;
     g.beta = beta;
@@ -372,15 +649,26 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     g.b_zp_len = (int)(b_zp ? b_zp_len : 1);
     if (chain) g.chain = *chain;
     else g.chain.n_ops = 0;
+    g.codes = icx::chain_codes(g.chain);
 
-    const bool vec = (K % 16 == 0) && icx::aligned16(A) && icx::aligned16(Bp);
+    const bool vec = K >= 16 && (K % 16 == 0) && icx::aligned16(A) && icx::aligned16(Bp);
+    const bool dma = vec && K >= 64 && K % 64 == 0;
+    const bool colchain = out_kind == OUT_F32 && icx::chain_is_col_only(g.chain);
+    // 256x256 tiles (128x128 per wave) when there are enough of them to fill the chip;
+    // otherwise 128x128 so that every CU gets tiles.  Row / full-tensor chain operands
+    // take the general per-element path, kept on the 128x128 tile.
+    const bool big = icx::cdiv(M, 256) * icx::cdiv(N, 256) >= 512 && (out_kind == OUT_I32 || colchain);
+    if (big) {
+        g.tiles_m = (int)icx::cdiv(M, 256);
+        g.tiles_n = (int)icx::cdiv(N, 256);
+    }
     const unsigned blocks = (unsigned)(g.tiles_m * g.tiles_n);
-    if (out_kind == OUT_I32) {
-        if (vec) hipLaunchKernelGGL((gemm_i8_kernel<true, OUT_I32>), dim3(blocks), dim3(kThreads), 0, s, g);
-        else hipLaunchKernelGGL((gemm_i8_kernel<false, OUT_I32>), dim3(blocks), dim3(kThreads), 0, s, g);
+    if (dma) {
+        if (big) launch_dma<256, 256, 4>(out_kind, colchain, blocks, s, g);
+        else launch_dma<128, 128, 3>(out_kind, colchain, blocks, s, g);
     } else {
-        if (vec) hipLaunchKernelGGL((gemm_i8_kernel<true, OUT_F32>), dim3(blocks), dim3(kThreads), 0, s, g);
-        else hipLaunchKernelGGL((gemm_i8_kernel<false, OUT_F32>), dim3(blocks), dim3(kThreads), 0, s, g);
+        if (big) launch_reg<256, 256>(vec, out_kind, colchain, blocks, s, g);
+        else launch_reg<128, 128>(vec, out_kind, colchain, blocks, s, g);
     }
     ICX_LAUNCH_CHECK("gemm_i8_kernel");
     return ICX_OK;
