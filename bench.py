@@ -34,7 +34,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg4", "cfg5a", "cfg5b"])
+    ap.add_argument("--config", default="cfg2",
+                    choices=["cfg1", "cfg2", "cfg4", "cfg5a", "cfg5b", "copy"],
+                    help="copy: the chain kernel with no ops over f32[65536,768] — a plain copy "
+                         "of known size, the scale for the rocprofv3 FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--kernel-reps", type=int, default=100,
                     help="back-to-back launches of the dominant kernel for its average duration")
     ap.add_argument("--cpu-rows", type=int, default=None,
@@ -59,7 +62,9 @@ class Runner:
         self.torch = torch
         self.L = lib()
         self.check = check
-        d = configs.make(cfg)
+        d = configs.make("cfg5b" if cfg == "copy" else cfg)
+        if cfg == "copy":
+            d = dict(d, chain=[])
         self.d = d
         dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
         self.keep = []
@@ -69,7 +74,10 @@ class Runner:
             self.N = d["w"].shape[1]
             self.x = dev(x)
             self.w = ops.PackedWeight(dev(d["w"]))
-            self.w_zp = dev(d["w_zp"])
+            # A weight zero point is an initializer: when it is all zeros (and the weight is
+            # int8) its row term is multiplied by exactly 0, so it is folded away at plan time,
+            # as the executor does (the kernel then needs no row sums).
+            self.w_zp = None if not np.any(d["w_zp"]) else dev(d["w_zp"])
             self.bzp_len = int(np.asarray(d["w_zp"]).size)
             self.xq = torch.empty((self.M, self.K), dtype=torch.uint8, device="cuda")
             self.xs = torch.empty((), dtype=torch.float32, device="cuda")
@@ -85,14 +93,14 @@ class Runner:
             self.keep += k
             self.a_dtype, self.b_dtype = ICX_U8, ICX_I8
             self.ops_count = 2.0 * self.M * self.N * self.K
-            self.dominant = "gemm_i8_kernel"
+            self.dominant = "gemm_i8_dma_kernel"
         elif cfg == "cfg5a":
             self.M, self.K = d["a"].shape
             self.N = d["b"].shape[1]
             self.a = dev(d["a"])
             self.a_zp = dev(d["a_zp"])
             self.w = ops.PackedWeight(dev(d["b"]))
-            self.w_zp = dev(d["b_zp"])
+            self.w_zp = None if not np.any(d["b_zp"]) else dev(d["b_zp"])  # folded when all-zero
             self.bzp_len = 1
             self.y = torch.empty((self.M, self.N), dtype=torch.float32, device="cuda")
             self.gemm_ws = torch.empty(max(1, self.L.icx_matmul_integer_workspace_size(self.M, self.K, self.N, 1)),
@@ -102,12 +110,13 @@ class Runner:
             self.keep += k
             self.a_dtype, self.b_dtype = ICX_U8, ICX_I8
             self.ops_count = 2.0 * self.M * self.N * self.K
-            self.dominant = "gemm_i8_kernel"
-        else:  # cfg5b
+            self.dominant = "gemm_i8_dma_kernel"
+        else:  # cfg5b, copy
             self.x = dev(d["x"])
             self.M, self.N = d["x"].shape
             self.y = torch.empty_like(self.x)
-            self.chain, k = ops.build_chain([(op, dev(c), False) for op, c in d["chain"]], self.M, self.N)
+            chain = [] if cfg == "copy" else [(op, dev(c), False) for op, c in d["chain"]]
+            self.chain, k = ops.build_chain(chain, self.M, self.N)
             self.keep += k
             self.ops_count = None
             self.dominant = "chain_cols_kernel"
@@ -119,7 +128,8 @@ class Runner:
     def dql(self, stream):
         self.check(self.L.icx_dynamic_quantize_linear(
             stream, self._p(self.x), self.x.numel(), self._p(self.xq), self._p(self.xs),
-            self._p(self.xzp), self._p(self.rs), self.K, self._p(self.dql_ws), self.dql_ws.numel()))
+            self._p(self.xzp), self._p(self.rs) if self.w_zp is not None else None, self.K,
+            self._p(self.dql_ws), self.dql_ws.numel()))
 
     def gemm(self, stream):
         if self.cfg == "cfg5a":
@@ -128,8 +138,10 @@ class Runner:
             a, azp, rs = self.xq, self.xzp, self.rs
         self.check(self.L.icx_qlinear_f32(
             stream, self._p(a), self.a_dtype, self._p(self.w.packed), self.b_dtype, 1,
-            self._p(self.w.colsum), self.M, self.K, self.N, self._p(azp), self._p(self.w_zp),
-            self.bzp_len, self._p(rs) if rs is not None else None, ctypes.byref(self.chain),
+            self._p(self.w.colsum), self.M, self.K, self.N, self._p(azp),
+            self._p(self.w_zp) if self.w_zp is not None else None,
+            self.bzp_len, self._p(rs) if (rs is not None and self.w_zp is not None) else None,
+            ctypes.byref(self.chain),
             self._p(self.y), self._p(self.gemm_ws), self.gemm_ws.numel()))
 
     def chain_only(self, stream):
@@ -137,7 +149,7 @@ class Runner:
                                               ctypes.byref(self.chain), self._p(self.y)))
 
     def step(self, stream):
-        if self.cfg == "cfg5b":
+        if self.cfg in ("cfg5b", "copy"):
             self.chain_only(stream)
         elif self.cfg == "cfg5a":
             self.gemm(stream)
@@ -146,7 +158,7 @@ class Runner:
             self.gemm(stream)
 
     def dominant_launch(self, stream):
-        if self.cfg == "cfg5b":
+        if self.cfg in ("cfg5b", "copy"):
             self.chain_only(stream)
         else:
             self.gemm(stream)
@@ -156,7 +168,7 @@ class Runner:
         import numpy as np
 
         M, N = self.M, self.N
-        if self.cfg == "cfg5b":
+        if self.cfg in ("cfg5b", "copy"):
             return 8.0 * M * N + sum(4.0 * N for _ in self.d["chain"])
         K = self.K
         b = M * K + K * N + 4.0 * M * N  # A u8, packed B i8, Y f32
@@ -166,6 +178,20 @@ class Runner:
             b += 4.0 * N * (1 + len(self.d["chain"])) + 4.0 * N * (self.bzp_len > 1)  # bias, chain, per-col zp
             b += 4.0 * N if np.size(self.d["w_scale"]) > 1 else 0
         return b
+
+
+def measured_traffic(cfg):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the plain-copy calibration), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_hbm_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 6 and parts[0] == "traffic" and parts[1] == cfg:
+                return float(parts[5])
+    return None
 
 
 def graph_of(fn, reps, torch):
@@ -296,27 +322,34 @@ def main():
 
     # ---- dominant kernel: average launch duration over R back-to-back launches --------
     reps = args.kernel_reps
-    g_k = graph_of(r.dominant_launch, reps, torch)
-    g_k.replay()
-    sync()
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record()
-    g_k.replay()
-    k1.record()
-    sync()
-    k_us = k0.elapsed_time(k1) * 1e3 / reps
+
+    def time_launches(fn):
+        """Average duration of `reps` back-to-back launches of fn on the current stream."""
+        if args.no_graph:
+            h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            fn(h)
+            sync()
+            k0.record()
+            for _ in range(reps):
+                fn(h)
+            k1.record()
+        else:
+            g = graph_of(fn, reps, torch)
+            g.replay()
+            sync()
+            k0.record()
+            g.replay()
+            k1.record()
+        sync()
+        return k0.elapsed_time(k1) * 1e3 / reps
+
+    k_us = time_launches(r.dominant_launch)
 
     # DQL (two launches) on its own, for the breakdown
     extra = {}
     if args.config in ("cfg1", "cfg2", "cfg4"):
-        g_d = graph_of(r.dql, reps, torch)
-        g_d.replay()
-        sync()
-        k0.record()
-        g_d.replay()
-        k1.record()
-        sync()
-        dql_us = k0.elapsed_time(k1) * 1e3 / reps
+        dql_us = time_launches(r.dql)
         n = r.x.numel()
         extra["dql_us"] = round(dql_us, 3)
         extra["dql_algorithmic_GBps"] = round(5.0 * n / (dql_us * 1e-6) / 1e9, 1)
@@ -332,12 +365,13 @@ def main():
         ach = r.ops_count / (k_us * 1e-6) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS,
                 "unit": "TFLOP/s", "op_kind": "int8 ops (2*M*N*K)", "frac": round(ach / PEAK_INT8_TOPS, 4),
-                "traffic": None, "kernel": r.dominant, "kernel_avg_us": round(k_us, 3),
-                "algorithmic_bytes": alg_bytes}
+                "traffic": measured_traffic(args.config), "kernel": r.dominant,
+                "kernel_avg_us": round(k_us, 3), "algorithmic_bytes": alg_bytes}
     else:
         ach = alg_bytes / (k_us * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": r.dominant,
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(args.config),
+                "kernel": r.dominant,
                 "kernel_avg_us": round(k_us, 3), "algorithmic_bytes": alg_bytes}
         if r.ops_count is not None:
             roof["kernel_int8_TOPS"] = round(r.ops_count / (k_us * 1e-6) / 1e12, 2)
@@ -349,6 +383,7 @@ def main():
         "cfg4": "cfg4: DQL + per-channel quantized linear x[64,384,1024] W[1024,4096]",
         "cfg5a": "cfg5a: MatMulInteger A u8[16384,4096] x B i8[4096,4096] + fused fp32 dequant",
         "cfg5b": "cfg5b: fused Mul/Add/Div/Mul chain on f32[65536,768] with [768] operands",
+        "copy": "copy calibration: chain kernel with no ops (plain copy) on f32[65536,768]",
     }[args.config]
     cfg = {"workload": workload, "M": r.M, "N": r.N}
     if hasattr(r, "K"):
@@ -360,10 +395,11 @@ def main():
         "data": "synthetic: seeded N(0,1) activations (SplitMix64 + Box-Muller), random-init int8 weights",
         "config": cfg, "roofline": roof,
         "timing": {"graph_replay": not args.no_graph, "wall_s": round(wall, 4), **extra},
+        "traffic_source": "profiles/traffic_hbm_pmc.txt (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
     }
-    if args.config == "cfg5b":
+    if args.config in ("cfg5b", "copy"):
         out["dtype"] = "f32"
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.config != "copy":
         cb = cpu_baseline(args.config, args.cpu_rows)
         cb["cores"] = 1
         out["cpu_baseline"] = cb

@@ -490,19 +490,38 @@ packed_colsum_kernel(const int8_t* __restrict__ packed, int K, int N, int32_t* _
     if (lane == 0) colsum[n] = s;
 }
 
-// Raw row sums of A (bytes as u8 or i8), one wave per row.
+// Raw row sums of A (bytes as u8 or i8), one wave per row; 16-byte loads summed with the
+// 4-way byte dot product against 0x01010101 when rows are 16-byte aligned.
 __global__ void __launch_bounds__(kThreads)
-rowsum_kernel(const void* __restrict__ A, int is_u8, int M, int K, int32_t* __restrict__ rowsum) {
+rowsum_kernel(const void* __restrict__ A, int is_u8, int M, int K, int vec,
+              int32_t* __restrict__ rowsum) {
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     if (m >= M) return;
     int s = 0;
-    if (is_u8) {
-        const uint8_t* p = reinterpret_cast<const uint8_t*>(A) + (size_t)m * K;
-        for (int k = lane; k < K; k += 64) s += (int)p[k];
+    const uint8_t* row = reinterpret_cast<const uint8_t*>(A) + (size_t)m * K;
+    if (vec) {
+        const uint4* r16 = reinterpret_cast<const uint4*>(row);
+        const int n16 = K / 16;
+#pragma unroll 4
+        for (int i = lane; i < n16; i += 64) {
+            const uint4 v = r16[i];
+            if (is_u8) {
+                s = (int)__builtin_amdgcn_udot4(v.x, 0x01010101u, (uint32_t)s, false);
+                s = (int)__builtin_amdgcn_udot4(v.y, 0x01010101u, (uint32_t)s, false);
+                s = (int)__builtin_amdgcn_udot4(v.z, 0x01010101u, (uint32_t)s, false);
+                s = (int)__builtin_amdgcn_udot4(v.w, 0x01010101u, (uint32_t)s, false);
+            } else {
+                s = __builtin_amdgcn_sdot4((int)v.x, 0x01010101, s, false);
+                s = __builtin_amdgcn_sdot4((int)v.y, 0x01010101, s, false);
+                s = __builtin_amdgcn_sdot4((int)v.z, 0x01010101, s, false);
+                s = __builtin_amdgcn_sdot4((int)v.w, 0x01010101, s, false);
+            }
+        }
+    } else if (is_u8) {
+        for (int k = lane; k < K; k += 64) s += (int)row[k];
     } else {
-        const int8_t* p = reinterpret_cast<const int8_t*>(A) + (size_t)m * K;
-        for (int k = lane; k < K; k += 64) s += (int)p[k];
+        for (int k = lane; k < K; k += 64) s += (int)(int8_t)row[k];
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
@@ -620,9 +639,10 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
             rowsum = a_rowsum;
         } else {
             int32_t* rs = reinterpret_cast<int32_t*>(wsb + L.rowsum_off);
+            const int rvec = (K % 16 == 0 && icx::aligned16(A)) ? 1 : 0;
             hipLaunchKernelGGL(rowsum_kernel, dim3((unsigned)icx::cdiv(M, kThreads / 64)),
                                dim3(kThreads), 0, s, A, a_dtype == ICX_U8 ? 1 : 0, (int)M,
-                               (int)K, rs);
+                               (int)K, rvec, rs);
             ICX_LAUNCH_CHECK("rowsum_kernel");
             rowsum = rs;
         }
