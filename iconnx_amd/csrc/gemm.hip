@@ -112,11 +112,13 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& g, int& tm, int& tn)
     tn = in_group / gsz;
 }
 
-template <int BM, int BN>
+// Wave grid WGM x WGN over the BM x BN block tile; each wave owns (BM/WGM) x (BN/WGN).
+template <int BM, int BN, int WGM, int WGN>
 struct EpiLayout {
-    static constexpr int WN = BN / 2;
+    static constexpr int NW = WGM * WGN;
+    static constexpr int WN = BN / WGN;
     static constexpr int SROW = WN + 8;  // floats per staged row (4-row offset = 32 banks)
-    static constexpr int STAGE_BYTES = 4 * 32 * SROW * 4;
+    static constexpr int STAGE_BYTES = NW * 32 * SROW * 4;
     static constexpr int BYTES = STAGE_BYTES + ICX_MAX_CHAIN * BN * 4;  // + column operands
 };
 
@@ -126,16 +128,18 @@ struct EpiLayout {
 // applied, then read back row-major as float4 / int4 so that the chain runs on 4
 // consecutive columns per lane with its column operands in LDS, and the global stores are
 // 16-byte and contiguous along rows.  `smem` must not be in use by the main loop any more.
-template <int BM, int BN, int OUT, bool COLCHAIN>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, v16i (&acc)[BM / 64][BN / 64],
+template <int BM, int BN, int WGM, int WGN, int OUT, bool COLCHAIN>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
+                                              v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
                                               int8_t* smem, int m0, int n0) {
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
-    using EL = EpiLayout<BM, BN>;
+    constexpr int NT = 64 * WGM * WGN;
+    using EL = EpiLayout<BM, BN, WGM, WGN>;
     constexpr int SROW = EL::SROW;
     const int t = threadIdx.x;
     const int lane = t & 63, wid = t >> 6;
-    const int wm = wid >> 1, wn = wid & 1;
+    const int wm = wid / WGN, wn = wid % WGN;
     const int lr = lane & 31;
 
     const int azp = load_zp(g.a_zp, g.a_zp_u8, 0);
@@ -160,7 +164,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, v16i (&acc)[BM 
         for (int k = 0; k < ICX_MAX_CHAIN; ++k) {
             if (k < g.chain.n_ops) {
                 const icx_chain_op& op = g.chain.ops[k];
-                for (int c = t; c < BN; c += kThreads) {
+                for (int c = t; c < BN; c += NT) {
                     const int col = min(n0 + c, g.N - 1);
                     float a = icx::col_factor(op.p0, op.kind0, col);
                     if (op.p1) a = __fmul_rn(a, icx::col_factor(op.p1, op.kind1, col));
@@ -242,7 +246,7 @@ __global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
     constexpr int AQ = BM * BK / 16 / kThreads;  // 16-byte chunks per thread per stage
     constexpr int BQ = BN * BK / 16 / kThreads;
     constexpr int TILE_BYTES = 2 * (BM + BN) * LDS_STRIDE;
-    constexpr int EPI_BYTES = EpiLayout<BM, BN>::BYTES;
+    constexpr int EPI_BYTES = EpiLayout<BM, BN, 2, 2>::BYTES;
     __shared__ __attribute__((aligned(16)))
         int8_t smem[TILE_BYTES > EPI_BYTES ? TILE_BYTES : EPI_BYTES];
     int8_t (*sA)[BM * LDS_STRIDE] = reinterpret_cast<int8_t (*)[BM * LDS_STRIDE]>(smem);
@@ -316,7 +320,7 @@ __global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
         __syncthreads();
     }
 
-    gemm_epilogue<BM, BN, OUT, COLCHAIN>(g, acc, smem, m0, n0);
+    gemm_epilogue<BM, BN, 2, 2, OUT, COLCHAIN>(g, acc, smem, m0, n0);
 }
 
 // ---- main loop B: LDS DMA (K % 64 == 0, 16-byte aligned operands) ---------------------
@@ -348,16 +352,22 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int BM, int BN, int NS, int OUT, bool COLCHAIN>
-__global__ void __launch_bounds__(kThreads) gemm_i8_dma_kernel(GemmArgs g) {
-    constexpr int WM = BM / 2, WN = BN / 2;
+template <int BM, int BN, int WGM, int WGN, int NS, int OUT, bool COLCHAIN>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma_kernel(GemmArgs g) {
+    constexpr int NW = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
     constexpr int ROWB = 64;                        // bytes per LDS row (= K step)
     constexpr int STAGE = (BM + BN) * ROWB;
-    constexpr int PA = BM / 64, PB = BN / 64;       // copies per wave per stage
+    // Only the first DW waves copy tiles (each 16-row copy is one wave instruction); the
+    // other waves go straight from the barrier to their MFMAs, keeping the matrix pipe of
+    // every SIMD busy while the copies are issued.
+    constexpr int DW = NW >= 8 ? NW / 2 : NW;
+    constexpr int PA = BM / 16 / DW, PB = BN / 16 / DW;  // copies per copying wave per stage
     constexpr int P = PA + PB;
+    static_assert(PA * 16 * DW == BM && PB * 16 * DW == BN, "tile rows must split over waves");
     constexpr int TILE_BYTES = NS * STAGE;
-    constexpr int EPI_BYTES = EpiLayout<BM, BN>::BYTES;
+    constexpr int EPI_BYTES = EpiLayout<BM, BN, WGM, WGN>::BYTES;
     __shared__ __attribute__((aligned(1024)))
         int8_t smem[TILE_BYTES > EPI_BYTES ? TILE_BYTES : EPI_BYTES];
 
@@ -366,35 +376,36 @@ __global__ void __launch_bounds__(kThreads) gemm_i8_dma_kernel(GemmArgs g) {
     const int m0 = tm * BM, n0 = tn * BN;
     const int t = threadIdx.x;
     const int lane = t & 63, wid = t >> 6;
-    const int wm = wid >> 1, wn = wid & 1;
+    const int wm = wid / WGN, wn = wid % WGN;
     const int lr = lane & 31;
-    const uint32_t base = lds_addr_of(smem);
+    const bool copier = wid < DW;
+    const int cw = copier ? wid : 0;
+    // wave-uniform LDS byte offsets of this wave's copies, in scalar registers
+    const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds_addr_of(smem) + cw * PA * 16 * ROWB);
+    const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds_addr_of(smem) + BM * ROWB + cw * PB * 16 * ROWB);
 
     // This lane's source rows / chunks for each of its copies (fixed across K steps).
     const int8_t* srcA[PA];
     const int8_t* srcB[PB];
 #pragma unroll
     for (int i = 0; i < PA; ++i) {
-        const int row = wid * (BM / 4) + 16 * i + (lane >> 2);
+        const int row = (cw * PA + i) * 16 + (lane >> 2);
         const int kc = (lane & 3) ^ ((row >> 2) & 3);
         srcA[i] = g.A + (size_t)min(m0 + row, g.M - 1) * g.K + 16 * kc;
     }
 #pragma unroll
     for (int i = 0; i < PB; ++i) {
-        const int row = wid * (BN / 4) + 16 * i + (lane >> 2);
+        const int row = (cw * PB + i) * 16 + (lane >> 2);
         const int kc = (lane & 3) ^ ((row >> 2) & 3);
         srcB[i] = g.Bp + (size_t)min(n0 + row, g.N - 1) * g.K + 16 * kc;
     }
     auto issue = [&](int buf, int kt) {
-        const uint32_t sa = base + buf * STAGE;
-        const uint32_t sb = sa + BM * ROWB;
+        if (!copier) return;
         const int k0 = kt * ROWB;
 #pragma unroll
-        for (int i = 0; i < PA; ++i)
-            dma16(srcA[i] + k0, __builtin_amdgcn_readfirstlane(sa + (wid * (BM / 4) + 16 * i) * ROWB));
+        for (int i = 0; i < PA; ++i) dma16(srcA[i] + k0, lds_a + buf * STAGE + i * 16 * ROWB);
 #pragma unroll
-        for (int i = 0; i < PB; ++i)
-            dma16(srcB[i] + k0, __builtin_amdgcn_readfirstlane(sb + (wid * (BN / 4) + 16 * i) * ROWB));
+        for (int i = 0; i < PB; ++i) dma16(srcB[i] + k0, lds_b + buf * STAGE + i * 16 * ROWB);
     };
 
     v16i acc[TI][TJ];
@@ -409,38 +420,61 @@ __global__ void __launch_bounds__(kThreads) gemm_i8_dma_kernel(GemmArgs g) {
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) issue(s, min(s, KT - 1));
 
+    // Fragment double buffering: the reads of one 32-wide half step are issued a phase
+    // ahead of its MFMAs.  Per K step kt:
+    //   read F1 (stage kt, half 1) | MFMAs on F0 (stage kt, half 0)
+    //   wait own copies of stage kt+1; barrier (everyone is past stage kt-1); issue the
+    //   copies of stage kt+NS-1 into stage kt-1's buffer
+    //   read F0 (stage kt+1, half 0) | MFMAs on F1
     const uint32_t axr = g.a_xor;
-    for (int kt = 0; kt < KT; ++kt) {
-        wait_vmcnt<P * (NS - 2)>();  // this wave's copies for step kt have landed
-        __syncthreads();             // ... everyone's, and step kt-1's buffer is free
-        issue((kt + NS - 1) % NS, min(kt + NS - 1, KT - 1));
-        const int8_t* sa = smem + (kt % NS) * STAGE;
+    v4i fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+    auto read_half = [&](int stage, int half, v4i (&fa)[TI], v4i (&fb)[TJ]) {
+        const int8_t* sa = smem + stage * STAGE;
         const int8_t* sb = sa + BM * ROWB;
+        const int kc = half * 2 + (lane >> 5);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            v4i a[TI], b[TJ];
-            const int kc = ks * 2 + (lane >> 5);
-#pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                const int row = wm * WM + i * 32 + lr;
-                v4i v = *reinterpret_cast<const v4i*>(sa + row * ROWB + 16 * (kc ^ ((row >> 2) & 3)));
-                a[i] = v ^ (int)axr;
-            }
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const int row = wn * WN + j * 32 + lr;
-                b[j] = *reinterpret_cast<const v4i*>(sb + row * ROWB + 16 * (kc ^ ((row >> 2) & 3)));
-            }
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < TI; ++i) {
+            const int row = wm * WM + i * 32 + lr;
+            fa[i] = *reinterpret_cast<const v4i*>(sa + row * ROWB + 16 * (kc ^ ((row >> 2) & 3)));
         }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int row = wn * WN + j * 32 + lr;
+            fb[j] = *reinterpret_cast<const v4i*>(sb + row * ROWB + 16 * (kc ^ ((row >> 2) & 3)));
+        }
+    };
+    auto mfma_half = [&](const v4i (&fa)[TI], const v4i (&fb)[TJ]) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const v4i a = fa[i] ^ (int)axr;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, fb[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    wait_vmcnt<P * (NS - 2)>();  // stage 0 has landed
+    __syncthreads();
+    read_half(0, 0, fa0, fb0);
+    // sched_barrier(0) keeps the compiler from sinking the fragment reads below the MFMAs
+    // they are meant to overlap.
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt % NS;
+        read_half(cur, 1, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<P * (NS - 3 > 0 ? NS - 3 : 0)>();  // this wave's copies of stage kt+1
+        __syncthreads();                              // everyone's; stage kt-1 is free
+        issue((kt + NS - 1) % NS, min(kt + NS - 1, KT - 1));
+        if (kt + 1 < KT) read_half((kt + 1) % NS, 0, fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
     }
     wait_vmcnt<0>();
     __syncthreads();  // all copies landed and all fragment reads done: LDS is free
-    gemm_epilogue<BM, BN, OUT, COLCHAIN>(g, acc, smem, m0, n0);
+    gemm_epilogue<BM, BN, WGM, WGN, OUT, COLCHAIN>(g, acc, smem, m0, n0);
 }
 
 // ---- weight packing -------------------------------------------------------------------
@@ -581,15 +615,15 @@ void launch_reg(bool vec, int out_kind, bool colchain, unsigned blocks, hipStrea
     }
 }
 
-template <int BM, int BN, int NS>
+template <int BM, int BN, int WGM, int WGN, int NS>
 void launch_dma(int out_kind, bool colchain, unsigned blocks, hipStream_t s, const GemmArgs& g) {
-    const dim3 grid(blocks), block(kThreads);
+    const dim3 grid(blocks), block(64 * WGM * WGN);
     if (out_kind == OUT_I32)
-        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, NS, OUT_I32, false>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_I32, false>), grid, block, 0, s, g);
     else if (colchain)
-        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, NS, OUT_F32, true>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_F32, true>), grid, block, 0, s, g);
     else
-        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, NS, OUT_F32, false>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_F32, false>), grid, block, 0, s, g);
 }
 
 int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,
@@ -684,8 +718,8 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     }
     const unsigned blocks = (unsigned)(g.tiles_m * g.tiles_n);
     if (dma) {
-        if (big) launch_dma<256, 256, 4>(out_kind, colchain, blocks, s, g);
-        else launch_dma<128, 128, 3>(out_kind, colchain, blocks, s, g);
+        if (big) launch_dma<256, 256, 2, 4, 4>(out_kind, colchain, blocks, s, g);
+        else launch_dma<128, 128, 2, 2, 3>(out_kind, colchain, blocks, s, g);
     } else {
         if (big) launch_reg<256, 256>(vec, out_kind, colchain, blocks, s, g);
         else launch_reg<128, 128>(vec, out_kind, colchain, blocks, s, g);
