@@ -39,6 +39,7 @@ class Chain(ctypes.Structure):
 _lib = None
 
 P, S, I = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+C, CP = ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)
 SIGNATURES = {
     "icx_status_str": ([I], ctypes.c_char_p),
     "icx_last_error": ([], ctypes.c_char_p),
@@ -53,6 +54,18 @@ SIGNATURES = {
     "icx_qlinear_f32": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, ctypes.POINTER(Chain), P, P, S], I),
     "icx_cast_i32_f32": ([P, P, S, P], I),
     "icx_dequantize_linear_f32": ([P, P, I, P, P, S, S, S, P], I),
+    "icx_graph_create": ([], P),
+    "icx_graph_destroy": ([P], None),
+    "icx_graph_add_input": ([P, C, I, P], I),
+    "icx_graph_add_initializer": ([P, C, I, I, P, P], I),
+    "icx_graph_add_node": ([P, C, C, I, CP, I, CP, I, CP, P], I),
+    "icx_graph_add_output": ([P, C], I),
+    "icx_graph_plan": ([P, P, S], I),
+    "icx_graph_compile": ([P, P], I),
+    "icx_graph_set_input": ([P, C, I, I, P, P, I], I),
+    "icx_graph_run": ([P, P], I),
+    "icx_graph_get_output": ([P, C, ctypes.POINTER(I), ctypes.POINTER(I), P, ctypes.POINTER(P)], I),
+    "icx_graph_pool_stats": ([P, P, P, P], I),
 }
 
 

@@ -25,12 +25,15 @@ HIP_FLAGS = [
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-SOURCES = ["dql.hip", "gemm.hip", "elementwise.hip"]
+# host-only C++ (the graph executor) goes through hipcc for the HIP runtime headers
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall"]
+SOURCES = ["dql.hip", "gemm.hip", "elementwise.hip", "executor.cpp"]
 
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    flags = HIP_FLAGS if src.endswith(".hip") else HOST_FLAGS
+    cmd = [HIPCC, *flags, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("hipcc failed for %s:\n%s\n%s" % (src, " ".join(cmd), r.stderr))

@@ -1,0 +1,219 @@
+"""GpuGraphExecutor over the C ABI graph executor (``icx_graph_*`` in include/iconnx_hip.h).
+
+Mirrors the reference's shim (src/cuda/inference/mod.rs:208-659): ``add_input`` (:306),
+``add_initializer`` (:317), ``add_node`` (:331), ``compile`` (:487), ``run`` (:428) with the
+input-shape guard (:441-460) and ``pool_stats`` (:381).  Lowering, fusion, weight packing,
+the memory pool and per-op dispatch all live in the native library
+(iconnx_amd/csrc/executor.cpp); this class only marshals names, host arrays and torch
+device tensors across the boundary.
+
+Differences from the reference that a caller can see:
+  * only the ops of the quantized-linear path dispatch (DynamicQuantizeLinear,
+    MatMulInteger, DequantizeLinear, Cast to FLOAT, Mul/Add/Sub/Div); any other op raises
+    IconnxError at run naming the node;
+  * ``MatMulInteger -> Cast -> Mul(scale) [-> Add(bias)] [-> Mul/Add/Sub/Div]*`` runs as one
+    fused GEMM (pattern ``QuantizedLinear``); the reference leaves it unfused;
+  * ``run_device`` returns device tensors without the host round trip.
+"""
+import ctypes
+from collections import namedtuple
+
+import numpy as np
+
+from ._lib import ICX_F32, ICX_I8, ICX_I32, ICX_U8, IconnxError, check, lib
+
+_NP_DT = {np.dtype(np.int8): ICX_I8, np.dtype(np.uint8): ICX_U8,
+          np.dtype(np.int32): ICX_I32, np.dtype(np.float32): ICX_F32}
+_DT_NP = {v: k for k, v in _NP_DT.items()}
+
+PlanEntry = namedtuple("PlanEntry", "node op_type kind pattern steps out wzp_folded")
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _torch_dt(code):
+    torch = _torch()
+    return {ICX_I8: torch.int8, ICX_U8: torch.uint8, ICX_I32: torch.int32,
+            ICX_F32: torch.float32}[code]
+
+
+def _dims(shape):
+    arr = (ctypes.c_int64 * max(len(shape), 1))(*[int(d) for d in shape])
+    return arr
+
+
+def _cstrs(names):
+    arr = (ctypes.c_char_p * max(len(names), 1))(*[n.encode() for n in names])
+    return arr
+
+
+_hip = None
+
+
+def _hip_memcpy_d2d(dst, src, nbytes, stream):
+    """hipMemcpyAsync device-to-device on `stream` (the HIP runtime torch already loaded)."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                        ctypes.c_int, ctypes.c_void_p]
+        _hip.hipMemcpyAsync.restype = ctypes.c_int
+    rc = _hip.hipMemcpyAsync(dst, src, nbytes, 3, stream)  # 3 = hipMemcpyDeviceToDevice
+    if rc != 0:
+        raise IconnxError(5, "hipMemcpyAsync of an output failed (hipError %d)" % rc)
+
+
+class GpuGraphExecutor:
+    """Build a graph, then ``run`` it on the GPU (one executor per thread, as in the
+    reference)."""
+
+    def __init__(self):
+        self._L = lib()
+        self._g = self._L.icx_graph_create()
+        if not self._g:
+            raise IconnxError(1, "icx_graph_create failed")
+        self._outputs = []
+        self._keep = []  # device inputs bound in place, alive until the next run
+
+    def __del__(self):
+        g, self._g = getattr(self, "_g", None), None
+        if g:
+            self._L.icx_graph_destroy(g)
+
+    # ---- construction -------------------------------------------------------------------
+    @classmethod
+    def from_model(cls, model):
+        """Seed inputs, initializers and nodes from a parsed model
+        (src/cuda/inference/mod.rs:250-271): node names are synthesised as ``n{i}``."""
+        exec_ = cls()
+        for name, shape in model.input_shapes():
+            exec_.add_input(name, shape)
+        for name, arr in model.extract_weights().items():
+            exec_.add_initializer(name, arr)
+        for i, node in enumerate(model.computation_graph()):
+            exec_.add_node("n%d" % i, node.op_type, node.inputs, node.outputs, node.attributes)
+        return exec_
+
+    def add_input(self, name, shape):
+        """``shape[i] is None`` marks a dynamic dimension."""
+        dims = [-1 if d is None else int(d) for d in shape]
+        check(self._L.icx_graph_add_input(self._g, name.encode(), len(dims), _dims(dims)))
+
+    def add_initializer(self, name, tensor):
+        """Host array (numpy or CPU torch).  Int8 / UInt8 / Int32 / Float32 are kept; other
+        dtypes are skipped, so a node reading one fails at run (as the reference does)."""
+        arr = tensor.numpy() if hasattr(tensor, "numpy") and not isinstance(tensor, np.ndarray) \
+            else np.asarray(tensor)
+        code = _NP_DT.get(arr.dtype)
+        if code is None:
+            return
+        arr = np.ascontiguousarray(arr)
+        check(self._L.icx_graph_add_initializer(
+            self._g, name.encode(), code, arr.ndim, _dims(arr.shape),
+            arr.ctypes.data_as(ctypes.c_void_p)))
+
+    def add_node(self, name, op_type, inputs, outputs, attributes=None):
+        """Attributes: integer-valued ones (``to``, ``axis``) are passed; others are not on
+        this path and are ignored."""
+        attrs = {k: int(v) for k, v in (attributes or {}).items()
+                 if isinstance(v, (int, np.integer)) and not isinstance(v, bool)}
+        keys = list(attrs)
+        vals = (ctypes.c_int64 * max(len(keys), 1))(*[attrs[k] for k in keys])
+        check(self._L.icx_graph_add_node(
+            self._g, name.encode(), op_type.encode(), len(inputs), _cstrs(list(inputs)),
+            len(outputs), _cstrs(list(outputs)), len(keys), _cstrs(keys), vals))
+
+    def add_output(self, name):
+        if name not in self._outputs:
+            self._outputs.append(name)
+        check(self._L.icx_graph_add_output(self._g, name.encode()))
+
+    # ---- lowering -------------------------------------------------------------------------
+    def plan(self):
+        """Fusion decision and op order (host only, no GPU work): a list of PlanEntry, plus
+        the DQL outputs whose row sums the fused GEMMs read."""
+        size = 1 << 16
+        while True:
+            buf = ctypes.create_string_buffer(size)
+            rc = self._L.icx_graph_plan(self._g, buf, size)
+            if rc == 0:
+                break
+            msg = self._L.icx_last_error().decode()
+            if "buffer has" not in msg or size > (1 << 26):
+                check(rc)
+            size *= 4
+        entries, rowsums = [], []
+        for line in buf.value.decode().splitlines():
+            parts = line.split()
+            if parts[0] == "rowsum":
+                rowsums.append(parts[1])
+                continue
+            extra = dict(p.split("=", 1) for p in parts[4:])
+            entries.append(PlanEntry(parts[0], parts[1], parts[2], parts[3],
+                                     int(extra.get("steps", 0)), extra.get("out"),
+                                     extra.get("wzp") == "folded"))
+        return entries, rowsums
+
+    def compile(self):
+        torch = _torch()
+        check(self._L.icx_graph_compile(self._g, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+
+    # ---- execution ------------------------------------------------------------------------
+    def _bind(self, inputs):
+        torch = _torch()
+        self._keep = []
+        for name, t in inputs.items():
+            if isinstance(t, torch.Tensor) and t.is_cuda:
+                t = t.contiguous()
+                code = _NP_DT.get(np.dtype(str(t.dtype).replace("torch.", "")))
+                if code is None:
+                    raise IconnxError(3, "input '%s': dtype %s unsupported" % (name, t.dtype))
+                self._keep.append(t)
+                check(self._L.icx_graph_set_input(self._g, name.encode(), code, t.dim(),
+                                                  _dims(t.shape), ctypes.c_void_p(t.data_ptr()), 1))
+                continue
+            arr = np.ascontiguousarray(t.numpy() if isinstance(t, torch.Tensor) else np.asarray(t))
+            code = _NP_DT.get(arr.dtype)
+            if code is None:
+                raise IconnxError(3, "input '%s': dtype %s unsupported" % (name, arr.dtype))
+            check(self._L.icx_graph_set_input(self._g, name.encode(), code, arr.ndim,
+                                              _dims(arr.shape), arr.ctypes.data_as(ctypes.c_void_p), 0))
+
+    def run_device(self, inputs, output_names):
+        """Run on ``torch.cuda.current_stream()``; returns {name: device tensor} (copies that
+        outlive the next run).  Nothing synchronises the host."""
+        torch = _torch()
+        for n in output_names:
+            self.add_output(n)
+        self._bind(inputs)
+        stream = torch.cuda.current_stream().cuda_stream
+        check(self._L.icx_graph_run(self._g, ctypes.c_void_p(stream)))
+        out = {}
+        for n in output_names:
+            dt, rank = ctypes.c_int(), ctypes.c_int()
+            dims = (ctypes.c_int64 * 8)()
+            ptr = ctypes.c_void_p()
+            check(self._L.icx_graph_get_output(self._g, n.encode(), ctypes.byref(dt),
+                                               ctypes.byref(rank), dims, ctypes.byref(ptr)))
+            t = torch.empty([dims[i] for i in range(rank.value)], dtype=_torch_dt(dt.value),
+                            device="cuda")
+            nbytes = t.numel() * t.element_size()
+            if nbytes:
+                _hip_memcpy_d2d(ctypes.c_void_p(t.data_ptr()), ptr, nbytes, ctypes.c_void_p(stream))
+            out[n] = t
+        return out
+
+    def run(self, inputs, output_names):
+        """As the reference's ``run``: host arrays in (device tensors also accepted), host
+        arrays (numpy) out."""
+        dev = self.run_device(inputs, output_names)
+        return {k: v.cpu().numpy() for k, v in dev.items()}
+
+    def pool_stats(self):
+        """(hipMalloc calls, pool hits, bytes held by the pool)."""
+        a, b, c = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+        check(self._L.icx_graph_pool_stats(self._g, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c)))
+        return a.value, b.value, c.value

@@ -139,6 +139,52 @@ int icx_dequantize_linear_f32(icx_stream_t stream, const void* x, int x_dtype,
                               const float* scale, const void* zp, size_t n,
                               size_t axis_size, size_t inner, float* y);
 
+
+/* ---- graph executor ------------------------------------------------------------------
+ * Mirrors GpuGraphExecutor (src/cuda/inference/mod.rs:208-659): add_input (:306),
+ * add_initializer (:317), add_node (:331), a lowering step (ir::lower,
+ * src/ir/lowering.rs:31-238: topological sort, fusion decision, initializer upload) and run
+ * (:428) with the input-shape guard (:441-460).  Only the ops of the quantized-linear path
+ * are dispatched: DynamicQuantizeLinear, MatMulInteger (2-D and 3-D x 2-D,
+ * layout.rs:1034-1095), DequantizeLinear, Cast (to FLOAT), Mul / Add / Sub / Div;
+ * anything else is an ICX_ERR_UNSUPPORTED error naming the op.
+ * Fused patterns (src/cuda/inference/fusion/patterns.rs:15-109 plus one new head):
+ *   QuantizedLinear  MatMulInteger -> Cast -> Mul(scale or Mul(x_scale, w_scale)) [-> Add]
+ *                    [-> Mul/Add/Sub/Div with static operands]*  => icx_qlinear_f32
+ *   MulAdd / AddMul / SubMul / DivMul / ElementwiseChain — chains of binary elementwise ops
+ *                    with static operands (scalar, [last dim], same shape) => icx_fused_chain_f32
+ * Attribute values are int64 (axis, to); names of absent optional inputs are "". */
+typedef struct icx_graph icx_graph;
+
+icx_graph* icx_graph_create(void);
+void icx_graph_destroy(icx_graph* g);
+/* dims: rank entries; -1 marks a dynamic dimension (shape[i] == None in the reference). */
+int icx_graph_add_input(icx_graph* g, const char* name, int rank, const int64_t* dims);
+/* Host data is copied (uploaded at compile).  dtype: ICX_I8 / ICX_U8 / ICX_I32 / ICX_F32. */
+int icx_graph_add_initializer(icx_graph* g, const char* name, int dtype, int rank,
+                              const int64_t* dims, const void* host_data);
+int icx_graph_add_node(icx_graph* g, const char* name, const char* op_type, int n_in,
+                       const char* const* inputs, int n_out, const char* const* outputs,
+                       int n_attr, const char* const* attr_names, const int64_t* attr_values);
+int icx_graph_add_output(icx_graph* g, const char* name);
+/* Host passes only (topological sort, fusion decision, zero-point folding); no GPU work.
+ * Writes a text summary into buf (may be NULL): one "<node> <op> <kind> <pattern> [k=v...]"
+ * line per executed op in order (kind Regular or FusedHead; a head's fused nodes follow it as
+ * Skip lines), then one "rowsum <tensor>" line per DQL output whose row sums are emitted. */
+int icx_graph_plan(icx_graph* g, char* buf, size_t buf_len);
+/* Plan (if needed), upload initializers, pack MatMulInteger weights (colsums), on stream. */
+int icx_graph_compile(icx_graph* g, icx_stream_t stream);
+/* Bind an input: `data` is host memory (copied H2D on the stream) or, with on_device = 1, a
+ * device pointer used in place. */
+int icx_graph_set_input(icx_graph* g, const char* name, int dtype, int rank, const int64_t* dims,
+                        const void* data, int on_device);
+int icx_graph_run(icx_graph* g, icx_stream_t stream);
+/* Device pointer / dtype / shape of an output after run (valid until the next run). */
+int icx_graph_get_output(icx_graph* g, const char* name, int* dtype, int* rank, int64_t* dims,
+                         const void** device_ptr);
+/* Memory pool statistics: allocations from hipMalloc, pool hits, bytes held. */
+int icx_graph_pool_stats(icx_graph* g, int64_t* hipmallocs, int64_t* hits, int64_t* bytes_held);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,243 @@
+"""Host-side lowering of the graph executor (no GPU): topological sort, dead-node
+elimination, the fusion decision and zero-point folding.
+
+Counterparts in the reference: the fusion-detection tests of
+src/ir/passes/elementwise_fusion (matchers.rs:363-409 MulAdd, :483-514 DivMul; exact
+two-op chains, static operands) and the lowering tests of src/ir/lowering.rs.  The
+QuantizedLinear head is new here: the reference leaves MatMulInteger -> Cast -> Mul -> Add
+unfused (src/cuda/inference/fusion/detection.rs:98-102).
+"""
+import numpy as np
+import pytest
+
+from iconnx_amd import configs, graphs
+from iconnx_amd._lib import IconnxError
+from iconnx_amd.executor import GpuGraphExecutor
+
+
+def heads(entries):
+    return [e for e in entries if e.kind == "FusedHead"]
+
+
+def by_node(entries):
+    return {e.node: e for e in entries}
+
+
+def linear(ex, w_zp=0, chain=(), prefix="l", x="x", dql=None, w_dtype=np.int8, N=16):
+    rng = np.random.default_rng(0)
+    w = rng.integers(-127, 128, size=(8, N)).astype(w_dtype)
+    zp = None if w_zp is None else np.asarray(w_zp, dtype=w_dtype)
+    return graphs.add_quantized_linear(ex, x, w, zp, np.float32(0.02),
+                                       rng.standard_normal(N).astype(np.float32), chain,
+                                       prefix=prefix, dql=dql)
+
+
+def test_quantized_linear_head_and_zero_point_folding():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    y = linear(ex, w_zp=0)
+    ex.add_output(y)
+    entries, rowsums = ex.plan()
+    h = heads(entries)
+    assert len(h) == 1 and h[0].pattern == "QuantizedLinear"
+    assert h[0].op_type == "MatMulInteger" and h[0].out == y
+    assert h[0].steps == 2  # Mul(acc_f, x_scale*w_scale) and Add(bias)
+    assert h[0].wzp_folded  # all-zero int8 weight zero point
+    assert rowsums == []  # no weight zero point left, int8 weights: no row sums needed
+    kinds = {e.node: e.kind for e in entries}
+    assert kinds["l.dql"] == "Regular"
+    for n in ("l.scale", "l.cast", "l.dequant", "l.bias_add"):
+        assert kinds[n] == "Skip", n
+
+
+def test_nonzero_weight_zero_point_requests_dql_row_sums():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    y = linear(ex, w_zp=np.arange(-8, 8))
+    ex.add_output(y)
+    entries, rowsums = ex.plan()
+    (h,) = heads(entries)
+    assert not h.wzp_folded
+    assert rowsums == ["l.x_q"]
+
+
+def test_uint8_weights_need_row_sums_even_without_zero_point():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    rng = np.random.default_rng(1)
+    y = graphs.add_quantized_linear(ex, "x", rng.integers(0, 256, (8, 16)).astype(np.uint8),
+                                    None, np.float32(0.1), None, prefix="u")
+    ex.add_output(y)
+    entries, rowsums = ex.plan()
+    (h,) = heads(entries)
+    assert h.steps == 1 and rowsums == ["u.x_q"]
+
+
+def test_cfg2_chain_is_absorbed_into_the_gemm_epilogue():
+    ex = GpuGraphExecutor()
+    y, _ = graphs.config_graph(ex, "cfg2")
+    ex.add_output(y)
+    entries, _ = ex.plan()
+    (h,) = heads(entries)
+    assert h.pattern == "QuantizedLinear" and h.steps == 6 and h.out == y
+    assert sum(e.kind != "Skip" for e in entries) == 2  # DQL + fused GEMM
+
+
+def test_requested_intermediate_output_stops_the_fusion():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    y = linear(ex, chain=[("Mul", np.ones(16)), ("Add", np.zeros(16))])
+    ex.add_output("l.linear")  # the pre-chain value must materialise
+    ex.add_output(y)
+    entries, _ = ex.plan()
+    hs = {h.pattern: h for h in heads(entries)}
+    assert hs["QuantizedLinear"].out == "l.linear" and hs["QuantizedLinear"].steps == 2
+    assert hs["MulAdd"].out == y
+
+
+def test_fan_out_of_the_accumulator_prevents_fusion():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    y = linear(ex)
+    ex.add_node("extra", "Cast", ["l.acc"], ["acc_copy"], {"to": 1})
+    ex.add_output(y)
+    ex.add_output("acc_copy")
+    entries, _ = ex.plan()
+    e = by_node(entries)
+    assert e["l.mmi"].kind == "Regular"
+    assert e["l.cast"].kind == "Regular"
+    # the dequant Mul -> bias Add pair is still a static-operand chain? No: the dequant
+    # Mul's operand is the runtime scale, so only plain ops remain.
+    assert not [h for h in heads(entries) if h.pattern == "QuantizedLinear"]
+
+
+@pytest.mark.parametrize("ops,pattern", [
+    (("Mul", "Add"), "MulAdd"), (("Add", "Mul"), "AddMul"), (("Sub", "Mul"), "SubMul"),
+    (("Div", "Mul"), "DivMul"), (("Mul", "Add", "Div"), "ElementwiseChain"),
+    (("Div", "Sub"), "ElementwiseChain"),
+])
+def test_elementwise_chain_patterns(ops, pattern):
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [4, 6])
+    cur = "x"
+    for i, op in enumerate(ops):
+        ex.add_initializer("c%d" % i, np.full(6, 1.5, np.float32))
+        ex.add_node("n%d" % i, op, [cur, "c%d" % i], ["t%d" % i])
+        cur = "t%d" % i
+    ex.add_output(cur)
+    entries, _ = ex.plan()
+    (h,) = heads(entries)
+    assert h.pattern == pattern and h.steps == len(ops) and h.out == cur
+
+
+def test_single_binary_op_and_runtime_operands_stay_regular():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [4, 6])
+    ex.add_input("z", [4, 6])
+    ex.add_initializer("c", np.ones(6, np.float32))
+    ex.add_node("a", "Mul", ["x", "c"], ["t0"])
+    ex.add_node("b", "Add", ["t0", "z"], ["t1"])  # runtime operand: not a static chain
+    ex.add_output("t1")
+    entries, _ = ex.plan()
+    assert not heads(entries)
+    assert [e.kind for e in entries] == ["Regular", "Regular"]
+
+
+def test_chain_longer_than_eight_splits():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    chain = [("Mul", np.full(16, 1.01)), ("Add", np.full(16, 0.01))] * 5  # 10 ops
+    y = linear(ex, chain=chain)
+    ex.add_output(y)
+    entries, _ = ex.plan()
+    hs = heads(entries)
+    assert [h.pattern for h in hs] == ["QuantizedLinear", "ElementwiseChain"]
+    assert hs[0].steps == 8  # dequant Mul + bias Add + 6 chain ops
+    assert hs[1].steps == 4 and hs[1].out == y
+
+
+def test_shared_dql_for_three_projections():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    dql = graphs.add_dynamic_quantize(ex, "x", "attn")
+    outs = [linear(ex, w_zp=np.arange(16) % 3, prefix=p, dql=dql) for p in ("q", "k", "v")]
+    for o in outs:
+        ex.add_output(o)
+    entries, rowsums = ex.plan()
+    assert [h.pattern for h in heads(entries)] == ["QuantizedLinear"] * 3
+    assert rowsums == ["attn.x_q"]
+    assert sum(e.op_type == "DynamicQuantizeLinear" and e.kind == "Regular" for e in entries) == 1
+
+
+def test_insertion_order_does_not_matter():
+    ref = GpuGraphExecutor()
+    ref.add_input("x", [None, 8])
+    y = linear(ref)
+    ref.add_output(y)
+    want, _ = ref.plan()
+
+    # same graph, nodes added in reverse order
+    class Recorder:
+        def __init__(self):
+            self.calls = []
+
+        def __getattr__(self, name):
+            return lambda *a, **k: self.calls.append((name, a, k))
+
+    rec = Recorder()
+    linear(rec)
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    inits = [c for c in rec.calls if c[0] == "add_initializer"]
+    nodes = [c for c in rec.calls if c[0] == "add_node"]
+    for name, a, k in inits + nodes[::-1]:
+        getattr(ex, name)(*a, **k)
+    ex.add_output(y)
+    got, _ = ex.plan()
+    assert [(e.op_type, e.kind, e.pattern, e.steps) for e in heads(got)] == \
+        [(e.op_type, e.kind, e.pattern, e.steps) for e in heads(want)]
+    order = [e.node for e in got if e.kind != "Skip"]
+    assert order.index("l.dql") < order.index("l.mmi")
+
+
+def test_dead_nodes_are_dropped_and_sinks_become_outputs():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    y = linear(ex)
+    ex.add_node("unused", "Mul", ["x", "l.bias"], ["dead"])
+    ex.add_output(y)
+    entries, _ = ex.plan()
+    assert "unused" not in by_node(entries)
+    # no requested outputs: every sink is live
+    ex2 = GpuGraphExecutor()
+    ex2.add_input("x", [None, 8])
+    linear(ex2)
+    ex2.add_initializer("k", np.ones(16, np.float32))
+    ex2.add_node("side", "Mul", ["x", "k"], ["side_out"])
+    entries2, _ = ex2.plan()
+    assert "side" in by_node(entries2)
+
+
+def test_cycle_is_an_error():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [2])
+    ex.add_node("a", "Add", ["x", "t1"], ["t0"])
+    ex.add_node("b", "Add", ["t0", "x"], ["t1"])
+    ex.add_output("t1")
+    with pytest.raises(IconnxError, match="cycle"):
+        ex.plan()
+
+
+def test_configs_plan_to_one_fused_gemm_each():
+    for cfg in ("cfg1", "cfg2", "cfg4"):
+        ex = GpuGraphExecutor()
+        y, d = graphs.config_graph(ex, cfg)
+        ex.add_output(y)
+        entries, rowsums = ex.plan()
+        live = [e for e in entries if e.kind != "Skip"]
+        assert [e.op_type for e in live] == ["DynamicQuantizeLinear", "MatMulInteger"], cfg
+        assert live[1].pattern == "QuantizedLinear"
+        per_channel_zp = np.any(np.asarray(d["w_zp"]) != 0)
+        assert live[1].wzp_folded == (not per_channel_zp), cfg
+        assert rowsums == (["%s.x_q" % cfg] if per_channel_zp else []), cfg
+        assert live[1].steps == 2 + len(d["chain"]), cfg
