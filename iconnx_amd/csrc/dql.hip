@@ -1,11 +1,14 @@
 // DynamicQuantizeLinear on gfx950: a two-launch, HBM-bound path.
 //
-//   launch 1  dql_minmax_kernel   — each block reduces a grid-stride share of x (float4
-//             loads, 4 in flight per lane) to one (min, max) pair, wave64 shuffles + LDS.
-//   launch 2  dql_quantize_*      — a persistent grid; every block first folds the <=512
-//             partial pairs (4 KB, L2-resident) and derives scale / zero point itself, so
-//             no grid-wide counter or memset is needed (safe to capture in a graph), then
-//             quantizes 16 elements per lane (4 x float4 in, one 16-byte store out).
+//   launch 1  dql_minmax_kernel   — block b reduces one contiguous slice of x (float4 loads,
+//             4 in flight per lane) to a (min, max) pair, wave64 shuffles + LDS.
+//   launch 2  dql_quantize_kernel / dql_quantize_rows_kernel — the same grid over the same
+//             slices: block b first folds the <= 1024 partial pairs (8 KB, L2-resident)
+//             and derives scale / zero point itself, so no grid-wide counter or memset is
+//             needed (safe to capture in a graph), then quantizes its slice (row mode also
+//             writes the row sums of y).
+//   Block b of both launches runs on the same XCD (b mod 8) and reads the same bytes, so
+//   launch 2 re-reads x from that XCD's L2 (small tensors) or the Infinity Cache.
 //
 // Semantics follow DynamicQuantizeLinear::forward
 // (src/operators/dynamic_quantize_linear.rs:32-112):
@@ -13,27 +16,40 @@
 //     including +0.0 winning over -0.0;
 //   * scale = (max-min)/255 and zp = clamp(rne(0 - min/scale)) in f64 (:89-91);
 //   * y = clamp(rne(x / scale) + zp) with the division in f64 (:97-103), NaN -> 0.
-// The per-element quotient is formed as x * (1/scale) in f64 (error < 2^-51 * 255 ~ 1e-13
-// in absolute terms since |x/scale| <= 255); only when that product lies within 1e-9 of a
-// half-integer — where rounding could depend on the last bits — is the correctly rounded
-// f64 division performed, so the result equals the reference's f64 division bit for bit.
+//
+// Per-element rounding.  |x / scale| <= 255 because min <= 0 <= max.  The fast path forms
+// q = x * fl32(1/scale) in f32: two roundings of relative size <= 2^-24 each give
+// |q - x/scale| <= 255 * 2^-23 < 3.1e-5.  When q is farther than 1e-4 from a half-integer,
+// rne(q) equals rne of the exact quotient and of its f64 rounding (which is within
+// 255 * 2^-53 of it).  Otherwise — and for NaN, subnormal x, or a scale outside
+// [1e-30, 1e30] — the f64 division is performed as the reference does.  The f64 path itself
+// uses x * (1/scale) and falls back to the correctly rounded division within 1e-9 of a tie.
 #include "icx_common.hpp"
 
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxPartials = 512;
+constexpr int kMaxBlocks = 1024;
 
 struct alignas(16) DqlParams {
-    double s;    // f64 scale (0 for the constant-input sentinel)
-    double inv;  // 1/s
+    double s;     // f64 scale (0 for the constant-input sentinel)
+    double inv;   // 1/s
+    float inv32;  // fl32(1/s), used when `fast`
     int zp;
-    int zero;    // min == max
+    int zero;     // min == max
+    int fast;     // scale in [1e-30, 1e30]
 };
 
 __device__ __forceinline__ void acc_minmax(float v, float& mn, float& mx) {
     mn = (v < mn) ? v : mn;  // NaN compares false: skipped
     mx = (v > mx) ? v : mx;
+}
+
+__device__ __forceinline__ void acc4(float4 v, float& mn, float& mx) {
+    acc_minmax(v.x, mn, mx);
+    acc_minmax(v.y, mn, mx);
+    acc_minmax(v.z, mn, mx);
+    acc_minmax(v.w, mn, mx);
 }
 
 __device__ __forceinline__ void wave_minmax(float& mn, float& mx) {
@@ -78,18 +94,23 @@ __device__ __forceinline__ DqlParams make_params(float mn, float mx) {
     if (mnd == mxd) {
         p.s = 0.0;
         p.inv = 0.0;
+        p.inv32 = 0.0f;
         p.zp = 0;
         p.zero = 1;
+        p.fast = 0;
         return p;
     }
     p.s = (mxd - mnd) / 255.0;
     p.zp = clamp_u8(rint(0.0 - mnd / p.s));
     p.inv = 1.0 / p.s;
+    p.inv32 = (float)p.inv;
     p.zero = 0;
+    p.fast = (p.s >= 1e-30 && p.s <= 1e30) ? 1 : 0;
     return p;
 }
 
-__device__ __forceinline__ uint32_t quant1(float x, const DqlParams& p) {
+// Reference-exact f64 path.
+__device__ __forceinline__ uint32_t quant1_f64(float x, const DqlParams& p) {
     const double xd = (double)x;
     const double q = xd * p.inv;
     const double fr = q - floor(q);
@@ -101,9 +122,43 @@ __device__ __forceinline__ uint32_t quant1(float x, const DqlParams& p) {
     return (uint32_t)clamp_u8(r + (double)p.zp);
 }
 
+__device__ __forceinline__ uint32_t quant1(float x, const DqlParams& p) {
+    if (p.zero) return 0u;
+    const float q = x * p.inv32;
+    const float r = rintf(q);
+    const float tie_dist = fabsf(fabsf(q - r) - 0.5f);  // q - r is exact (Sterbenz)
+    // NaN fails every comparison and so takes the exact path, as do subnormal inputs.
+    const bool ok = p.fast && tie_dist > 1e-4f && (fabsf(x) >= 1.17549435e-38f || x == 0.0f);
+    if (!ok) return quant1_f64(x, p);
+    int v = (int)r + p.zp;
+    v = v < 0 ? 0 : v;
+    v = v > 255 ? 255 : v;
+    return (uint32_t)v;
+}
+
 __device__ __forceinline__ uint32_t quant4(float4 v, const DqlParams& p) {
     return quant1(v.x, p) | (quant1(v.y, p) << 8) | (quant1(v.z, p) << 16) |
            (quant1(v.w, p) << 24);
+}
+
+__device__ __forceinline__ uint32_t bytesum4(uint32_t q) {
+    return __builtin_amdgcn_udot4(q, 0x01010101u, 0u, false);
+}
+
+// Slice of this block: `units` units of `unit` elements split as evenly as possible over
+// the grid; the last block also takes the `tail` elements past units * unit.
+struct Slice {
+    size_t e0, e1;
+};
+
+__device__ __forceinline__ Slice slice_of(size_t units, size_t unit, size_t tail) {
+    const size_t G = gridDim.x, b = blockIdx.x;
+    const size_t per = units / G, rem = units % G;
+    const size_t u0 = b * per + (b < rem ? b : rem);
+    const size_t u1 = u0 + per + (b < rem ? 1 : 0);
+    Slice s{u0 * unit, u1 * unit};
+    if (b == G - 1) s.e1 += tail;
+    return s;
 }
 
 // Reduce the partials of launch 1 (every block of launch 2 does this redundantly).
@@ -118,71 +173,70 @@ __device__ __forceinline__ DqlParams fold_partials(const float2* __restrict__ pa
     return make_params(mn, mx);
 }
 
+// `vec`: x is 16-byte aligned and unit % 4 == 0, so a slice is whole float4s (+ tail).
 __global__ void __launch_bounds__(kThreads)
-dql_minmax_kernel(const float* __restrict__ x, size_t n, int vec, float2* __restrict__ part) {
+dql_minmax_kernel(const float* __restrict__ x, size_t units, size_t unit, size_t tail, int vec,
+                  float2* __restrict__ part) {
+    const Slice sl = slice_of(units, unit, tail);
     float mn = 0.0f, mx = 0.0f;
-    const size_t tid = (size_t)blockIdx.x * kThreads + threadIdx.x;
-    const size_t stride = (size_t)gridDim.x * kThreads;
+    const size_t t = threadIdx.x;
+    size_t scalar_from = sl.e0;
     if (vec) {
         const float4* x4 = reinterpret_cast<const float4*>(x);
-        const size_t n4 = n / 4;
-        size_t i = tid;
-        for (; i + 3 * stride < n4; i += 4 * stride) {
-            float4 a = x4[i], b = x4[i + stride], c = x4[i + 2 * stride], d = x4[i + 3 * stride];
-            acc_minmax(a.x, mn, mx); acc_minmax(a.y, mn, mx); acc_minmax(a.z, mn, mx); acc_minmax(a.w, mn, mx);
-            acc_minmax(b.x, mn, mx); acc_minmax(b.y, mn, mx); acc_minmax(b.z, mn, mx); acc_minmax(b.w, mn, mx);
-            acc_minmax(c.x, mn, mx); acc_minmax(c.y, mn, mx); acc_minmax(c.z, mn, mx); acc_minmax(c.w, mn, mx);
-            acc_minmax(d.x, mn, mx); acc_minmax(d.y, mn, mx); acc_minmax(d.z, mn, mx); acc_minmax(d.w, mn, mx);
+        const size_t b4 = sl.e0 / 4, end4 = b4 + (sl.e1 - sl.e0) / 4;
+        size_t i = b4 + t;
+        for (; i + 3 * kThreads < end4; i += 4 * kThreads) {
+            const float4 a = x4[i], b = x4[i + kThreads], c = x4[i + 2 * kThreads],
+                         d = x4[i + 3 * kThreads];
+            acc4(a, mn, mx);
+            acc4(b, mn, mx);
+            acc4(c, mn, mx);
+            acc4(d, mn, mx);
         }
-        for (; i < n4; i += stride) {
-            float4 a = x4[i];
-            acc_minmax(a.x, mn, mx); acc_minmax(a.y, mn, mx); acc_minmax(a.z, mn, mx); acc_minmax(a.w, mn, mx);
-        }
-        for (size_t j = n4 * 4 + tid; j < n; j += stride) acc_minmax(x[j], mn, mx);
-    } else {
-        for (size_t j = tid; j < n; j += stride) acc_minmax(x[j], mn, mx);
+        for (; i < end4; i += kThreads) acc4(x4[i], mn, mx);
+        scalar_from = end4 * 4;
     }
+    for (size_t j = scalar_from + t; j < sl.e1; j += kThreads) acc_minmax(x[j], mn, mx);
     block_minmax(mn, mx);
     if (threadIdx.x == 0) part[blockIdx.x] = make_float2(mn, mx);
 }
 
+// Flat quantize of this block's slice: lane-consecutive float4 in, 4 bytes out.
+// `vec`: x 16-byte and y 4-byte aligned (unit == 4).
 __global__ void __launch_bounds__(kThreads)
-dql_quantize_flat_kernel(const float* __restrict__ x, size_t n, int vec, uint8_t* __restrict__ y,
-                         const float2* __restrict__ part, int G, float* __restrict__ y_scale,
-                         uint8_t* __restrict__ y_zp) {
+dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size_t tail, int vec,
+                    uint8_t* __restrict__ y, const float2* __restrict__ part, int G,
+                    float* __restrict__ y_scale, uint8_t* __restrict__ y_zp) {
     const DqlParams p = fold_partials(part, G);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         *y_scale = (float)p.s;
         *y_zp = (uint8_t)p.zp;
     }
-    const size_t tid = (size_t)blockIdx.x * kThreads + threadIdx.x;
-    const size_t stride = (size_t)gridDim.x * kThreads;
+    const Slice sl = slice_of(units, unit, tail);
+    const size_t t = threadIdx.x;
+    size_t scalar_from = sl.e0;
     if (vec) {
-        // 16 elements per lane per step: four float4 loads, one 16-byte store.
         const float4* x4 = reinterpret_cast<const float4*>(x);
-        uint4* y16 = reinterpret_cast<uint4*>(y);
-        const size_t n16 = n / 16;
-        for (size_t i = tid; i < n16; i += stride) {
-            float4 a = x4[4 * i], b = x4[4 * i + 1], c = x4[4 * i + 2], d = x4[4 * i + 3];
-            uint4 o;
-            if (p.zero) {
-                o = make_uint4(0, 0, 0, 0);
-            } else {
-                o.x = quant4(a, p);
-                o.y = quant4(b, p);
-                o.z = quant4(c, p);
-                o.w = quant4(d, p);
-            }
-            y16[i] = o;
+        uint32_t* y4 = reinterpret_cast<uint32_t*>(y);
+        const size_t b4 = sl.e0 / 4, end4 = b4 + (sl.e1 - sl.e0) / 4;
+        size_t i = b4 + t;
+        for (; i + 3 * kThreads < end4; i += 4 * kThreads) {
+            const float4 a = x4[i], b = x4[i + kThreads], c = x4[i + 2 * kThreads],
+                         d = x4[i + 3 * kThreads];
+            y4[i] = quant4(a, p);
+            y4[i + kThreads] = quant4(b, p);
+            y4[i + 2 * kThreads] = quant4(c, p);
+            y4[i + 3 * kThreads] = quant4(d, p);
         }
-        for (size_t j = n16 * 16 + tid; j < n; j += stride)
-            y[j] = p.zero ? 0 : (uint8_t)quant1(x[j], p);
-    } else {
-        for (size_t j = tid; j < n; j += stride) y[j] = p.zero ? 0 : (uint8_t)quant1(x[j], p);
+        for (; i < end4; i += kThreads) y4[i] = quant4(x4[i], p);
+        scalar_from = end4 * 4;
     }
+    for (size_t j = scalar_from + t; j < sl.e1; j += kThreads) y[j] = (uint8_t)quant1(x[j], p);
 }
 
-// One wave per row; also emits the row sums of y (u8 summed as int32).
+// Row mode: the slices are whole rows; one wave per row at a time, and the row sums of y
+// (u8 summed as int32) are written too.  `vec`: x 16-byte and y 4-byte aligned and
+// row_len % 4 == 0.
 __global__ void __launch_bounds__(kThreads)
 dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_len, int vec,
                          uint8_t* __restrict__ y, int32_t* __restrict__ rowsum,
@@ -193,25 +247,35 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
         *y_scale = (float)p.s;
         *y_zp = (uint8_t)p.zp;
     }
-    const int lane = threadIdx.x & 63;
-    const size_t wave = (size_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    const size_t nwaves = (size_t)gridDim.x * (kThreads / 64);
-    for (size_t r = wave; r < rows; r += nwaves) {
+    const Slice sl = slice_of(rows, 1, 0);  // a range of rows
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    for (size_t r = sl.e0 + wid; r < sl.e1; r += kThreads / 64) {
         const float* xr = x + r * row_len;
         uint8_t* yr = y + r * row_len;
         uint32_t s = 0;
         if (vec) {
             const float4* x4 = reinterpret_cast<const float4*>(xr);
             uint32_t* y4 = reinterpret_cast<uint32_t*>(yr);
-#pragma unroll 4
-            for (size_t i = lane; i < row_len / 4; i += 64) {
-                uint32_t q = p.zero ? 0u : quant4(x4[i], p);
+            const size_t n4 = row_len / 4;
+            size_t i = lane;
+            for (; i + 3 * 64 < n4; i += 4 * 64) {
+                const float4 a = x4[i], b = x4[i + 64], c = x4[i + 128], d = x4[i + 192];
+                const uint32_t qa = quant4(a, p), qb = quant4(b, p), qc = quant4(c, p),
+                               qd = quant4(d, p);
+                y4[i] = qa;
+                y4[i + 64] = qb;
+                y4[i + 128] = qc;
+                y4[i + 192] = qd;
+                s += bytesum4(qa) + bytesum4(qb) + bytesum4(qc) + bytesum4(qd);
+            }
+            for (; i < n4; i += 64) {
+                const uint32_t q = quant4(x4[i], p);
                 y4[i] = q;
-                s += (q & 0xFF) + ((q >> 8) & 0xFF) + ((q >> 16) & 0xFF) + (q >> 24);
+                s += bytesum4(q);
             }
         } else {
             for (size_t i = lane; i < row_len; i += 64) {
-                uint32_t q = p.zero ? 0u : quant1(xr[i], p);
+                const uint32_t q = quant1(xr[i], p);
                 yr[i] = (uint8_t)q;
                 s += q;
             }
@@ -224,7 +288,7 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
 
 }  // namespace
 
-extern "C" size_t icx_dql_workspace_size(size_t) { return sizeof(float2) * kMaxPartials; }
+extern "C" size_t icx_dql_workspace_size(size_t) { return sizeof(float2) * kMaxBlocks; }
 
 extern "C" int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, size_t n,
                                            uint8_t* y, float* y_scale, uint8_t* y_zp,
@@ -241,25 +305,44 @@ extern "C" int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, 
                  row_len, n);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     float2* part = reinterpret_cast<float2*>(ws);
-    const int vec = icx::aligned16(x) ? 1 : 0;
-    // Launch 1: enough blocks for ~16 float4 per lane, capped at kMaxPartials.
-    int G = (int)std::min<size_t>(kMaxPartials, std::max<size_t>(1, icx::cdiv(n, (size_t)kThreads * 16)));
-    hipLaunchKernelGGL(dql_minmax_kernel, dim3(G), dim3(kThreads), 0, s, x, n, vec, part);
+    const bool x16 = icx::aligned16(x), y4 = (reinterpret_cast<uintptr_t>(y) & 3u) == 0;
+    // Partition: rows in row mode, float4 groups (or single elements) otherwise.  Both
+    // launches use the same grid, so block b reads the same slice twice; ~4 float4 per lane.
+    size_t units, unit, tail;
+    if (opt_rowsum) {
+        units = n / row_len;
+        unit = row_len;
+        tail = 0;
+    } else if (x16 && y4) {
+        units = n / 4;
+        unit = 4;
+        tail = n % 4;
+    } else {
+        units = n;
+        unit = 1;
+        tail = 0;
+    }
+    size_t want = icx::cdiv(n, (size_t)kThreads * 16);
+    if (opt_rowsum) {
+        // the same number of rows for every wave: rows_per_wave * 4 waves per block
+        const size_t rpw = std::max<size_t>(1, icx::cdiv(units, (size_t)4 * kMaxBlocks));
+        want = icx::cdiv(units, 4 * rpw);
+    }
+    const int G = (int)std::max<size_t>(1, std::min<size_t>({(size_t)kMaxBlocks, want, units}));
+    const int vec1 = (x16 && unit % 4 == 0) ? 1 : 0;
+    hipLaunchKernelGGL(dql_minmax_kernel, dim3(G), dim3(kThreads), 0, s, x, units, unit, tail,
+                       vec1, part);
     ICX_LAUNCH_CHECK("dql_minmax_kernel");
     if (opt_rowsum) {
-        const size_t rows = n / row_len;
-        const int rvec =
-            (vec && row_len % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 3u) == 0) ? 1 : 0;
-        const int blocks = (int)std::min<size_t>(2048, std::max<size_t>(1, icx::cdiv(rows, kThreads / 64)));
-        hipLaunchKernelGGL(dql_quantize_rows_kernel, dim3(blocks), dim3(kThreads), 0, s, x, rows,
+        const int rvec = (x16 && y4 && row_len % 4 == 0) ? 1 : 0;
+        hipLaunchKernelGGL(dql_quantize_rows_kernel, dim3(G), dim3(kThreads), 0, s, x, units,
                            row_len, rvec, y, opt_rowsum, part, G, y_scale, y_zp);
         ICX_LAUNCH_CHECK("dql_quantize_rows_kernel");
     } else {
-        const int qvec = (vec && icx::aligned16(y)) ? 1 : 0;
-        const int blocks = (int)std::min<size_t>(2048, std::max<size_t>(1, icx::cdiv(n, (size_t)kThreads * 16)));
-        hipLaunchKernelGGL(dql_quantize_flat_kernel, dim3(blocks), dim3(kThreads), 0, s, x, n, qvec,
-                           y, part, G, y_scale, y_zp);
-        ICX_LAUNCH_CHECK("dql_quantize_flat_kernel");
+        const int qvec = (x16 && y4 && unit == 4) ? 1 : 0;
+        hipLaunchKernelGGL(dql_quantize_kernel, dim3(G), dim3(kThreads), 0, s, x, units, unit,
+                           tail, qvec, y, part, G, y_scale, y_zp);
+        ICX_LAUNCH_CHECK("dql_quantize_kernel");
     }
     return ICX_OK;
 }

@@ -68,12 +68,12 @@ chain_cols_kernel(const float4* __restrict__ X, uint32_t n4, uint32_t cols4, icx
         for (int u = 0; u < 4; ++u) v[u] = X[i + u * stride];
         icx::run_chain4(codes, ch.n_ops, v, opnd);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) Y[i + u * stride] = v[u];
+        for (int u = 0; u < 4; ++u) icx::store_nt(&Y[i + u * stride], v[u]);
     }
     for (; i < n4; i += stride) {
         float4 v[1] = {X[i]};
         icx::run_chain4(codes, ch.n_ops, v, opnd);
-        Y[i] = v[0];
+        icx::store_nt(&Y[i], v[0]);
     }
 }
 
@@ -150,7 +150,7 @@ extern "C" int icx_fused_chain_f32(icx_stream_t stream, const float* X, size_t r
     size_t g = 1, a = kThreads, bq = cols4;
     while (bq) { size_t tt = a % bq; a = bq; bq = tt; }  // a = gcd(256, cols4)
     const size_t unit_blocks = cols4 ? cols4 / a : 1;    // lcm(256, cols4) / 256
-    if (cols4) g = std::max<size_t>(1, 2048 / unit_blocks) * unit_blocks;
+    if (cols4) g = std::max<size_t>(1, 1024 / unit_blocks) * unit_blocks;
     if (cols % 4 == 0 && cols4 > 0 && icx::aligned16(X) && icx::aligned16(Y) &&
         n / 4 < 0x7fffffffull && icx::chain_is_col_only(*chain) && unit_blocks <= 8192) {
         hipLaunchKernelGGL(chain_cols_kernel, dim3((unsigned)g), dim3(kThreads), 0, s,

