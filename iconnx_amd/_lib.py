@@ -13,6 +13,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "iconnx_hip.h")
 
 ICX_I8, ICX_U8, ICX_I32, ICX_F32 = 0, 1, 2, 3
 OP_ADD, OP_SUB, OP_MUL, OP_DIV = 0, 1, 2, 3
+OP_ERF, OP_SAVE, OP_MUL_SAVED = 4, 5, 6
 BCAST_SCALAR, BCAST_COL, BCAST_ROW, BCAST_FULL = 0, 1, 2, 3
 MAX_CHAIN = 8
 
@@ -54,6 +55,11 @@ SIGNATURES = {
     "icx_qlinear_f32": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, ctypes.POINTER(Chain), P, P, S], I),
     "icx_cast_i32_f32": ([P, P, S, P], I),
     "icx_dequantize_linear_f32": ([P, P, I, P, P, S, S, S, P], I),
+    "icx_layer_norm_f32": ([P, P, P, S, S, P, P, ctypes.c_float, P], I),
+    "icx_softmax_f32": ([P, P, S, S, P], I),
+    "icx_transpose": ([P, P, S, I, P, P, P], I),
+    "icx_matmul_f32": ([P, P, P, S, I, S, S, S, P], I),
+    "icx_attention_f32": ([P, P, P, P, S, S, S, S, S, S, S, S, ctypes.c_float, I, I, P], I),
     "icx_graph_create": ([], P),
     "icx_graph_destroy": ([P], None),
     "icx_graph_add_input": ([P, C, I, P], I),

@@ -28,8 +28,26 @@ __device__ __forceinline__ float load_bcast(const float* p, int kind, size_t r, 
     }
 }
 
+__device__ __forceinline__ bool op_takes_operand(int op) { return op <= ICX_OP_DIV; }
+
+// erf as the reference evaluates it (src/operators/erf.rs:21-31): Abramowitz-Stegun 7.1.26
+// in f32, one rounding per operation, with the device expf.
+__device__ __forceinline__ float erf_ref(float x) {
+    const float sign = (x != x) ? x : (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : copysignf(1.0f, x)));
+    const float a = fabsf(x);
+    const float t = __fdiv_rn(1.0f, __fadd_rn(1.0f, __fmul_rn(0.3275911f, a)));
+    float p = __fsub_rn(__fmul_rn(1.0614054f, t), 1.4531521f);
+    p = __fadd_rn(__fmul_rn(p, t), 1.4214138f);
+    p = __fsub_rn(__fmul_rn(p, t), 0.28449672f);
+    p = __fadd_rn(__fmul_rn(p, t), 0.2548296f);
+    const float e = expf(__fmul_rn(-a, a));
+    const float y = __fsub_rn(1.0f, __fmul_rn(__fmul_rn(p, t), e));
+    return __fmul_rn(sign, y);
+}
+
 __device__ __forceinline__ float chain_operand(const icx_chain_op& op, size_t r, size_t c,
                                                size_t cols) {
+    if (!op_takes_operand(op.op)) return 0.0f;
     float a = load_bcast(op.p0, op.kind0, r, c, cols);
     if (op.p1) a = __fmul_rn(a, load_bcast(op.p1, op.kind1, r, c, cols));
     return a;
@@ -48,11 +66,22 @@ __device__ __forceinline__ float apply_one(const icx_chain_op& op, float v, floa
     return op.operand_is_lhs ? apply_binary(op.op, o, v) : apply_binary(op.op, v, o);
 }
 
+// One step including the operand-free ones; `s` is the saved value.
+__device__ __forceinline__ float step_one(const icx_chain_op& op, float v, float o, float& s) {
+    switch (op.op) {
+        case ICX_OP_ERF: return erf_ref(v);
+        case ICX_OP_SAVE: s = v; return v;
+        case ICX_OP_MUL_SAVED: return __fmul_rn(s, v);
+        default: return apply_one(op, v, o);
+    }
+}
+
 __device__ __forceinline__ float apply_chain(const icx_chain& ch, float v, size_t r, size_t c,
                                              size_t cols) {
+    float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < ICX_MAX_CHAIN; ++i)
-        if (i < ch.n_ops) v = apply_one(ch.ops[i], v, chain_operand(ch.ops[i], r, c, cols));
+        if (i < ch.n_ops) v = step_one(ch.ops[i], v, chain_operand(ch.ops[i], r, c, cols), s);
     return v;
 }
 
@@ -65,7 +94,7 @@ __device__ __forceinline__ void load_col_operands(const icx_chain& ch, size_t c,
                                                   float (&o)[ICX_MAX_CHAIN]) {
 #pragma unroll
     for (int i = 0; i < ICX_MAX_CHAIN; ++i) {
-        if (i < ch.n_ops) {
+        if (i < ch.n_ops && op_takes_operand(ch.ops[i].op)) {
             const icx_chain_op& op = ch.ops[i];
             float a = col_factor(op.p0, op.kind0, c);
             if (op.p1) a = __fmul_rn(a, col_factor(op.p1, op.kind1, c));
@@ -78,22 +107,30 @@ __device__ __forceinline__ void load_col_operands(const icx_chain& ch, size_t c,
 
 __device__ __forceinline__ float apply_loaded(const icx_chain& ch, float v,
                                               const float (&o)[ICX_MAX_CHAIN]) {
+    float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < ICX_MAX_CHAIN; ++i)
-        if (i < ch.n_ops) v = apply_one(ch.ops[i], v, o[i]);
+        if (i < ch.n_ops) v = step_one(ch.ops[i], v, o[i], s);
     return v;
 }
 
 // ---- op-major evaluation over a register block of float4 values ------------------------
-// The op codes of a chain packed 4 bits per op: bits [1:0] = ICX_OP_*, bit 2 = operand on
+// The op codes of a chain packed 4 bits per op: bits [2:0] = ICX_OP_*, bit 3 = operand on
 // the left.  One uniform switch per op, then straight-line IEEE ops over every value the
 // lane holds — no per-element branching.  `opnd(k)` returns the float4 operand of op k for
-// the lane's 4 columns.
+// the lane's 4 columns (unused by the operand-free ops).
 __host__ __device__ inline uint32_t chain_codes(const icx_chain& ch) {
     uint32_t c = 0;
     for (int i = 0; i < ch.n_ops; ++i)
-        c |= (uint32_t)((ch.ops[i].op & 3) | (ch.ops[i].operand_is_lhs ? 4 : 0)) << (4 * i);
+        c |= (uint32_t)((ch.ops[i].op & 7) | (ch.ops[i].operand_is_lhs ? 8 : 0)) << (4 * i);
     return c;
+}
+
+// 0 when every step is a binary op, 2 when an operand-free step (erf / save) occurs.
+inline int chain_mode(const icx_chain& ch) {
+    for (int i = 0; i < ch.n_ops; ++i)
+        if (ch.ops[i].op > ICX_OP_DIV) return 2;
+    return 0;
 }
 
 #define ICX_EW4(expr)                                   \
@@ -104,30 +141,56 @@ __host__ __device__ inline uint32_t chain_codes(const icx_chain& ch) {
         { float& x = v[u].w; const float y = o.w; x = (expr); } \
     }
 
-template <int NV, typename OpndFn>
+// Operand-free steps over the whole block; `sv` holds the saved values.
+#define ICX_EW4S(stmt)                                                  \
+    _Pragma("unroll") for (int u = 0; u < NV; ++u) {                    \
+        { float& x = v[u].x; float& z = sv[u].x; stmt; }                \
+        { float& x = v[u].y; float& z = sv[u].y; stmt; }                \
+        { float& x = v[u].z; float& z = sv[u].z; stmt; }                \
+        { float& x = v[u].w; float& z = sv[u].w; stmt; }                \
+    }
+
+// MODE 0: the four binary ops only (no extra registers, no erf code); MODE 2: also the
+// operand-free steps (erf, save, multiply by the saved value).  The host picks the mode
+// with chain_mode(), so kernels without a GELU-style chain do not pay for it.
+template <int MODE, int NV, typename OpndFn>
 __device__ __forceinline__ void run_chain4(uint32_t codes, int n_ops, float4 (&v)[NV],
                                            OpndFn opnd) {
+    float4 sv[MODE == 2 ? NV : 1];
 #pragma unroll 1
     for (int k = 0; k < n_ops; ++k) {
+        const uint32_t code = (codes >> (4 * k)) & 15u;
+        if constexpr (MODE == 2) {
+            if ((code & 7u) > ICX_OP_DIV) {
+                switch (code & 7u) {
+                    case ICX_OP_SAVE: ICX_EW4S(z = x) break;
+                    case ICX_OP_MUL_SAVED: ICX_EW4S(x = __fmul_rn(z, x)) break;
+                    default: ICX_EW4S(x = erf_ref(x)) break;
+                }
+                continue;
+            }
+        }
         const float4 o = opnd(k);
-        switch ((codes >> (4 * k)) & 7u) {
+        switch (code) {
             case ICX_OP_ADD: ICX_EW4(__fadd_rn(x, y)) break;
-            case ICX_OP_ADD | 4: ICX_EW4(__fadd_rn(y, x)) break;
+            case ICX_OP_ADD | 8: ICX_EW4(__fadd_rn(y, x)) break;
             case ICX_OP_SUB: ICX_EW4(__fsub_rn(x, y)) break;
-            case ICX_OP_SUB | 4: ICX_EW4(__fsub_rn(y, x)) break;
+            case ICX_OP_SUB | 8: ICX_EW4(__fsub_rn(y, x)) break;
             case ICX_OP_MUL: ICX_EW4(__fmul_rn(x, y)) break;
-            case ICX_OP_MUL | 4: ICX_EW4(__fmul_rn(y, x)) break;
+            case ICX_OP_MUL | 8: ICX_EW4(__fmul_rn(y, x)) break;
             case ICX_OP_DIV: ICX_EW4(__fdiv_rn(x, y)) break;
             default: ICX_EW4(__fdiv_rn(y, x)) break;
         }
     }
 }
 #undef ICX_EW4
+#undef ICX_EW4S
 
 // Host side: true when every operand factor is a scalar or a [cols] vector.
 inline bool chain_is_col_only(const icx_chain& ch) {
     for (int i = 0; i < ch.n_ops; ++i) {
         const icx_chain_op& o = ch.ops[i];
+        if (o.op > ICX_OP_DIV) continue;
         if (o.kind0 != ICX_BCAST_SCALAR && o.kind0 != ICX_BCAST_COL) return false;
         if (o.p1 && o.kind1 != ICX_BCAST_SCALAR && o.kind1 != ICX_BCAST_COL) return false;
     }

@@ -24,8 +24,9 @@ int validate_chain(const icx_chain* ch, const char* who) {
                  ICX_MAX_CHAIN);
     for (int i = 0; i < ch->n_ops; ++i) {
         const icx_chain_op& o = ch->ops[i];
-        if (o.op < ICX_OP_ADD || o.op > ICX_OP_DIV)
+        if (o.op < ICX_OP_ADD || o.op > ICX_OP_MUL_SAVED)
             ICX_FAIL(ICX_ERR_INVALID_ARG, "%s: chain op %d has unknown op code %d", who, i, o.op);
+        if (o.op > ICX_OP_DIV) continue;  // operand-free step
         if (!o.p0) ICX_FAIL(ICX_ERR_INVALID_ARG, "%s: chain op %d has a null operand", who, i);
         if (o.kind0 < ICX_BCAST_SCALAR || o.kind0 > ICX_BCAST_FULL ||
             (o.p1 && (o.kind1 < ICX_BCAST_SCALAR || o.kind1 > ICX_BCAST_FULL)))
@@ -45,6 +46,7 @@ constexpr int kThreads = 256;
 // chain operands are computed once into a thread-private LDS slot, and each step is four
 // float4 loads in flight, the chain applied op by op (one uniform branch per op, straight
 // IEEE arithmetic over the 16 values) and four float4 stores.
+template <int MODE>
 __global__ void __launch_bounds__(kThreads)
 chain_cols_kernel(const float4* __restrict__ X, uint32_t n4, uint32_t cols4, icx_chain ch,
                   uint32_t codes, float4* __restrict__ Y) {
@@ -66,13 +68,13 @@ chain_cols_kernel(const float4* __restrict__ X, uint32_t n4, uint32_t cols4, icx
         float4 v[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) v[u] = X[i + u * stride];
-        icx::run_chain4(codes, ch.n_ops, v, opnd);
+        icx::run_chain4<MODE>(codes, ch.n_ops, v, opnd);
 #pragma unroll
         for (int u = 0; u < 4; ++u) icx::store_nt(&Y[i + u * stride], v[u]);
     }
     for (; i < n4; i += stride) {
         float4 v[1] = {X[i]};
-        icx::run_chain4(codes, ch.n_ops, v, opnd);
+        icx::run_chain4<MODE>(codes, ch.n_ops, v, opnd);
         icx::store_nt(&Y[i], v[0]);
     }
 }
@@ -153,9 +155,14 @@ extern "C" int icx_fused_chain_f32(icx_stream_t stream, const float* X, size_t r
     if (cols4) g = std::max<size_t>(1, 1024 / unit_blocks) * unit_blocks;
     if (cols % 4 == 0 && cols4 > 0 && icx::aligned16(X) && icx::aligned16(Y) &&
         n / 4 < 0x7fffffffull && icx::chain_is_col_only(*chain) && unit_blocks <= 8192) {
-        hipLaunchKernelGGL(chain_cols_kernel, dim3((unsigned)g), dim3(kThreads), 0, s,
-                           reinterpret_cast<const float4*>(X), (uint32_t)(n / 4), (uint32_t)cols4,
-                           *chain, icx::chain_codes(*chain), reinterpret_cast<float4*>(Y));
+        if (icx::chain_mode(*chain) == 2)
+            hipLaunchKernelGGL(chain_cols_kernel<2>, dim3((unsigned)g), dim3(kThreads), 0, s,
+                               reinterpret_cast<const float4*>(X), (uint32_t)(n / 4), (uint32_t)cols4,
+                               *chain, icx::chain_codes(*chain), reinterpret_cast<float4*>(Y));
+        else
+            hipLaunchKernelGGL(chain_cols_kernel<0>, dim3((unsigned)g), dim3(kThreads), 0, s,
+                               reinterpret_cast<const float4*>(X), (uint32_t)(n / 4), (uint32_t)cols4,
+                               *chain, icx::chain_codes(*chain), reinterpret_cast<float4*>(Y));
         ICX_LAUNCH_CHECK("chain_cols_kernel");
     } else {
         hipLaunchKernelGGL(chain_scalar_kernel, dim3(grid_for(n, kThreads * 4, 8192)), dim3(kThreads),

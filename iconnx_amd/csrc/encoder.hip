@@ -1,0 +1,438 @@
+// fp32 ops around the quantized linears of a DistilBERT-shaped encoder, on gfx950:
+//
+//   LayerNormalization (last axis, optionally of x + residual)
+//       src/operators/layer_normalization.rs:25-80 — eight lanes per row, each summing the
+//       strided slice x[j], x[j+8], ... in order, combined as ndarray 0.16's unrolled_fold
+//       does (the reference's mean_axis over a contiguous axis); every step one f32
+//       rounding, so the result is bit-identical to that restatement.
+//   Softmax (last axis)            src/operators/softmax.rs:25-40, same reduction layout.
+//   Transpose (rank <= 6)          src/operators/transpose.rs:10-40.
+//   MatMul f32 (batched)           src/operators/matmul.rs:20-150; LDS-tiled FMA kernel.
+//   Attention (fused)              the decomposed Reshape/Transpose/MatMul/scale/Softmax/
+//       MatMul/Transpose/Reshape subgraph of a BERT self-attention, over [B, S, H*D]
+//       activations, with fp32 MFMA (v_mfma_f32_32x32x2f32) and the softmax in registers.
+#include "icx_common.hpp"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// ---- row reductions in the unrolled_fold order ------------------------------------------
+// Lane j (0..7) of an 8-lane group holds partial p_j; every lane of the group returns
+// acc = 0 + (p0+p4) + (p1+p5) + (p2+p6) + (p3+p7), before the leftover elements.
+__device__ __forceinline__ float combine8(float p) {
+    const float p0 = __shfl(p, 0, 8), p1 = __shfl(p, 1, 8), p2 = __shfl(p, 2, 8),
+                p3 = __shfl(p, 3, 8), p4 = __shfl(p, 4, 8), p5 = __shfl(p, 5, 8),
+                p6 = __shfl(p, 6, 8), p7 = __shfl(p, 7, 8);
+    float acc = 0.0f;
+    acc = __fadd_rn(acc, __fadd_rn(p0, p4));
+    acc = __fadd_rn(acc, __fadd_rn(p1, p5));
+    acc = __fadd_rn(acc, __fadd_rn(p2, p6));
+    acc = __fadd_rn(acc, __fadd_rn(p3, p7));
+    return acc;
+}
+
+__device__ __forceinline__ float ln_in(const float* x, const float* res, size_t i) {
+    return res ? __fadd_rn(x[i], res[i]) : x[i];
+}
+
+// 32 rows per block: 8 rows per wave, 8 lanes per row.
+__global__ void __launch_bounds__(kThreads)
+layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t rows,
+                  size_t cols, const float* __restrict__ scale, const float* __restrict__ bias,
+                  float eps, float* __restrict__ y) {
+    const int lane = threadIdx.x & 63, j = lane & 7;
+    const size_t row = (size_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    if (row >= rows) return;  // a whole 8-lane group leaves together
+    const float* xr = x + row * cols;
+    const float* rr = res ? res + row * cols : nullptr;
+    const size_t n8 = cols / 8 * 8;
+    const float fcols = (float)cols;
+    // mean
+    float p = 0.0f;
+    for (size_t i = j; i < n8; i += 8) p = __fadd_rn(p, ln_in(xr, rr, i));
+    float acc = combine8(p);
+    for (size_t i = n8; i < cols; ++i) acc = __fadd_rn(acc, ln_in(xr, rr, i));
+    const float mean = __fdiv_rn(acc, fcols);
+    // variance of the centred values
+    p = 0.0f;
+    for (size_t i = j; i < n8; i += 8) {
+        const float c = __fsub_rn(ln_in(xr, rr, i), mean);
+        p = __fadd_rn(p, __fmul_rn(c, c));
+    }
+    acc = combine8(p);
+    for (size_t i = n8; i < cols; ++i) {
+        const float c = __fsub_rn(ln_in(xr, rr, i), mean);
+        acc = __fadd_rn(acc, __fmul_rn(c, c));
+    }
+    const float var = __fdiv_rn(acc, fcols);
+    const float sd = sqrtf(__fadd_rn(var, eps));  // correctly rounded (build flag), as f32::sqrt
+    float* yr = y + row * cols;
+    for (size_t i = j; i < cols; i += 8) {
+        const float c = __fsub_rn(ln_in(xr, rr, i), mean);
+        yr[i] = __fadd_rn(__fmul_rn(__fdiv_rn(c, sd), scale[i]), bias[i]);
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+softmax_kernel(const float* __restrict__ x, size_t rows, size_t cols, float* __restrict__ y) {
+    const int lane = threadIdx.x & 63, j = lane & 7;
+    const size_t row = (size_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    if (row >= rows) return;
+    const float* xr = x + row * cols;
+    float* yr = y + row * cols;
+    float m = -INFINITY;
+    for (size_t i = j; i < cols; i += 8) m = fmaxf(m, xr[i]);  // NaN-ignoring, as f32::max
+#pragma unroll
+    for (int o = 4; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 8));
+    const size_t n8 = cols / 8 * 8;
+    float p = 0.0f;
+    for (size_t i = j; i < n8; i += 8) {
+        const float e = expf(__fsub_rn(xr[i], m));
+        yr[i] = e;
+        p = __fadd_rn(p, e);
+    }
+    float acc = combine8(p);
+    for (size_t i = n8; i < cols; ++i) {
+        const float e = expf(__fsub_rn(xr[i], m));
+        if (j == 0) yr[i] = e;
+        acc = __fadd_rn(acc, e);
+    }
+    // each lane reads back only the values it wrote itself (the tail belongs to lane 0)
+    for (size_t i = j; i < n8; i += 8) yr[i] = __fdiv_rn(yr[i], acc);
+    if (j == 0)
+        for (size_t i = n8; i < cols; ++i) yr[i] = __fdiv_rn(yr[i], acc);
+}
+
+// ---- transpose ---------------------------------------------------------------------------
+struct TransposeArgs {
+    int rank;
+    int64_t out_dims[6];
+    int64_t in_stride_of_out[6];  // input stride of output axis d
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+transpose_kernel(const T* __restrict__ x, size_t n, TransposeArgs a, T* __restrict__ y) {
+    const size_t stride = (size_t)gridDim.x * kThreads;
+    for (size_t o = (size_t)blockIdx.x * kThreads + threadIdx.x; o < n; o += stride) {
+        size_t rem = o, src = 0;
+        for (int d = a.rank - 1; d >= 0; --d) {
+            const size_t idx = rem % (size_t)a.out_dims[d];
+            rem /= (size_t)a.out_dims[d];
+            src += idx * (size_t)a.in_stride_of_out[d];
+        }
+        y[o] = x[src];
+    }
+}
+
+// ---- batched f32 matmul: 64x64 tiles, 4x4 outputs per thread, K step 16 -----------------
+__global__ void __launch_bounds__(kThreads)
+matmul_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, int M, int K, int N,
+                  int b_broadcast, int tiles_n, float* __restrict__ C) {
+    __shared__ float sa[16][64 + 4];
+    __shared__ float sb[16][64 + 4];
+    const int batch = blockIdx.y;
+    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+    const float* a = A + (size_t)batch * M * K;
+    const float* b = B + (b_broadcast ? 0 : (size_t)batch * K * N);
+    float* c = C + (size_t)batch * M * N;
+    const int t = threadIdx.x, tr = t / 16, tc = t % 16;
+    const int m0 = tm * 64, n0 = tn * 64;
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < K; k0 += 16) {
+        for (int i = t; i < 16 * 64; i += kThreads) {
+            const int kk = i % 16, mm = i / 16;  // A tile stored k-major
+            const int gm = m0 + mm, gk = k0 + kk;
+            sa[kk][mm] = (gm < M && gk < K) ? a[(size_t)gm * K + gk] : 0.0f;
+            const int nn = i % 64, kb = i / 64;
+            const int gn = n0 + nn, gk2 = k0 + kb;
+            sb[kb][nn] = (gn < N && gk2 < K) ? b[(size_t)gk2 * N + gn] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                av[u] = sa[kk][tr * 4 + u];
+                bv[u] = sb[kk][tc * 4 + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[u][v] = fmaf(av[u], bv[v], acc[u][v]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int gm = m0 + tr * 4 + u;
+        if (gm >= M) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int gn = n0 + tc * 4 + v;
+            if (gn < N) c[(size_t)gm * N + gn] = acc[u][v];
+        }
+    }
+}
+
+// ---- fused self-attention, S <= 128, D == 64 --------------------------------------------
+// One block per (batch, head), 4 waves; wave w owns query rows [32w, 32w + 32).
+//   scores = (Q K^T) (*|/) scale   (or Q scaled first)  — 4 tiles of 32x32, K = 64
+//   P = softmax over the keys, in registers (lanes of a half-wave hold one row's columns)
+//   ctx = P V                                            — 2 tiles of 32x32, K = S
+// v_mfma_f32_32x32x2f32: A lane l = A[l % 32][l / 32], B lane l = B[l / 32][l % 32],
+// D register r of lane l = D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int ATT_S = 128, ATT_D = 64;
+constexpr int QK_STRIDE = ATT_D + 1;   // floats per LDS row of Q, K, V (bank-conflict free)
+constexpr int P_STRIDE = ATT_S + 1;
+
+struct AttnArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* out;
+    int S, H;
+    int64_t ldq, ldk, ldv, ldo;  // row strides (elements) of the [B*S, *] activations
+    float scale;
+    int scale_div;  // 1: x / scale, 0: x * scale
+    int scale_q;    // 1: applied to Q before the product, 0: to the scores
+};
+
+__device__ __forceinline__ float apply_scale(float x, const AttnArgs& a) {
+    return a.scale_div ? __fdiv_rn(x, a.scale) : __fmul_rn(x, a.scale);
+}
+
+__global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
+    extern __shared__ float smem[];
+    float* sq = smem;                        // [128][65]
+    float* sk = sq + ATT_S * QK_STRIDE;      // [128][65]
+    float* sv = sk + ATT_S * QK_STRIDE;      // [128][65]
+    float* sp = smem;                        // [128][129], over Q and K once they are read
+    const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int S = a.S;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int lr = lane & 31, lh = lane >> 5;
+
+    // load Q, K, V of (b, h): rows past S are zero
+    for (int i = t; i < ATT_S * (ATT_D / 4); i += kThreads) {
+        const int r = i / (ATT_D / 4), c4 = (i % (ATT_D / 4)) * 4;
+        float4 qv = make_float4(0, 0, 0, 0), kv = qv, vv = qv;
+        if (r < S) {
+            const size_t row = (size_t)b * S + r;
+            qv = *reinterpret_cast<const float4*>(a.q + row * a.ldq + h * ATT_D + c4);
+            kv = *reinterpret_cast<const float4*>(a.k + row * a.ldk + h * ATT_D + c4);
+            vv = *reinterpret_cast<const float4*>(a.v + row * a.ldv + h * ATT_D + c4);
+            if (a.scale_q) {
+                qv.x = apply_scale(qv.x, a);
+                qv.y = apply_scale(qv.y, a);
+                qv.z = apply_scale(qv.z, a);
+                qv.w = apply_scale(qv.w, a);
+            }
+        }
+        float* dq = sq + r * QK_STRIDE + c4;
+        float* dk = sk + r * QK_STRIDE + c4;
+        float* dv = sv + r * QK_STRIDE + c4;
+        dq[0] = qv.x; dq[1] = qv.y; dq[2] = qv.z; dq[3] = qv.w;
+        dk[0] = kv.x; dk[1] = kv.y; dk[2] = kv.z; dk[3] = kv.w;
+        dv[0] = vv.x; dv[1] = vv.y; dv[2] = vv.z; dv[3] = vv.w;
+    }
+    __syncthreads();
+
+    // scores for rows [32w, 32w+32) x 128 keys
+    v16f acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+    const int qrow = 32 * w + lr;
+#pragma unroll 4
+    for (int k2 = 0; k2 < ATT_D / 2; ++k2) {
+        const int kk = 2 * k2 + lh;
+        const float av = sq[qrow * QK_STRIDE + kk];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float bv = sk[(32 * j + lr) * QK_STRIDE + kk];
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[j], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // Q and K are no longer read: P may overwrite them
+
+    // softmax of each row; row of register r in this half-wave: 32w + 8(r/4) + 4 lh + r%4
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        float s[4];
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = 32 * j + lr;
+            s[j] = a.scale_q ? acc[j][r] : apply_scale(acc[j][r], a);
+            if (col >= S) s[j] = -INFINITY;
+            m = fmaxf(m, s[j]);
+        }
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 32));
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s[j] = expf(__fsub_rn(s[j], m));
+            sum = __fadd_rn(sum, s[j]);
+        }
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, o, 32));
+        const int row = 32 * w + 8 * (r / 4) + 4 * lh + (r % 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sp[row * P_STRIDE + 32 * j + lr] = __fdiv_rn(s[j], sum);
+    }
+    __syncthreads();
+
+    // ctx = P V for rows [32w, 32w+32) x 64
+    v16f o2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o2[j][r] = 0.0f;
+#pragma unroll 4
+    for (int c2 = 0; c2 < ATT_S / 2; ++c2) {
+        const int cc = 2 * c2 + lh;
+        const float av = sp[qrow * P_STRIDE + cc];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float bv = sv[cc * QK_STRIDE + 32 * j + lr];
+            o2[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, o2[j], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = 32 * w + 8 * (r / 4) + 4 * lh + (r % 4);
+        if (row >= S) continue;
+        float* dst = a.out + ((size_t)b * S + row) * a.ldo + h * ATT_D;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) dst[32 * j + lr] = o2[j][r];
+    }
+}
+
+constexpr size_t kAttnSmem = (size_t)3 * ATT_S * QK_STRIDE * sizeof(float);
+
+unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
+    size_t b = icx::cdiv(work, per_block);
+    if (b < 1) b = 1;
+    return (unsigned)(b > cap ? cap : b);
+}
+
+}  // namespace
+
+extern "C" int icx_layer_norm_f32(icx_stream_t stream, const float* x, const float* residual,
+                                  size_t rows, size_t cols, const float* scale,
+                                  const float* bias, float eps, float* y) {
+    icx::clear_error();
+    if (!x || !scale || !bias || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "LayerNormalization: null pointer argument");
+    if (cols == 0 && rows) ICX_FAIL(ICX_ERR_SHAPE, "LayerNormalization: empty normalized axis");
+    if (rows == 0) return ICX_OK;
+    hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)icx::cdiv(rows, 32)), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), x, residual, rows, cols, scale, bias,
+                       eps, y);
+    ICX_LAUNCH_CHECK("layer_norm_kernel");
+    return ICX_OK;
+}
+
+extern "C" int icx_softmax_f32(icx_stream_t stream, const float* x, size_t rows, size_t cols,
+                               float* y) {
+    icx::clear_error();
+    if (!x || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "Softmax: null pointer argument");
+    if (x == y) ICX_FAIL(ICX_ERR_INVALID_ARG, "Softmax: input and output must not alias");
+    if (rows == 0 || cols == 0) return ICX_OK;
+    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)icx::cdiv(rows, 32)), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), x, rows, cols, y);
+    ICX_LAUNCH_CHECK("softmax_kernel");
+    return ICX_OK;
+}
+
+extern "C" int icx_transpose(icx_stream_t stream, const void* x, size_t elem_bytes, int rank,
+                             const int64_t* dims, const int* perm, void* y) {
+    icx::clear_error();
+    if (!x || !y || (rank && (!dims || !perm)))
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "Transpose: null pointer argument");
+    if (rank < 0 || rank > 6) ICX_FAIL(ICX_ERR_UNSUPPORTED, "Transpose: rank %d outside [0, 6]", rank);
+    if (elem_bytes != 1 && elem_bytes != 4)
+        ICX_FAIL(ICX_ERR_DTYPE, "Transpose: element size %zu unsupported (1 or 4 bytes)", elem_bytes);
+    TransposeArgs a{};
+    a.rank = rank;
+    int64_t in_stride[6];
+    int64_t st = 1;
+    size_t n = 1;
+    bool seen[6] = {false, false, false, false, false, false};
+    for (int d = rank - 1; d >= 0; --d) {
+        if (dims[d] < 0) ICX_FAIL(ICX_ERR_SHAPE, "Transpose: negative dimension");
+        in_stride[d] = st;
+        st *= dims[d];
+    }
+    for (int d = 0; d < rank; ++d) {
+        if (perm[d] < 0 || perm[d] >= rank || seen[perm[d]])
+            ICX_FAIL(ICX_ERR_INVALID_ARG, "Transpose: perm is not a permutation of [0, %d)", rank);
+        seen[perm[d]] = true;
+        a.out_dims[d] = dims[perm[d]];
+        a.in_stride_of_out[d] = in_stride[perm[d]];
+        n *= (size_t)dims[perm[d]];
+    }
+    if (n == 0) return ICX_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid(grid_for(n, kThreads * 4, 8192)), block(kThreads);
+    if (elem_bytes == 4)
+        hipLaunchKernelGGL(transpose_kernel<uint32_t>, grid, block, 0, s,
+                           reinterpret_cast<const uint32_t*>(x), n, a, reinterpret_cast<uint32_t*>(y));
+    else
+        hipLaunchKernelGGL(transpose_kernel<uint8_t>, grid, block, 0, s,
+                           reinterpret_cast<const uint8_t*>(x), n, a, reinterpret_cast<uint8_t*>(y));
+    ICX_LAUNCH_CHECK("transpose_kernel");
+    return ICX_OK;
+}
+
+extern "C" int icx_matmul_f32(icx_stream_t stream, const float* a, const float* b, size_t batch,
+                              int b_broadcast, size_t M, size_t K, size_t N, float* c) {
+    icx::clear_error();
+    if (!a || !b || !c) ICX_FAIL(ICX_ERR_INVALID_ARG, "MatMul: null pointer argument");
+    if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || batch > 65535)
+        ICX_FAIL(ICX_ERR_SHAPE, "MatMul: dimensions out of range");
+    if (batch == 0 || M == 0 || N == 0) return ICX_OK;
+    const int tiles_n = (int)icx::cdiv(N, 64);
+    const dim3 grid((unsigned)(icx::cdiv(M, 64) * tiles_n), (unsigned)batch);
+    hipLaunchKernelGGL(matmul_f32_kernel, grid, dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), a, b, (int)M, (int)K, (int)N,
+                       b_broadcast ? 1 : 0, tiles_n, c);
+    ICX_LAUNCH_CHECK("matmul_f32_kernel");
+    return ICX_OK;
+}
+
+extern "C" int icx_attention_f32(icx_stream_t stream, const float* q, const float* k,
+                                 const float* v, size_t B, size_t S, size_t H, size_t D,
+                                 size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
+                                 int scale_div, int scale_q, float* out) {
+    icx::clear_error();
+    if (!q || !k || !v || !out) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention: null pointer argument");
+    if (D != (size_t)ATT_D || S == 0 || S > (size_t)ATT_S)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention: head size %zu / sequence %zu unsupported (D = 64, S <= 128)", D, S);
+    if (ldq < H * D || ldk < H * D || ldv < H * D || ldo < H * D || (ldq | ldk | ldv) % 4 ||
+        !icx::aligned16(q) || !icx::aligned16(k) || !icx::aligned16(v))
+        ICX_FAIL(ICX_ERR_SHAPE, "Attention: row strides must cover H*D and keep 16-byte alignment");
+    if (B * H == 0) return ICX_OK;
+    if (B * H > 0x7fffffff) ICX_FAIL(ICX_ERR_SHAPE, "Attention: too many (batch, head) pairs");
+    AttnArgs a{q, k, v, out, (int)S, (int)H, (int64_t)ldq, (int64_t)ldk, (int64_t)ldv, (int64_t)ldo,
+               scale, scale_div ? 1 : 0, scale_q ? 1 : 0};
+    static bool smem_set = false;  // ~98 KB of dynamic LDS is above the default limit
+    if (!smem_set) {
+        ICX_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)kAttnSmem));
+        smem_set = true;
+    }
+    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)(B * H)), dim3(kThreads), kAttnSmem,
+                       reinterpret_cast<hipStream_t>(stream), a);
+    ICX_LAUNCH_CHECK("attention_kernel");
+    return ICX_OK;
+}

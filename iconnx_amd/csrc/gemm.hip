@@ -37,6 +37,9 @@ constexpr int LDS_STRIDE = BK + 16;  // bytes per LDS row (padding against bank 
 constexpr int GROUP_M = 8;
 
 enum { OUT_I32 = 0, OUT_F32 = 1 };
+// Epilogue chain forms: general per-element operands; column operands, binary ops only;
+// column operands with the operand-free erf / save steps (GELU).
+enum { CH_GENERAL = 0, CH_COL = 1, CH_COL_EXT = 2 };
 
 struct GemmArgs {
     const int8_t* A;   // [M,K] raw (u8 or i8 bytes)
@@ -128,7 +131,7 @@ struct EpiLayout {
 // applied, then read back row-major as float4 / int4 so that the chain runs on 4
 // consecutive columns per lane with its column operands in LDS, and the global stores are
 // 16-byte and contiguous along rows.  `smem` must not be in use by the main loop any more.
-template <int BM, int BN, int WGM, int WGN, int OUT, bool COLCHAIN>
+template <int BM, int BN, int WGM, int WGN, int OUT, int CH>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
                                               v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
                                               int8_t* smem, int m0, int n0) {
@@ -159,10 +162,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
     const int rsub = lane / LPR;
     const int gcol = n0 + wn * WN + cc;
     float* sop = reinterpret_cast<float*>(smem + EL::STAGE_BYTES);
-    if (OUT == OUT_F32 && COLCHAIN) {
+    if (OUT == OUT_F32 && CH != CH_GENERAL) {
 #pragma unroll
         for (int k = 0; k < ICX_MAX_CHAIN; ++k) {
-            if (k < g.chain.n_ops) {
+            if (k < g.chain.n_ops && icx::op_takes_operand(g.chain.ops[k].op)) {
                 const icx_chain_op& op = g.chain.ops[k];
                 for (int c = t; c < BN; c += NT) {
                     const int col = min(n0 + c, g.N - 1);
@@ -204,8 +207,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
         for (int q = 0; q < NQ; ++q)
             v[q] = *reinterpret_cast<const float4*>(&stage[(q * RPI + rsub) * SROW + cc]);
         if (OUT == OUT_F32) {
-            if (COLCHAIN) {
-                icx::run_chain4(g.codes, g.chain.n_ops, v, [&](int k) {
+            if constexpr (CH != CH_GENERAL) {
+                icx::run_chain4<CH == CH_COL_EXT ? 2 : 0>(g.codes, g.chain.n_ops, v, [&](int k) {
                     return *reinterpret_cast<const float4*>(&sop[k * BN + wn * WN + cc]);
                 });
             } else {
@@ -239,7 +242,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
 // ---- main loop A: register-staged (any K, any alignment) -------------------------------
 // Block tile BM x BN, 4 waves in 2x2, each wave a (BM/2) x (BN/2) sub-tile made of
 // TI x TJ v_mfma_i32_32x32x32_i8 tiles; two LDS stages with rows padded by 16 B.
-template <int BM, int BN, bool VEC, int OUT, bool COLCHAIN>
+template <int BM, int BN, bool VEC, int OUT, int CH>
 __global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TI = WM / 32, TJ = WN / 32;
@@ -320,7 +323,7 @@ __global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
         __syncthreads();
     }
 
-    gemm_epilogue<BM, BN, 2, 2, OUT, COLCHAIN>(g, acc, smem, m0, n0);
+    gemm_epilogue<BM, BN, 2, 2, OUT, CH>(g, acc, smem, m0, n0);
 }
 
 // ---- main loop B: LDS DMA (K % 64 == 0, 16-byte aligned operands) ---------------------
@@ -352,7 +355,7 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int OUT, bool COLCHAIN>
+template <int BM, int BN, int WGM, int WGN, int NS, int OUT, int CH>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma_kernel(GemmArgs g) {
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -474,7 +477,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma_kernel(GemmArgs g)
     }
     wait_vmcnt<0>();
     __syncthreads();  // all copies landed and all fragment reads done: LDS is free
-    gemm_epilogue<BM, BN, WGM, WGN, OUT, COLCHAIN>(g, acc, smem, m0, n0);
+    gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0);
 }
 
 // ---- weight packing -------------------------------------------------------------------
@@ -599,31 +602,47 @@ int pack_weight_impl(hipStream_t s, const void* B, int b_dtype, size_t K, size_t
     return ICX_OK;
 }
 
-template <int BM, int BN>
-void launch_reg(bool vec, int out_kind, bool colchain, unsigned blocks, hipStream_t s,
-                const GemmArgs& g) {
+template <int BM, int BN, bool VEC>
+void launch_reg_v(int out_kind, int ch, unsigned blocks, hipStream_t s, const GemmArgs& g) {
     const dim3 grid(blocks), block(kThreads);
-    if (out_kind == OUT_I32) {
-        if (vec) hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, true, OUT_I32, false>), grid, block, 0, s, g);
-        else hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, false, OUT_I32, false>), grid, block, 0, s, g);
-    } else if (colchain) {
-        if (vec) hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, true, OUT_F32, true>), grid, block, 0, s, g);
-        else hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, false, OUT_F32, true>), grid, block, 0, s, g);
-    } else {
-        if (vec) hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, true, OUT_F32, false>), grid, block, 0, s, g);
-        else hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, false, OUT_F32, false>), grid, block, 0, s, g);
-    }
+    if (out_kind == OUT_I32)
+        hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, VEC, OUT_I32, CH_GENERAL>), grid, block, 0, s, g);
+    else if (ch == CH_COL)
+        hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, VEC, OUT_F32, CH_COL>), grid, block, 0, s, g);
+    else if (ch == CH_COL_EXT)
+        hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, VEC, OUT_F32, CH_COL_EXT>), grid, block, 0, s, g);
+    else
+        hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, VEC, OUT_F32, CH_GENERAL>), grid, block, 0, s, g);
+}
+
+template <int BM, int BN>
+void launch_reg(bool vec, int out_kind, int ch, unsigned blocks, hipStream_t s, const GemmArgs& g) {
+    if (vec) launch_reg_v<BM, BN, true>(out_kind, ch, blocks, s, g);
+    else launch_reg_v<BM, BN, false>(out_kind, ch, blocks, s, g);
 }
 
 template <int BM, int BN, int WGM, int WGN, int NS>
-void launch_dma(int out_kind, bool colchain, unsigned blocks, hipStream_t s, const GemmArgs& g) {
+void launch_dma(int out_kind, int ch, unsigned blocks, hipStream_t s, const GemmArgs& g) {
     const dim3 grid(blocks), block(64 * WGM * WGN);
     if (out_kind == OUT_I32)
-        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_I32, false>), grid, block, 0, s, g);
-    else if (colchain)
-        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_F32, true>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_I32, CH_GENERAL>), grid, block, 0, s, g);
+    else if (ch == CH_COL)
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_F32, CH_COL>), grid, block, 0, s, g);
+    else if (ch == CH_COL_EXT)
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_F32, CH_COL_EXT>), grid, block, 0, s, g);
     else
-        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_F32, false>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<BM, BN, WGM, WGN, NS, OUT_F32, CH_GENERAL>), grid, block, 0, s, g);
+}
+
+// The 256x256 tile is only instantiated for int32 output and binary column chains (its
+// register budget has no room for the general or GELU epilogues).
+template <int WGM, int WGN, int NS>
+void launch_dma_big(int out_kind, unsigned blocks, hipStream_t s, const GemmArgs& g) {
+    const dim3 grid(blocks), block(64 * WGM * WGN);
+    if (out_kind == OUT_I32)
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 256, WGM, WGN, NS, OUT_I32, CH_GENERAL>), grid, block, 0, s, g);
+    else
+        hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 256, WGM, WGN, NS, OUT_F32, CH_COL>), grid, block, 0, s, g);
 }
 
 int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,
@@ -708,21 +727,22 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     const bool vec = K >= 16 && (K % 16 == 0) && icx::aligned16(A) && icx::aligned16(Bp);
     const bool dma = vec && K >= 64 && K % 64 == 0;
     const bool colchain = out_kind == OUT_F32 && icx::chain_is_col_only(g.chain);
+    const int ch = !colchain ? CH_GENERAL : (icx::chain_mode(g.chain) == 2 ? CH_COL_EXT : CH_COL);
     // 256x256 tiles (128x128 per wave) when there are enough of them to fill the chip;
     // otherwise 128x128 so that every CU gets tiles.  Row / full-tensor chain operands
     // take the general per-element path, kept on the 128x128 tile.
-    const bool big = icx::cdiv(M, 256) * icx::cdiv(N, 256) >= 512 && (out_kind == OUT_I32 || colchain);
+    const bool big = icx::cdiv(M, 256) * icx::cdiv(N, 256) >= 512 && (out_kind == OUT_I32 || ch == CH_COL);
     if (big) {
         g.tiles_m = (int)icx::cdiv(M, 256);
         g.tiles_n = (int)icx::cdiv(N, 256);
     }
     const unsigned blocks = (unsigned)(g.tiles_m * g.tiles_n);
     if (dma) {
-        if (big) launch_dma<256, 256, 2, 4, 4>(out_kind, colchain, blocks, s, g);
-        else launch_dma<128, 128, 2, 2, 3>(out_kind, colchain, blocks, s, g);
+        if (big) launch_dma_big<2, 4, 4>(out_kind, blocks, s, g);
+        else launch_dma<128, 128, 2, 2, 3>(out_kind, ch, blocks, s, g);
     } else {
-        if (big) launch_reg<256, 256>(vec, out_kind, colchain, blocks, s, g);
-        else launch_reg<128, 128>(vec, out_kind, colchain, blocks, s, g);
+        if (big) launch_reg<256, 256>(vec, out_kind, ch, blocks, s, g);
+        else launch_reg<128, 128>(vec, out_kind, ch, blocks, s, g);
     }
     ICX_LAUNCH_CHECK("gemm_i8_kernel");
     return ICX_OK;

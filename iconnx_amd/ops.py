@@ -21,14 +21,16 @@ import ctypes
 import torch
 
 from ._lib import (BCAST_COL, BCAST_FULL, BCAST_ROW, BCAST_SCALAR, ICX_F32, ICX_I8, ICX_I32,
-                   ICX_U8, MAX_CHAIN, OP_ADD, OP_DIV, OP_MUL, OP_SUB, Chain, IconnxError, check,
-                   lib)
+                   ICX_U8, MAX_CHAIN, OP_ADD, OP_DIV, OP_ERF, OP_MUL, OP_MUL_SAVED, OP_SAVE,
+                   OP_SUB, Chain, IconnxError, check, lib)
 
 ERR_SHAPE, ERR_DTYPE, ERR_INVALID = 2, 3, 1
 _DT = {torch.int8: ICX_I8, torch.uint8: ICX_U8, torch.int32: ICX_I32, torch.float32: ICX_F32}
 _DT_NAME = {torch.int8: "Int8", torch.uint8: "UInt8", torch.int32: "Int32",
             torch.float32: "Float32", torch.int64: "Int64", torch.float16: "Float16"}
-_OPS = {"Add": OP_ADD, "Sub": OP_SUB, "Mul": OP_MUL, "Div": OP_DIV}
+_OPS = {"Add": OP_ADD, "Sub": OP_SUB, "Mul": OP_MUL, "Div": OP_DIV, "Erf": OP_ERF,
+        "Save": OP_SAVE, "MulSaved": OP_MUL_SAVED}
+_OPERAND_FREE = ("Erf", "Save", "MulSaved")
 
 
 def _name(dt):
@@ -200,6 +202,10 @@ def build_chain(ops, rows, cols):
     ch.n_ops = len(ops)
     keep = []
     for i, (name, operand, is_lhs) in enumerate(ops):
+        if name in _OPERAND_FREE:  # erf / save / multiply by the saved value
+            o = ch.ops[i]
+            o.op, o.operand_is_lhs, o.kind0, o.kind1, o.p0, o.p1 = _OPS[name], 0, 0, 0, None, None
+            continue
         factors = operand if isinstance(operand, (tuple, list)) else (operand,)
         kinds, ptrs = [], []
         for f in factors:
@@ -356,3 +362,89 @@ def gpu_dequantize_linear(x, scale, zp=None, axis=1):
     check(lib().icx_dequantize_linear_f32(_stream(), _p(x), _DT[x.dtype], _p(scale), _p(zp), n,
                                           axis_size, inner, _p(y)))
     return y
+
+
+# ---------------------------------------------------------------------------------------
+# Encoder ops (fp32)
+# ---------------------------------------------------------------------------------------
+def _f32_cuda(*ts):
+    for t in ts:
+        if t is not None:
+            _require_cuda(t)
+            if t.dtype != torch.float32:
+                raise IconnxError(ERR_DTYPE, "expected Float32, got %s" % _name(t.dtype))
+
+
+def gpu_layer_norm(x, scale, bias, eps=1e-5, residual=None):
+    """LayerNormalization over the last axis of x (or of x + residual)."""
+    _f32_cuda(x, scale, bias, residual)
+    x = x.contiguous()
+    cols = x.shape[-1]
+    if scale.numel() != cols or bias.numel() != cols:
+        raise IconnxError(ERR_SHAPE, "LayerNorm: scale/bias must have %d elements" % cols)
+    if residual is not None:
+        if residual.shape != x.shape:
+            raise IconnxError(ERR_SHAPE, "LayerNorm: residual shape differs from the input")
+        residual = residual.contiguous()
+    y = torch.empty_like(x)
+    check(lib().icx_layer_norm_f32(_stream(), _p(x), _p(residual), x.numel() // cols, cols,
+                                   _p(scale.contiguous()), _p(bias.contiguous()),
+                                   ctypes.c_float(eps), _p(y)))
+    return y
+
+
+def gpu_softmax(x):
+    _f32_cuda(x)
+    x = x.contiguous()
+    cols = x.shape[-1]
+    y = torch.empty_like(x)
+    check(lib().icx_softmax_f32(_stream(), _p(x), x.numel() // max(cols, 1), cols, _p(y)))
+    return y
+
+
+def gpu_erf(x):
+    """Erf (the reference's Abramowitz-Stegun evaluation) as a one-step chain."""
+    return gpu_fused_chain(x, [("Erf", None, False)])
+
+
+def gpu_transpose(x, perm=None):
+    _require_cuda(x)
+    x = x.contiguous()
+    rank = x.dim()
+    perm = list(range(rank))[::-1] if perm is None else [int(p) for p in perm]
+    y = torch.empty([x.shape[p] for p in perm], dtype=x.dtype, device=x.device)
+    dims = (ctypes.c_int64 * max(rank, 1))(*x.shape)
+    pm = (ctypes.c_int * max(rank, 1))(*perm)
+    check(lib().icx_transpose(_stream(), _p(x), x.element_size(), rank, dims, pm, _p(y)))
+    return y
+
+
+def gpu_matmul_f32(a, b):
+    """Batched a @ b with the reference's batch rules (equal batch dims or b without)."""
+    _f32_cuda(a, b)
+    a, b = a.contiguous(), b.contiguous()
+    M, K, N = a.shape[-2], a.shape[-1], b.shape[-1]
+    if b.shape[-2] != K:
+        raise IconnxError(ERR_SHAPE, "MatMul: inner dimensions must match")
+    ab, bb = tuple(a.shape[:-2]), tuple(b.shape[:-2])
+    if bb and ab != bb:
+        raise IconnxError(ERR_SHAPE, "MatMul: batch dimensions must be compatible")
+    batch = 1
+    for d in ab:
+        batch *= d
+    c = torch.empty(ab + (M, N), dtype=torch.float32, device=a.device)
+    check(lib().icx_matmul_f32(_stream(), _p(a), _p(b), batch, 0 if bb else 1, M, K, N, _p(c)))
+    return c
+
+
+def gpu_attention(q, k, v, heads, scale, scale_div=True, scale_q=False):
+    """Fused self-attention over [B, S, H*D] tensors (see icx_attention_f32)."""
+    _f32_cuda(q, k, v)
+    B, S, HD = q.shape
+    D = HD // heads
+    out = torch.empty_like(q)
+    check(lib().icx_attention_f32(_stream(), _p(q.contiguous()), _p(k.contiguous()),
+                                  _p(v.contiguous()), B, S, heads, D, HD, HD, HD, HD,
+                                  ctypes.c_float(scale), 1 if scale_div else 0,
+                                  1 if scale_q else 0, _p(out)))
+    return out

@@ -97,6 +97,12 @@ int icx_matmul_integer(icx_stream_t stream, const void* A, int a_dtype, const vo
  * Mul/Add/Div broadcast path (src/cuda/executor/elementwise.rs:54-200), with [cols]
  * broadcast allowed everywhere (the reference DivMul requires equal shapes). */
 enum { ICX_OP_ADD = 0, ICX_OP_SUB = 1, ICX_OP_MUL = 2, ICX_OP_DIV = 3 };
+/* Operand-free steps (p0 may be NULL; kinds ignored), for the erf-GELU subgraph
+ * Mul(x, Add(Erf(Div(x, c0)), c1)) [* c2] (src/operators/erf.rs:21-31):
+ *   ICX_OP_ERF        v = erf(v) — the reference's Abramowitz-Stegun 7.1.26 evaluated in f32;
+ *   ICX_OP_SAVE       s = v (v unchanged);
+ *   ICX_OP_MUL_SAVED  v = s * v (one rounding; operand_is_lhs ignored, products commute). */
+enum { ICX_OP_ERF = 4, ICX_OP_SAVE = 5, ICX_OP_MUL_SAVED = 6 };
 enum { ICX_BCAST_SCALAR = 0, ICX_BCAST_COL = 1, ICX_BCAST_ROW = 2, ICX_BCAST_FULL = 3 };
 #define ICX_MAX_CHAIN 8
 
@@ -139,6 +145,44 @@ int icx_dequantize_linear_f32(icx_stream_t stream, const void* x, int x_dtype,
                               const float* scale, const void* zp, size_t n,
                               size_t axis_size, size_t inner, float* y);
 
+
+/* ---- encoder ops (fp32) --------------------------------------------------------------
+ * The fp32 ops a DistilBERT-shaped encoder needs around its quantized linears.  Parity: the
+ * f32 reductions follow the reference's CPU order where it is defined by its own code
+ * (LayerNormalization, Softmax: ndarray's eight-way unrolled sum); exp and the MatMul
+ * summation order are the device's, so those outputs match the reference within f32
+ * rounding tolerance rather than bit for bit. */
+
+/* LayerNormalization over the last axis (src/operators/layer_normalization.rs:25-80) of
+ * x [rows, cols], or of (x + residual) when residual is not NULL (the Add feeding the norm,
+ * one f32 rounding).  scale, bias: [cols]. */
+int icx_layer_norm_f32(icx_stream_t stream, const float* x, const float* residual, size_t rows,
+                       size_t cols, const float* scale, const float* bias, float eps, float* y);
+
+/* Softmax over the last axis (src/operators/softmax.rs:25-40).  x and y must not alias. */
+int icx_softmax_f32(icx_stream_t stream, const float* x, size_t rows, size_t cols, float* y);
+
+/* Transpose (src/operators/transpose.rs:10-40): y = x.permuted_axes(perm), standard layout;
+ * rank <= 6; elements of 1 or 4 bytes. */
+int icx_transpose(icx_stream_t stream, const void* x, size_t elem_bytes, int rank,
+                  const int64_t* dims, const int* perm, void* y);
+
+/* Batched f32 MatMul (src/operators/matmul.rs:20-150): c[i] = a[i] @ b[b_broadcast ? 0 : i],
+ * a [M,K], b [K,N], all row-major; batch <= 65535. */
+int icx_matmul_f32(icx_stream_t stream, const float* a, const float* b, size_t batch,
+                   int b_broadcast, size_t M, size_t K, size_t N, float* c);
+
+/* Fused self-attention over [B, S, H*D] activations (row strides ld*, elements): for every
+ * (b, h), out[b, s, h*D + d] = sum_c softmax_c(score[s, c]) * v[b, c, h*D + d] with
+ * score[s, c] = sum_d q[b, s, h*D + d] * k[b, c, h*D + d], scaled by `scale` (division when
+ * scale_div, else multiplication), applied to q before the product when scale_q, else to the
+ * scores.  This is the BERT subgraph Reshape -> Transpose -> MatMul -> Div|Mul -> Softmax ->
+ * MatMul -> Transpose -> Reshape the reference runs node by node
+ * (src/operators/{reshape,transpose,matmul,div,softmax}.rs).  D == 64, S <= 128. */
+int icx_attention_f32(icx_stream_t stream, const float* q, const float* k, const float* v,
+                      size_t B, size_t S, size_t H, size_t D, size_t ldq, size_t ldk,
+                      size_t ldv, size_t ldo, float scale, int scale_div, int scale_q,
+                      float* out);
 
 /* ---- graph executor ------------------------------------------------------------------
  * Mirrors GpuGraphExecutor (src/cuda/inference/mod.rs:208-659): add_input (:306),

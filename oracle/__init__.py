@@ -13,6 +13,11 @@ conditions under which it panics — raised here as :class:`OracleError`):
 * :func:`cast_i32_f32` — ``src/operators/cast.rs:46-49``
 * :func:`add`/:func:`sub`/:func:`mul`/:func:`div` — ``src/operators/{add,mul,div}.rs``
 * :func:`dequantize_linear` — ``src/operators/dequantize_linear.rs:32-214``
+* :func:`layer_norm` — ``src/operators/layer_normalization.rs:25-80`` (last axis)
+* :func:`softmax` — ``src/operators/softmax.rs:25-40`` (last axis)
+* :func:`erf` — ``src/operators/erf.rs:21-31``
+* :func:`matmul_f32` — ``src/operators/matmul.rs:20-150`` (f64-accumulated; tolerance)
+* :func:`transpose` — ``src/operators/transpose.rs:10-40``
 
 Parity pins (tests/test_oracle.py): the ONNX 1.18 node goldens the reference vendors
 (tests/golden/onnx_node_goldens.json), the reference's unit-test literals, brute-force
@@ -64,6 +69,18 @@ def _load():
     lib.orc_binary_f32.restype = ctypes.c_int
     lib.orc_dequantize_linear.argtypes = [P, ctypes.c_int, P, P, S, S, S, P]
     lib.orc_dequantize_linear.restype = None
+    lib.orc_sum_unrolled8.argtypes = [P, S]
+    lib.orc_sum_unrolled8.restype = ctypes.c_float
+    lib.orc_layer_norm.argtypes = [P, S, S, P, P, ctypes.c_float, P]
+    lib.orc_layer_norm.restype = None
+    lib.orc_softmax_last.argtypes = [P, S, S, P]
+    lib.orc_softmax_last.restype = None
+    lib.orc_erf.argtypes = [P, S, P]
+    lib.orc_erf.restype = None
+    lib.orc_matmul_f32.argtypes = [P, P, S, ctypes.c_int, S, S, S, P]
+    lib.orc_matmul_f32.restype = None
+    lib.orc_transpose.argtypes = [P, S, ctypes.c_int, P, P, P]
+    lib.orc_transpose.restype = None
     _lib = lib
     return lib
 
@@ -263,3 +280,84 @@ def qlinear_graph(x, w, w_zp, x_scale_times_w_scale_inputs, bias, chain=(), rows
         y = fn(operand, y) if operand_is_lhs else fn(y, operand)
     out["y"] = y
     return out
+
+
+# ---- encoder ops (fp32) ------------------------------------------------------------------
+def _f32(x):
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def sum_unrolled8(x):
+    """f32 sum in ndarray 0.16's unrolled_fold order (eight strided partials)."""
+    x = _f32(x).reshape(-1)
+    return np.float32(_load().orc_sum_unrolled8(_ptr(x), x.size))
+
+
+def _last_axis(x, axis):
+    if axis not in (-1, x.ndim - 1):
+        raise OracleError("only the last axis is supported (got axis %d of rank %d)"
+                          % (axis, x.ndim))
+
+
+def layer_norm(x, scale, bias, eps=1e-5, axis=-1):
+    x = _f32(x)
+    _last_axis(x, axis)
+    cols = x.shape[-1]
+    scale, bias = _f32(scale).reshape(-1), _f32(bias).reshape(-1)
+    if scale.size != cols or bias.size != cols:
+        raise OracleError("LayerNorm: cannot broadcast scale/bias to the last axis")
+    y = np.empty_like(x)
+    _load().orc_layer_norm(_ptr(x), x.size // max(cols, 1), cols, _ptr(scale), _ptr(bias),
+                           ctypes.c_float(eps), _ptr(y))
+    return y
+
+
+def softmax(x, axis=-1):
+    x = _f32(x)
+    _last_axis(x, axis)
+    y = np.empty_like(x)
+    cols = x.shape[-1]
+    _load().orc_softmax_last(_ptr(x), x.size // max(cols, 1), cols, _ptr(y))
+    return y
+
+
+def erf(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    _load().orc_erf(_ptr(x), x.size, _ptr(y))
+    return y
+
+
+def matmul_f32(a, b):
+    """Batched a @ b with the reference's batch rules: equal batch dims, or one side
+    without batch dims (matmul.rs:68-86)."""
+    a, b = _f32(a), _f32(b)
+    if a.ndim < 2 or b.ndim < 2 or a.shape[-1] != b.shape[-2]:
+        raise OracleError("MatMul: inner dimensions must match")
+    M, K, N = a.shape[-2], a.shape[-1], b.shape[-1]
+    ab, bb = a.shape[:-2], b.shape[:-2]
+    if not ab and bb:
+        a = np.ascontiguousarray(np.broadcast_to(a, bb + (M, K)))
+        batch, out_b, b_bcast = int(np.prod(bb)), bb, 0
+    elif ab and not bb:
+        batch, out_b, b_bcast = int(np.prod(ab)), ab, 1
+    elif ab == bb:
+        batch, out_b, b_bcast = int(np.prod(ab)) if ab else 1, ab, 0
+    else:
+        raise OracleError("MatMul: batch dimensions must be compatible")
+    c = np.empty(out_b + (M, N), np.float32)
+    _load().orc_matmul_f32(_ptr(a), _ptr(b), batch, b_bcast, M, K, N, _ptr(c))
+    return c
+
+
+def transpose(x, perm=None):
+    x = np.ascontiguousarray(x)
+    rank = x.ndim
+    perm = list(range(rank))[::-1] if perm is None else [int(p) for p in perm]
+    if sorted(perm) != list(range(rank)) or rank > 8:
+        raise OracleError("Transpose: bad permutation %s" % perm)
+    y = np.empty(tuple(x.shape[p] for p in perm), x.dtype)
+    dims = np.array(x.shape, dtype=np.uintp)
+    pm = np.array(perm, dtype=np.int32)
+    _load().orc_transpose(_ptr(x), x.itemsize, rank, _ptr(dims), _ptr(pm), _ptr(y))
+    return y

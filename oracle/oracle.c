@@ -6,6 +6,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* Rust `f64::clamp(qmin, qmax) as u8`: clamp keeps NaN, the saturating cast maps NaN to 0
@@ -159,5 +160,107 @@ void orc_dequantize_linear(const void* x, int x_dt, const float* scale, const vo
         float xi = load_as_f32(x, x_dt, i);
         float zpi = zp ? load_as_f32(zp, x_dt, ax) : 0.0f;
         y[i] = (xi - zpi) * scale[ax];
+    }
+}
+
+/* ---- encoder ops ----------------------------------------------------------------------- */
+
+float orc_sum_unrolled8(const float* x, size_t n) {
+    float p[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int j = 0; j < 8; ++j) p[j] = p[j] + x[i + j];
+    float acc = 0.0f;
+    acc = acc + (p[0] + p[4]);
+    acc = acc + (p[1] + p[5]);
+    acc = acc + (p[2] + p[6]);
+    acc = acc + (p[3] + p[7]);
+    for (; i < n; ++i) acc = acc + x[i];
+    return acc;
+}
+
+void orc_layer_norm(const float* x, size_t rows, size_t cols, const float* scale,
+                    const float* bias, float eps, float* y) {
+    /* layer_normalization.rs:45-77; mean_axis = sum_axis / n with n as f32 */
+    float* c = (float*)malloc(cols * sizeof(float));
+    float* sq = (float*)malloc(cols * sizeof(float));
+    for (size_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * cols;
+        const float mean = orc_sum_unrolled8(xr, cols) / (float)cols;
+        for (size_t j = 0; j < cols; ++j) {
+            c[j] = xr[j] - mean;
+            sq[j] = c[j] * c[j];
+        }
+        const float var = orc_sum_unrolled8(sq, cols) / (float)cols;
+        const float sd = sqrtf(var + eps);
+        for (size_t j = 0; j < cols; ++j) {
+            const float nrm = c[j] / sd;
+            y[r * cols + j] = nrm * scale[j] + bias[j];
+        }
+    }
+    free(c);
+    free(sq);
+}
+
+void orc_softmax_last(const float* x, size_t rows, size_t cols, float* y) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * cols;
+        float* yr = y + r * cols;
+        float m = -INFINITY;
+        for (size_t j = 0; j < cols; ++j) m = fmaxf(m, xr[j]); /* f32::max ignores NaN */
+        for (size_t j = 0; j < cols; ++j) yr[j] = expf(xr[j] - m);
+        const float s = orc_sum_unrolled8(yr, cols);
+        for (size_t j = 0; j < cols; ++j) yr[j] = yr[j] / s;
+    }
+}
+
+static float erf1(float x) {
+    /* erf.rs:21-31: sign * (1 - poly(t) * t * exp(-a*a)), t = 1 / (1 + 0.3275911 a) */
+    const float sign = isnan(x) ? x : (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : copysignf(1.0f, x)));
+    const float a = fabsf(x);
+    const float t = 1.0f / (1.0f + 0.3275911f * a);
+    const float poly = ((((1.0614054f * t - 1.4531521f) * t) + 1.4214138f) * t - 0.28449672f) * t
+                       + 0.2548296f;
+    const float y = 1.0f - poly * t * expf(-a * a);
+    return sign * y;
+}
+
+void orc_erf(const float* x, size_t n, float* y) {
+    for (size_t i = 0; i < n; ++i) y[i] = erf1(x[i]);
+}
+
+void orc_matmul_f32(const float* a, const float* b, size_t batch, int b_broadcast, size_t M,
+                    size_t K, size_t N, float* c) {
+    for (size_t bi = 0; bi < batch; ++bi) {
+        const float* ab = a + bi * M * K;
+        const float* bb = b + (b_broadcast ? 0 : bi * K * N);
+        float* cb = c + bi * M * N;
+        for (size_t m = 0; m < M; ++m)
+            for (size_t n = 0; n < N; ++n) {
+                double s = 0.0;
+                for (size_t k = 0; k < K; ++k) s += (double)ab[m * K + k] * (double)bb[k * N + n];
+                cb[m * N + n] = (float)s;
+            }
+    }
+}
+
+void orc_transpose(const void* x, size_t elem, int rank, const size_t* dims, const int* perm,
+                   void* y) {
+    size_t n = 1, in_stride[8], out_dims[8];
+    for (int d = 0; d < rank; ++d) n *= dims[d];
+    size_t st = 1;
+    for (int d = rank - 1; d >= 0; --d) {
+        in_stride[d] = st;
+        st *= dims[d];
+    }
+    for (int d = 0; d < rank; ++d) out_dims[d] = dims[perm[d]];
+    for (size_t o = 0; o < n; ++o) {
+        size_t rem = o, src = 0;
+        for (int d = rank - 1; d >= 0; --d) {
+            const size_t idx = rem % out_dims[d];
+            rem /= out_dims[d];
+            src += idx * in_stride[perm[d]];
+        }
+        memcpy((char*)y + o * elem, (const char*)x + src * elem, elem);
     }
 }

@@ -61,6 +61,38 @@ int orc_binary_f32(int op, const float* a, const size_t* a_shape, int a_rank, co
 void orc_dequantize_linear(const void* x, int x_dt, const float* scale, const void* zp,
                            size_t n, size_t axis_size, size_t inner, float* y);
 
+/* ---- encoder ops (fp32) -------------------------------------------------------------- */
+
+/* Sum of a contiguous f32 slice in the order of ndarray 0.16's `numeric_util::unrolled_fold`
+ * (the reference's `sum_axis` / `mean_axis` over a contiguous last axis, Cargo.toml:21):
+ * eight partial sums p_j over x[j], x[j+8], ... then acc = 0 + (p0+p4), + (p1+p5),
+ * + (p2+p6), + (p3+p7), then the < 8 leftover elements in order. */
+float orc_sum_unrolled8(const float* x, size_t n);
+
+/* LayerNormalization over the last axis (src/operators/layer_normalization.rs:25-80):
+ * mean = sum/n; c = x - mean; var = sum(c*c)/n; std = sqrt(var + eps);
+ * y = (c / std) * scale + bias, every step one f32 rounding.  x, y: [rows, cols]. */
+void orc_layer_norm(const float* x, size_t rows, size_t cols, const float* scale,
+                    const float* bias, float eps, float* y);
+
+/* Softmax over the last axis (src/operators/softmax.rs:25-40): m = max (NaN-ignoring fold
+ * from -inf), e = exp(x - m) (libm expf, as Rust's f32::exp), y = e / sum(e). */
+void orc_softmax_last(const float* x, size_t rows, size_t cols, float* y);
+
+/* Erf (src/operators/erf.rs:21-31): Abramowitz-Stegun 7.1.26 in f32 with libm expf. */
+void orc_erf(const float* x, size_t n, float* y);
+
+/* Batched f32 MatMul (src/operators/matmul.rs:20-150): c[b] = a[b] @ b[b or 0], a [M,K],
+ * b [K,N].  Accumulated in f64 and rounded once: the reference's sgemm summation order
+ * (matrixmultiply crate microkernels) is not restated, so parity with it is by tolerance. */
+void orc_matmul_f32(const float* a, const float* b, size_t batch, int b_broadcast, size_t M,
+                    size_t K, size_t N, float* c);
+
+/* Transpose (src/operators/transpose.rs:10-40): y = x.permuted_axes(perm) in standard
+ * layout; elem bytes 1, 4 or 8; rank <= 8. */
+void orc_transpose(const void* x, size_t elem, int rank, const size_t* dims, const int* perm,
+                   void* y);
+
 #ifdef __cplusplus
 }
 #endif

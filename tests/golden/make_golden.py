@@ -32,6 +32,30 @@ TESTS = [
     "test_add_bcast",
     "test_div",
     "test_div_bcast",
+    # encoder ops (fp32): LayerNormalization over the last axis, Softmax, Erf, MatMul,
+    # Transpose
+    "test_layer_normalization_2d_axis1",
+    "test_layer_normalization_2d_axis_negative_1",
+    "test_layer_normalization_3d_axis2_epsilon",
+    "test_layer_normalization_3d_axis_negative_1_epsilon",
+    "test_layer_normalization_4d_axis3",
+    "test_layer_normalization_4d_axis_negative_1",
+    "test_softmax_example",
+    "test_softmax_axis_2",
+    "test_softmax_default_axis",
+    "test_softmax_negative_axis",
+    "test_softmax_large_number",
+    "test_erf",
+    "test_matmul_2d",
+    "test_matmul_3d",
+    "test_matmul_4d",
+    "test_transpose_default",
+    "test_transpose_all_permutations_0",
+    "test_transpose_all_permutations_1",
+    "test_transpose_all_permutations_2",
+    "test_transpose_all_permutations_3",
+    "test_transpose_all_permutations_4",
+    "test_transpose_all_permutations_5",
 ]
 
 # TensorProto.DataType values used by these tests.
@@ -144,13 +168,17 @@ def decode_node(model_buf):
                 elif nf == 4:
                     op = nv.decode()
                 elif nf == 5:
-                    aname, aval = "", None
-                    for af, _, av in fields(nv):
+                    aname, aval, ints = "", None, []
+                    for af, awt, av in fields(nv):
                         if af == 1:
                             aname = av.decode()
+                        elif af == 2:  # AttributeProto.f
+                            aval = struct.unpack("<f", av)[0]
                         elif af == 3:  # AttributeProto.i
                             aval = _signed(av, 64)
-                    attrs[aname] = aval
+                        elif af == 8:  # AttributeProto.ints
+                            ints += [_signed(x, 64) for x in (_packed_varints(av) if awt == 2 else [av])]
+                    attrs[aname] = ints if ints else aval
             return op, ins, outs, attrs
     raise ValueError("no node")
 
