@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libiconnx_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "iconnx_hip.h")
 
-ICX_I8, ICX_U8, ICX_I32, ICX_F32 = 0, 1, 2, 3
+ICX_I8, ICX_U8, ICX_I32, ICX_F32, ICX_I64 = 0, 1, 2, 3, 4
 OP_ADD, OP_SUB, OP_MUL, OP_DIV = 0, 1, 2, 3
 OP_ERF, OP_SAVE, OP_MUL_SAVED = 4, 5, 6
 BCAST_SCALAR, BCAST_COL, BCAST_ROW, BCAST_FULL = 0, 1, 2, 3
@@ -66,6 +66,8 @@ SIGNATURES = {
     "icx_graph_add_initializer": ([P, C, I, I, P, P], I),
     "icx_graph_add_node": ([P, C, C, I, CP, I, CP, I, CP, P], I),
     "icx_graph_add_output": ([P, C], I),
+    "icx_graph_set_node_attr_float": ([P, C, C, ctypes.c_double], I),
+    "icx_graph_set_node_attr_ints": ([P, C, C, I, P], I),
     "icx_graph_plan": ([P, P, S], I),
     "icx_graph_compile": ([P, P], I),
     "icx_graph_set_input": ([P, C, I, I, P, P, I], I),

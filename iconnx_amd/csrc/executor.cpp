@@ -1,20 +1,28 @@
-// Graph executor for the quantized-linear path: the MI355X counterpart of the reference's
-// GpuGraphExecutor shim (src/cuda/inference/mod.rs:208-659), its lowering (ir::lower,
-// src/ir/lowering.rs:31-238) and per-op dispatch (src/cuda/executor/mod.rs:107-597).
+// Graph executor for the quantized-linear path and the encoder around it: the MI355X
+// counterpart of the reference's GpuGraphExecutor shim (src/cuda/inference/mod.rs:208-659),
+// its lowering (ir::lower, src/ir/lowering.rs:31-238) and per-op dispatch
+// (src/cuda/executor/mod.rs:107-597).
 //
-//   build:   add_input / add_initializer / add_node / add_output (host only)
+//   build:   add_input / add_initializer / add_node (+ float and int-list attributes) /
+//            add_output (host only)
 //   plan:    requested outputs (or the graph's sinks, mod.rs:505-519) and dead-node
-//            elimination; topological sort; fusion decision: a QuantizedLinear head over
-//            MatMulInteger -> Cast -> Mul -> [Add] -> [chain], elementwise chains reported
-//            as MulAdd / AddMul / SubMul / DivMul when they are exactly those two ops;
-//            weight zero-point folding; last use of every tensor            (host only)
+//            elimination; topological sort; fusion decision (host only):
+//              Attention        Reshape/Transpose/MatMul/scale/Softmax/MatMul/Transpose/
+//                               Reshape of a BERT self-attention -> one fused kernel
+//              QuantizedLinear  MatMulInteger -> Cast -> Mul -> [Add] -> [chain] [-> GELU]
+//              AddLayerNorm     LayerNormalization(Add(a, b))
+//              MulAdd / AddMul / SubMul / DivMul / ElementwiseChain / Gelu
+//            weight zero-point folding; Reshape outputs alias their input; last use of
+//            every tensor
 //   compile: upload initializers, pack MatMulInteger weights once (icx_pack_weight)
 //   run:     input shape guard, then every planned op on the caller's stream; intermediate
 //            tensors come from a size-class pool on hipMalloc and return to it at their
-//            last use (stream order makes the reuse safe).
+//            last use (stream order makes the reuse safe).  A fused head whose runtime
+//            shapes fall outside its kernel runs its member nodes one by one instead.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <exception>
 #include <map>
@@ -29,7 +37,14 @@ namespace {
 
 using icx::set_error;
 
-size_t dtype_size(int dt) { return (dt == ICX_I8 || dt == ICX_U8) ? 1 : 4; }
+size_t dtype_size(int dt) {
+    switch (dt) {
+        case ICX_I8:
+        case ICX_U8: return 1;
+        case ICX_I64: return 8;
+        default: return 4;
+    }
+}
 
 const char* dtype_name(int dt) {
     switch (dt) {
@@ -37,6 +52,7 @@ const char* dtype_name(int dt) {
         case ICX_U8: return "UInt8";
         case ICX_I32: return "Int32";
         case ICX_F32: return "Float32";
+        case ICX_I64: return "Int64";
         default: return "?";
     }
 }
@@ -70,14 +86,21 @@ struct Node {
     std::string name, op;
     std::vector<std::string> in, out;
     std::map<std::string, int64_t> attr;
+    std::map<std::string, double> fattr;
+    std::map<std::string, std::vector<int64_t>> iattrs;
     int64_t attr_or(const std::string& k, int64_t d) const {
         auto it = attr.find(k);
         return it == attr.end() ? d : it->second;
     }
+    double fattr_or(const std::string& k, double d) const {
+        auto it = fattr.find(k);
+        return it == fattr.end() ? d : it->second;
+    }
 };
 
 // One step of an elementwise chain: v = v op operand (or operand op v).  The operand is a
-// tensor, or the product of two (a folded Mul(x_scale, w_scale) node).
+// tensor, or the product of two (a folded Mul(x_scale, w_scale) node); operand-free steps
+// (erf, save, multiply by the saved value) leave it empty.
 struct Step {
     int op = ICX_OP_MUL;
     bool lhs = false;
@@ -85,7 +108,18 @@ struct Step {
 };
 
 enum class Kind { Regular, FusedHead, Skip };
-enum class Pattern { None, QuantizedLinear, MulAdd, AddMul, SubMul, DivMul, ElementwiseChain };
+enum class Pattern {
+    None,
+    QuantizedLinear,
+    MulAdd,
+    AddMul,
+    SubMul,
+    DivMul,
+    ElementwiseChain,
+    Gelu,
+    Attention,
+    AddLayerNorm
+};
 
 const char* kind_name(Kind k) {
     return k == Kind::Regular ? "Regular" : k == Kind::FusedHead ? "FusedHead" : "Skip";
@@ -99,6 +133,9 @@ const char* pattern_name(Pattern p) {
         case Pattern::SubMul: return "SubMul";
         case Pattern::DivMul: return "DivMul";
         case Pattern::ElementwiseChain: return "ElementwiseChain";
+        case Pattern::Gelu: return "Gelu";
+        case Pattern::Attention: return "Attention";
+        case Pattern::AddLayerNorm: return "AddLayerNorm";
         default: return "-";
     }
 }
@@ -112,7 +149,17 @@ struct PlannedOp {
     bool w_zp_folded = false;      // all-zero weight zero point dropped
     std::string chain_in, out;     // chain input (elementwise heads) and fused output
     std::vector<Step> steps;
-    std::vector<std::pair<std::string, std::string>> members;  // (name, op) folded in
+    std::vector<Node> members;     // nodes folded into this head, in graph order
+    std::vector<Node> sub;         // Attention: every node of the pattern, in graph order
+    // Attention: q, k, v activations [B, S, H*D]; heads, head size; scale and where it acts
+    std::string q, k, v;
+    int64_t heads = 0, head_dim = 0;
+    float scale = 1.0f;
+    bool scale_div = false, scale_q = false;
+    std::string q_shape, k_shape, v_shape, o_shape;  // Reshape shape initializers
+    // AddLayerNorm: LN(x + res)
+    std::string ln_x, ln_res, ln_scale, ln_bias;
+    float eps = 1e-5f;
 };
 
 struct DevTensor {
@@ -189,9 +236,10 @@ struct icx_graph {
     // plan
     bool planned = false, compiled = false;
     std::vector<PlannedOp> plan;
-    std::vector<std::string> live_outputs;   // requested outputs, or the sinks
-    std::map<std::string, size_t> last_use;  // tensor -> plan index of its last reader
-    std::set<std::string> rowsum_wanted;     // DQL outputs whose row sums a GEMM reads
+    std::vector<std::string> live_outputs;     // requested outputs, or the sinks
+    std::set<std::string> keep;                // tensors that stay until the next run
+    std::map<std::string, size_t> last_use;    // tensor -> plan index of its last reader
+    std::set<std::string> rowsum_wanted;       // DQL outputs whose row sums a GEMM reads
 
     // device state
     std::map<std::string, DevTensor> weights;      // uploaded initializers
@@ -229,6 +277,11 @@ struct icx_graph {
         rowsum_of.clear();
     }
     void invalidate() { planned = compiled = false; }
+    Node* find_node(const std::string& name) {
+        for (auto& n : nodes)
+            if (n.name == name) return &n;
+        return nullptr;
+    }
 };
 
 namespace {
@@ -272,26 +325,40 @@ class Planner {
         const int n = (int)nodes_.size();
         std::vector<PlannedOp> ops(n);
         for (int i = 0; i < n; ++i) ops[i].node = nodes_[i];
-        // quantized-linear heads first: they own their Cast / Mul / Add / chain nodes
-        for (int pass = 0; pass < 2; ++pass) {
+        // attention first (it owns Transposes / MatMuls), then the quantized linears (they
+        // own their Cast / Mul / Add / chain / GELU nodes), residual norms, plain chains
+        for (int pass = 0; pass < 4; ++pass) {
             for (int i = 0; i < n; ++i) {
                 if (claimed_.count(i)) continue;
                 PlannedOp head;
                 head.node = nodes_[i];
                 std::vector<int> mem;
-                const bool hit = pass == 0 ? match_qlinear(i, head, mem) : match_chain(i, head, mem);
+                bool hit = false;
+                switch (pass) {
+                    case 0: hit = match_attention(i, head, mem); break;
+                    case 1: hit = match_qlinear(i, head, mem); break;
+                    case 2: hit = match_add_layer_norm(i, head, mem); break;
+                    default: hit = match_chain(i, head, mem); break;
+                }
                 if (!hit) continue;
                 // The head runs at its last member's position: every operand of every member
                 // is produced before that point, and nothing else reads the members' outputs.
                 int pos = i;
                 claimed_.insert(i);
+                std::sort(mem.begin(), mem.end());
                 for (int m : mem) {
                     claimed_.insert(m);
                     pos = std::max(pos, m);
-                    head.members.emplace_back(nodes_[m].name, nodes_[m].op);
+                    head.members.push_back(nodes_[m]);
                     ops[m].kind = Kind::Skip;
                 }
                 ops[i].kind = Kind::Skip;
+                if (head.pattern == Pattern::Attention) {
+                    std::vector<int> all = mem;
+                    all.push_back(i);
+                    std::sort(all.begin(), all.end());
+                    for (int k : all) head.sub.push_back(nodes_[k]);
+                }
                 ops[pos] = head;
             }
         }
@@ -305,7 +372,14 @@ class Planner {
             if (p != gi_.producer.end() && nodes_[p->second].op == "DynamicQuantizeLinear")
                 g_.rowsum_wanted.insert(op.a);
         }
+        // last readers; a Reshape output aliases its input's buffer, so uses of the alias
+        // extend the buffer's life, and a live alias keeps it until the next run
         g_.last_use.clear();
+        std::map<std::string, std::string> root;
+        auto root_of = [&](const std::string& t) {
+            auto it = root.find(t);
+            return it == root.end() ? t : it->second;
+        };
         for (size_t i = 0; i < g_.plan.size(); ++i) {
             const PlannedOp& op = g_.plan[i];
             if (op.kind == Kind::Skip) continue;
@@ -314,9 +388,23 @@ class Planner {
                 uses.push_back(st.opnd0);
                 if (!st.opnd1.empty()) uses.push_back(st.opnd1);
             }
-            if (!op.chain_in.empty()) uses.push_back(op.chain_in);
+            if (op.kind == Kind::FusedHead)
+                for (auto& m : op.members) uses.insert(uses.end(), m.in.begin(), m.in.end());
+            for (auto& x : {op.chain_in, op.q, op.k, op.v, op.ln_x, op.ln_res, op.a}) uses.push_back(x);
             for (auto& u : uses)
-                if (!u.empty()) g_.last_use[u] = i;
+                if (!u.empty()) {
+                    g_.last_use[u] = i;
+                    g_.last_use[root_of(u)] = i;
+                }
+            if (op.kind == Kind::Regular && op.node.op == "Reshape" && !op.node.out.empty())
+                root[op.node.out[0]] = root_of(op.node.in[0]);
+            for (auto& m : op.sub)  // a fused head run node by node creates the same aliases
+                if (m.op == "Reshape" && !m.out.empty()) root[m.out[0]] = root_of(m.in[0]);
+        }
+        g_.keep.clear();
+        for (auto& o : g_.live_outputs) {
+            g_.keep.insert(o);
+            g_.keep.insert(root_of(o));
         }
         g_.planned = true;
         return ICX_OK;
@@ -397,6 +485,16 @@ class Planner {
         auto it = g_.inits.find(t);
         return it != g_.inits.end() && it->second.dtype == ICX_F32;
     }
+    bool static_scalar(const std::string& t, float* v) const {
+        auto it = g_.inits.find(t);
+        if (it == g_.inits.end() || it->second.dtype != ICX_F32 || numel(it->second.shape) != 1) return false;
+        std::memcpy(v, it->second.data.data(), 4);
+        return true;
+    }
+    int producer(const std::string& t) const {
+        auto it = gi_.producer.find(t);
+        return it == gi_.producer.end() ? -1 : it->second;
+    }
     // The single reader of t, or -1 (also when t is a live output: it must materialise).
     int sole_consumer(const std::string& t) const {
         if (outs_.count(t)) return -1;
@@ -404,6 +502,12 @@ class Planner {
         if (it == gi_.consumers.end() || it->second.size() != 1) return -1;
         return it->second[0];
     }
+    bool is_op(int i, const char* op) const { return i >= 0 && !claimed_.count(i) && nodes_[i].op == op; }
+    bool has_perm(int i, std::initializer_list<int64_t> perm) const {
+        auto it = nodes_[i].iattrs.find("perm");
+        return it != nodes_[i].iattrs.end() && it->second == std::vector<int64_t>(perm);
+    }
+
     // Node ni as a chain step over `cur` with a static f32 operand.
     bool as_step(int ni, const std::string& cur, Step& st) const {
         const Node& n = nodes_[ni];
@@ -418,14 +522,59 @@ class Planner {
         st.opnd1.clear();
         return true;
     }
+    // x -> [Div(x, c0) -> Erf -> Add(., c1)] -> Mul(x, .) [-> Mul(., c2)]: the erf-GELU of
+    // PyTorch's export.  Appends SAVE, DIV, ERF, ADD, MUL_SAVED [, MUL] to `steps`.
+    bool match_gelu(std::string& cur, std::vector<Step>& steps, std::vector<int>& mem) const {
+        if (outs_.count(cur)) return false;
+        auto cs = gi_.consumers.find(cur);
+        if (cs == gi_.consumers.end() || cs->second.size() != 2) return false;
+        int di = -1, mi = -1;
+        for (int c : cs->second) {
+            if (is_op(c, "Div") && nodes_[c].in.size() == 2 && nodes_[c].in[0] == cur) di = c;
+            if (is_op(c, "Mul")) mi = c;
+        }
+        if (di < 0 || mi < 0 || di == mi || !static_f32(nodes_[di].in[1])) return false;
+        const int ei = sole_consumer(nodes_[di].out[0]);
+        if (!is_op(ei, "Erf")) return false;
+        const int ai = sole_consumer(nodes_[ei].out[0]);
+        Step add;
+        if (ai < 0 || !as_step(ai, nodes_[ei].out[0], add) || add.op != ICX_OP_ADD) return false;
+        const std::string a_out = nodes_[ai].out[0];
+        if (sole_consumer(a_out) != mi) return false;
+        const Node& m = nodes_[mi];
+        if (m.in.size() != 2 || !((m.in[0] == cur && m.in[1] == a_out) || (m.in[1] == cur && m.in[0] == a_out)))
+            return false;
+        const size_t need = steps.size() + 5;
+        if (need > ICX_MAX_CHAIN) return false;
+        Step sv, dv, ev, ms;
+        sv.op = ICX_OP_SAVE;
+        dv.op = ICX_OP_DIV;
+        dv.opnd0 = nodes_[di].in[1];
+        ev.op = ICX_OP_ERF;
+        ms.op = ICX_OP_MUL_SAVED;
+        steps.insert(steps.end(), {sv, dv, ev, add, ms});
+        mem.insert(mem.end(), {di, ei, ai, mi});
+        cur = m.out[0];
+        const int hi = sole_consumer(cur);
+        Step half;
+        if (steps.size() < ICX_MAX_CHAIN && hi >= 0 && as_step(hi, cur, half) && half.op == ICX_OP_MUL) {
+            steps.push_back(half);
+            mem.push_back(hi);
+            cur = nodes_[hi].out[0];
+        }
+        return true;
+    }
     void extend_chain(std::string& cur, std::vector<Step>& steps, std::vector<int>& mem) const {
         while ((int)steps.size() < ICX_MAX_CHAIN) {
             const int c = sole_consumer(cur);
             Step st;
-            if (c < 0 || !as_step(c, cur, st)) break;
-            steps.push_back(st);
-            mem.push_back(c);
-            cur = nodes_[c].out[0];
+            if (c >= 0 && as_step(c, cur, st)) {
+                steps.push_back(st);
+                mem.push_back(c);
+                cur = nodes_[c].out[0];
+                continue;
+            }
+            if (!match_gelu(cur, steps, mem)) break;
         }
     }
 
@@ -440,11 +589,10 @@ class Planner {
         const std::string w_zp = m.in.size() > 3 ? m.in[3] : "";
         if (!w_zp.empty() && !is_init(w_zp)) return false;
         const int ci = sole_consumer(m.out[0]);
-        if (ci < 0 || nodes_[ci].op != "Cast" || nodes_[ci].attr_or("to", -1) != 1 || nodes_[ci].out.size() != 1)
-            return false;
+        if (!is_op(ci, "Cast") || nodes_[ci].attr_or("to", -1) != 1 || nodes_[ci].out.size() != 1) return false;
         const std::string cast_out = nodes_[ci].out[0];
         const int si = sole_consumer(cast_out);
-        if (si < 0 || nodes_[si].op != "Mul" || nodes_[si].in.size() != 2 || nodes_[si].out.size() != 1) return false;
+        if (!is_op(si, "Mul") || nodes_[si].in.size() != 2 || nodes_[si].out.size() != 1) return false;
         const Node& s1 = nodes_[si];
         const bool left = s1.in[0] == cast_out, right = s1.in[1] == cast_out;
         if (left == right) return false;
@@ -454,12 +602,11 @@ class Planner {
         st.lhs = !left;
         mem = {ci, si};
         // scale = Mul(x_scale, w_scale) read only here: a product operand, rounded once
-        auto sp = gi_.producer.find(scale);
-        if (sp != gi_.producer.end() && nodes_[sp->second].op == "Mul" && nodes_[sp->second].in.size() == 2 &&
-            sole_consumer(scale) == si && !claimed_.count(sp->second)) {
-            st.opnd0 = nodes_[sp->second].in[0];
-            st.opnd1 = nodes_[sp->second].in[1];
-            mem.push_back(sp->second);
+        const int sp = producer(scale);
+        if (is_op(sp, "Mul") && nodes_[sp].in.size() == 2 && sole_consumer(scale) == si) {
+            st.opnd0 = nodes_[sp].in[0];
+            st.opnd1 = nodes_[sp].in[1];
+            mem.push_back(sp);
         } else {
             st.opnd0 = scale;
         }
@@ -478,23 +625,45 @@ class Planner {
         return true;
     }
 
-    // Two or more binary ops over one running tensor with static operands.
+    // Two or more binary ops over one running tensor with static operands, or a GELU.
     bool match_chain(int ni, PlannedOp& head, std::vector<int>& mem) {
         const Node& n = nodes_[ni];
-        if (op_code(n.op) < 0 || n.in.size() != 2 || n.out.size() != 1) return false;
-        std::string in;
-        if (static_f32(n.in[1]) && !static_f32(n.in[0])) in = n.in[0];
-        else if (static_f32(n.in[0]) && !static_f32(n.in[1])) in = n.in[1];
-        else return false;
-        Step st;
-        if (!as_step(ni, in, st)) return false;
-        std::vector<Step> steps = {st};
-        std::string cur = n.out[0];
+        std::vector<Step> steps;
+        std::string in, cur;
         mem.clear();
-        extend_chain(cur, steps, mem);
-        if (steps.size() < 2) return false;
+        bool gelu_start = false;
+        if (n.op == "Div" && n.in.size() == 2 && !static_f32(n.in[0])) {
+            // a GELU whose input is this Div's dividend
+            in = cur = n.in[0];
+            std::vector<int> gm;
+            if (match_gelu(cur, steps, gm) && std::find(gm.begin(), gm.end(), ni) != gm.end()) {
+                for (int m : gm)
+                    if (m != ni) mem.push_back(m);
+                extend_chain(cur, steps, mem);
+                gelu_start = true;
+            } else {
+                steps.clear();
+            }
+        }
+        if (gelu_start) {
+        } else if (op_code(n.op) >= 0 && n.in.size() == 2 && n.out.size() == 1) {
+            if (static_f32(n.in[1]) && !static_f32(n.in[0])) in = n.in[0];
+            else if (static_f32(n.in[0]) && !static_f32(n.in[1])) in = n.in[1];
+            else return false;
+            Step st;
+            if (!as_step(ni, in, st)) return false;
+            steps.push_back(st);
+            cur = n.out[0];
+            extend_chain(cur, steps, mem);
+            if (steps.size() < 2) return false;
+        } else {
+            return false;
+        }
         head.kind = Kind::FusedHead;
         head.pattern = Pattern::ElementwiseChain;
+        bool gelu = false;
+        for (auto& s : steps) gelu = gelu || s.op == ICX_OP_ERF;
+        if (gelu) head.pattern = Pattern::Gelu;
         if (steps.size() == 2) {
             const int a = steps[0].op, b = steps[1].op;
             if (a == ICX_OP_MUL && b == ICX_OP_ADD) head.pattern = Pattern::MulAdd;
@@ -505,6 +674,104 @@ class Planner {
         head.chain_in = in;
         head.steps = steps;
         head.out = cur;
+        return true;
+    }
+
+    // LayerNormalization(Add(a, b)) with the Add read only by the norm.
+    bool match_add_layer_norm(int li, PlannedOp& head, std::vector<int>& mem) {
+        const Node& ln = nodes_[li];
+        if (ln.op != "LayerNormalization" || ln.in.size() != 3 || ln.out.empty() || ln.attr_or("axis", -1) != -1)
+            return false;
+        const int ai = producer(ln.in[0]);
+        if (!is_op(ai, "Add") || nodes_[ai].in.size() != 2 || sole_consumer(ln.in[0]) != li) return false;
+        head.kind = Kind::FusedHead;
+        head.pattern = Pattern::AddLayerNorm;
+        head.ln_x = nodes_[ai].in[0];
+        head.ln_res = nodes_[ai].in[1];
+        head.ln_scale = ln.in[1];
+        head.ln_bias = ln.in[2];
+        head.eps = (float)ln.fattr_or("epsilon", 1e-5);
+        head.out = ln.out[0];
+        mem = {ai};
+        return true;
+    }
+
+    // [B,S,H*D] --Reshape--> [B,S,H,D] --Transpose(perm)--> ; returns the Reshape input
+    bool split_heads(const std::string& t, std::initializer_list<int64_t> perm, std::string* src,
+                     std::string* shape, std::vector<int>& mem) const {
+        const int ti = producer(t);
+        if (!is_op(ti, "Transpose") || !has_perm(ti, perm) || sole_consumer(t) < 0) return false;
+        const int ri = producer(nodes_[ti].in[0]);
+        if (!is_op(ri, "Reshape") || nodes_[ri].in.size() != 2 || sole_consumer(nodes_[ti].in[0]) != ti)
+            return false;
+        auto sh = g_.inits.find(nodes_[ri].in[1]);
+        if (sh == g_.inits.end() || sh->second.dtype != ICX_I64 || numel(sh->second.shape) != 4) return false;
+        *src = nodes_[ri].in[0];
+        *shape = nodes_[ri].in[1];
+        mem.push_back(ti);
+        mem.push_back(ri);
+        return true;
+    }
+
+    // Anchored at the Softmax of a BERT self-attention.
+    bool match_attention(int si, PlannedOp& head, std::vector<int>& mem) {
+        const Node& sm = nodes_[si];
+        if (sm.op != "Softmax" || sm.in.size() != 1 || sm.out.size() != 1) return false;
+        const int64_t axis = sm.attr_or("axis", -1);
+        if (axis != -1 && axis != 3) return false;
+        std::vector<int> m;
+        // scores scale: Div / Mul by a scalar, on the scores or on Q
+        std::string s = sm.in[0];
+        bool scaled = false;
+        int pi = producer(s);
+        if ((is_op(pi, "Div") || is_op(pi, "Mul")) && nodes_[pi].in.size() == 2 && sole_consumer(s) == si &&
+            static_scalar(nodes_[pi].in[1], &head.scale)) {
+            head.scale_div = nodes_[pi].op == "Div";
+            head.scale_q = false;
+            scaled = true;
+            m.push_back(pi);
+            s = nodes_[pi].in[0];
+        }
+        const int m1 = producer(s);
+        if (!is_op(m1, "MatMul") || nodes_[m1].in.size() != 2 || sole_consumer(s) < 0) return false;
+        m.push_back(m1);
+        std::string qa = nodes_[m1].in[0];
+        const int qs = producer(qa);
+        if (!scaled && (is_op(qs, "Div") || is_op(qs, "Mul")) && nodes_[qs].in.size() == 2 &&
+            sole_consumer(qa) == m1 && static_scalar(nodes_[qs].in[1], &head.scale)) {
+            head.scale_div = nodes_[qs].op == "Div";
+            head.scale_q = true;
+            scaled = true;
+            m.push_back(qs);
+            qa = nodes_[qs].in[0];
+        }
+        if (!scaled) {
+            head.scale = 1.0f;
+            head.scale_div = false;
+            head.scale_q = false;
+        }
+        if (!split_heads(qa, {0, 2, 1, 3}, &head.q, &head.q_shape, m)) return false;
+        if (!split_heads(nodes_[m1].in[1], {0, 2, 3, 1}, &head.k, &head.k_shape, m)) return false;
+        const int m2 = sole_consumer(sm.out[0]);
+        if (!is_op(m2, "MatMul") || nodes_[m2].in.size() != 2 || nodes_[m2].in[0] != sm.out[0]) return false;
+        m.push_back(m2);
+        if (!split_heads(nodes_[m2].in[1], {0, 2, 1, 3}, &head.v, &head.v_shape, m)) return false;
+        const int ot = sole_consumer(nodes_[m2].out[0]);
+        if (!is_op(ot, "Transpose") || !has_perm(ot, {0, 2, 1, 3})) return false;
+        const int orr = sole_consumer(nodes_[ot].out[0]);
+        if (!is_op(orr, "Reshape") || nodes_[orr].in.size() != 2) return false;
+        auto osh = g_.inits.find(nodes_[orr].in[1]);
+        if (osh == g_.inits.end() || osh->second.dtype != ICX_I64 || numel(osh->second.shape) != 3) return false;
+        m.push_back(ot);
+        m.push_back(orr);
+        const int64_t* qsh = reinterpret_cast<const int64_t*>(g_.inits[head.q_shape].data.data());
+        head.heads = qsh[2];
+        head.head_dim = qsh[3];
+        head.o_shape = nodes_[orr].in[1];
+        head.kind = Kind::FusedHead;
+        head.pattern = Pattern::Attention;
+        head.out = nodes_[orr].out[0];
+        mem = m;
         return true;
     }
 };
@@ -547,6 +814,50 @@ std::vector<int64_t> broadcast_shape(const std::vector<int64_t>& a, const std::v
     return s;
 }
 
+// ONNX Reshape target (src/operators/reshape.rs): 0 copies the input dim (allowzero = 0),
+// one -1 is inferred.
+int reshape_target(const std::vector<int64_t>& in, const std::vector<int64_t>& spec, bool allowzero,
+                   std::vector<int64_t>* out) {
+    out->assign(spec.begin(), spec.end());
+    int infer = -1;
+    int64_t known = 1;
+    for (size_t i = 0; i < spec.size(); ++i) {
+        if (spec[i] == 0 && !allowzero) {
+            if (i >= in.size()) {
+                set_error("Reshape: 0 at axis %zu copies a dimension the input does not have", i);
+                return ICX_ERR_SHAPE;
+            }
+            (*out)[i] = in[i];
+        } else if (spec[i] == -1) {
+            if (infer >= 0) {
+                set_error("Reshape: more than one -1 in the target shape");
+                return ICX_ERR_SHAPE;
+            }
+            infer = (int)i;
+            continue;
+        } else if (spec[i] < -1) {
+            set_error("Reshape: invalid target dimension %lld", (long long)spec[i]);
+            return ICX_ERR_SHAPE;
+        }
+        known *= (*out)[i];
+    }
+    const int64_t total = numel(in);
+    if (infer >= 0) {
+        if (known == 0 || total % known) {
+            set_error("Reshape: cannot infer the -1 dimension of %s for %lld elements",
+                      shape_str(spec).c_str(), (long long)total);
+            return ICX_ERR_SHAPE;
+        }
+        (*out)[infer] = total / known;
+    }
+    if (numel(*out) != total) {
+        set_error("Reshape: target %s has %lld elements, input %s has %lld", shape_str(*out).c_str(),
+                  (long long)numel(*out), shape_str(in).c_str(), (long long)total);
+        return ICX_ERR_SHAPE;
+    }
+    return ICX_OK;
+}
+
 class Runner {
    public:
     Runner(icx_graph& g, hipStream_t s) : g_(g), s_(s) {}
@@ -573,33 +884,30 @@ class Runner {
 
     int dispatch(const PlannedOp& op) {
         if (op.kind == Kind::FusedHead) {
-            if (op.pattern == Pattern::QuantizedLinear) return run_qlinear(op);
-            return run_chain(op.chain_in, op.steps, op.out, pattern_name(op.pattern));
+            switch (op.pattern) {
+                case Pattern::QuantizedLinear: return run_qlinear(op);
+                case Pattern::Attention: return run_attention(op);
+                case Pattern::AddLayerNorm:
+                    return run_layer_norm(op.ln_x, op.ln_res, op.ln_scale, op.ln_bias, op.eps, op.out,
+                                          "AddLayerNorm");
+                default: return run_chain(op.chain_in, op.steps, op.out, pattern_name(op.pattern));
+            }
         }
-        const std::string& t = op.node.op;
-        if (t == "DynamicQuantizeLinear") return run_dql(op.node);
-        if (t == "MatMulInteger") return run_matmul_integer(op.node);
-        if (t == "DequantizeLinear") return run_dequantize(op.node);
-        if (t == "Cast") return run_cast(op.node);
-        if (op_code(t) >= 0) return run_binary(op.node);
-        set_error("op '%s' is not on the quantized-linear path", t.c_str());
-        return ICX_ERR_UNSUPPORTED;
+        return run_node(op.node);
     }
 
     // Return to the pool every pooled tensor whose last reader was plan entry i, or that
-    // nothing reads.  Live outputs stay until the next run.
+    // nothing reads.  Live outputs (and buffers they alias) stay until the next run.
     void release_dead(size_t i) {
         for (auto it = g_.values.begin(); it != g_.values.end();) {
             const std::string& name = it->first;
-            const bool is_out =
-                std::find(g_.live_outputs.begin(), g_.live_outputs.end(), name) != g_.live_outputs.end();
             std::string key = name;
             const size_t sfx = name.rfind("::rowsum");
             if (sfx != std::string::npos) key = name.substr(0, sfx);
             auto lu = g_.last_use.find(key);
-            const bool dead = lu == g_.last_use.end() || lu->second <= i;
-            if (it->second.pooled && !is_out && dead) {
-                g_.pool.put(it->second.ptr, it->second.cls);
+            const bool dead = !g_.keep.count(name) && (lu == g_.last_use.end() || lu->second <= i);
+            if (dead) {
+                if (it->second.pooled) g_.pool.put(it->second.ptr, it->second.cls);
                 it = g_.values.erase(it);
             } else {
                 ++it;
@@ -610,6 +918,36 @@ class Runner {
    private:
     icx_graph& g_;
     hipStream_t s_;
+
+    int run_node(const Node& n) {
+        const std::string& t = n.op;
+        if (t == "DynamicQuantizeLinear") return run_dql(n);
+        if (t == "MatMulInteger") return run_matmul_integer(n);
+        if (t == "DequantizeLinear") return run_dequantize(n);
+        if (t == "Cast") return run_cast(n);
+        if (t == "LayerNormalization") {
+            const DevTensor* x = n.in.empty() ? nullptr : find(n.in[0]);
+            const int64_t axis = n.attr_or("axis", -1);
+            if (n.in.size() != 3 || !x || (axis != -1 && axis != (int64_t)x->shape.size() - 1)) {
+                set_error("LayerNormalization: only the last axis, with scale and bias, is on this path");
+                return ICX_ERR_UNSUPPORTED;
+            }
+            return run_layer_norm(n.in[0], "", n.in[1], n.in[2], (float)n.fattr_or("epsilon", 1e-5), n.out[0],
+                                  "LayerNormalization");
+        }
+        if (t == "Softmax") return run_softmax(n);
+        if (t == "Erf") {
+            Step st;
+            st.op = ICX_OP_ERF;
+            return run_chain(n.in[0], {st}, n.out[0], "Erf");
+        }
+        if (t == "Transpose") return run_transpose(n);
+        if (t == "Reshape") return run_reshape(n);
+        if (t == "MatMul") return run_matmul_f32(n);
+        if (op_code(t) >= 0) return run_binary(n);
+        set_error("op '%s' is not on the quantized-linear path", t.c_str());
+        return ICX_ERR_UNSUPPORTED;
+    }
 
     const DevTensor* find(const std::string& name) const {
         auto v = g_.values.find(name);
@@ -655,16 +993,19 @@ class Runner {
         g_.ws_bytes = bytes;
         return ICX_OK;
     }
+    int need_f32(const std::string& name, const DevTensor** out, const char* who) const {
+        int rc = need(name, out, who);
+        if (rc) return rc;
+        if ((*out)->dtype == ICX_F32) return ICX_OK;
+        set_error("%s: '%s' must be Float32, got %s", who, name.c_str(), dtype_name((*out)->dtype));
+        return ICX_ERR_DTYPE;
+    }
 
     int chain_operand(const std::string& name, const std::vector<int64_t>& out_shape, const char* who,
                       int32_t* kind, const float** p) const {
         const DevTensor* t;
-        int rc = need(name, &t, who);
+        int rc = need_f32(name, &t, who);
         if (rc) return rc;
-        if (t->dtype != ICX_F32) {
-            set_error("%s: operand '%s' must be Float32, got %s", who, name.c_str(), dtype_name(t->dtype));
-            return ICX_ERR_DTYPE;
-        }
         *kind = bcast_kind(t->shape, out_shape);
         *p = static_cast<const float*>(t->ptr);
         if (*kind >= 0) return ICX_OK;
@@ -680,6 +1021,7 @@ class Runner {
             icx_chain_op& o = ch.ops[k];
             o.op = steps[k].op;
             o.operand_is_lhs = steps[k].lhs ? 1 : 0;
+            if (steps[k].op > ICX_OP_DIV) continue;  // operand-free step
             int rc = chain_operand(steps[k].opnd0, out_shape, who, &o.kind0, &o.p0);
             if (rc) return rc;
             if (!steps[k].opnd1.empty()) {
@@ -782,6 +1124,218 @@ class Runner {
                                rowsum, &ch, static_cast<float*>(Y->ptr), g_.ws, g_.ws_bytes);
     }
 
+    int shape_init(const std::string& name, std::vector<int64_t>* v) const {
+        auto it = g_.inits.find(name);
+        if (it == g_.inits.end() || it->second.dtype != ICX_I64) {
+            set_error("Reshape: shape '%s' must be an Int64 initializer", name.c_str());
+            return ICX_ERR_UNSUPPORTED;
+        }
+        const int64_t* p = reinterpret_cast<const int64_t*>(it->second.data.data());
+        v->assign(p, p + numel(it->second.shape));
+        return ICX_OK;
+    }
+
+    // Fused attention, or its member nodes when the shapes are outside the kernel.
+    int run_attention(const PlannedOp& op) {
+        const DevTensor *Q, *K, *V;
+        int rc = need_f32(op.q, &Q, "Attention");
+        if (!rc) rc = need_f32(op.k, &K, "Attention");
+        if (!rc) rc = need_f32(op.v, &V, "Attention");
+        if (rc) return rc;
+        bool fused = Q->shape.size() == 3 && Q->shape == K->shape && Q->shape == V->shape && op.head_dim == 64 &&
+                     op.heads > 0 && Q->shape[2] == op.heads * op.head_dim && Q->shape[1] > 0 && Q->shape[1] <= 128;
+        std::vector<int64_t> split = {Q->shape.empty() ? 0 : Q->shape[0], Q->shape.size() > 1 ? Q->shape[1] : 0,
+                                      op.heads, op.head_dim};
+        for (const std::string* sh : {&op.q_shape, &op.k_shape, &op.v_shape}) {
+            std::vector<int64_t> spec, tgt;
+            if (!fused) break;
+            if (shape_init(*sh, &spec) || reshape_target(Q->shape, spec, false, &tgt) || tgt != split) fused = false;
+        }
+        std::vector<int64_t> oshape;
+        if (fused) {
+            std::vector<int64_t> spec;
+            std::vector<int64_t> full = {Q->shape[0], Q->shape[1], op.heads, op.head_dim};
+            if (shape_init(op.o_shape, &spec) || reshape_target(full, spec, false, &oshape) || oshape != Q->shape)
+                fused = false;
+        }
+        icx::clear_error();
+        if (!fused) {  // run the decomposed subgraph as the reference does
+            for (const Node& m : op.sub) {
+                rc = run_node(m);
+                if (rc) return rc;
+            }
+            return ICX_OK;
+        }
+        const std::vector<int64_t> shape = Q->shape;
+        const float *q = static_cast<const float*>(Q->ptr), *k = static_cast<const float*>(K->ptr),
+                    *v = static_cast<const float*>(V->ptr);
+        DevTensor* O;
+        rc = alloc(op.out, ICX_F32, shape, &O);
+        if (rc) return rc;
+        const size_t hd = (size_t)shape[2];
+        return icx_attention_f32(s_, q, k, v, shape[0], shape[1], op.heads, op.head_dim, hd, hd, hd, hd, op.scale,
+                                 op.scale_div ? 1 : 0, op.scale_q ? 1 : 0, static_cast<float*>(O->ptr));
+    }
+
+    int run_layer_norm(const std::string& xn, const std::string& resn, const std::string& sn, const std::string& bn,
+                       float eps, const std::string& out, const char* who) {
+        const DevTensor *X, *R = nullptr, *S, *B;
+        int rc = need_f32(xn, &X, who);
+        if (!rc && !resn.empty()) rc = need_f32(resn, &R, who);
+        if (!rc) rc = need_f32(sn, &S, who);
+        if (!rc) rc = need_f32(bn, &B, who);
+        if (rc) return rc;
+        if (R && R->shape != X->shape) {
+            // the Add broadcasts: materialise it, then normalise
+            Step st;
+            st.op = ICX_OP_ADD;
+            bool ok;
+            const std::vector<int64_t> bs = broadcast_shape(X->shape, R->shape, &ok);
+            const bool x_full = bs == X->shape;
+            st.opnd0 = x_full ? resn : xn;
+            st.lhs = !x_full;
+            const std::string tmp = out + "::sum";
+            rc = run_chain(x_full ? xn : resn, {st}, tmp, who);
+            if (rc) return rc;
+            return run_layer_norm(tmp, "", sn, bn, eps, out, who);
+        }
+        if (X->shape.empty()) {
+            set_error("%s: input must have at least one axis", who);
+            return ICX_ERR_SHAPE;
+        }
+        const int64_t cols = X->shape.back();
+        if (numel(S->shape) != cols || numel(B->shape) != cols) {
+            set_error("%s: scale %s / bias %s do not match the normalised axis (%lld)", who,
+                      shape_str(S->shape).c_str(), shape_str(B->shape).c_str(), (long long)cols);
+            return ICX_ERR_SHAPE;
+        }
+        const std::vector<int64_t> shape = X->shape;
+        const float *x = static_cast<const float*>(X->ptr), *r = R ? static_cast<const float*>(R->ptr) : nullptr,
+                    *sc = static_cast<const float*>(S->ptr), *bi = static_cast<const float*>(B->ptr);
+        DevTensor* Y;
+        rc = alloc(out, ICX_F32, shape, &Y);
+        if (rc) return rc;
+        return icx_layer_norm_f32(s_, x, r, cols ? numel(shape) / cols : 0, cols, sc, bi, eps,
+                                  static_cast<float*>(Y->ptr));
+    }
+
+    int run_softmax(const Node& n) {
+        const DevTensor* X;
+        int rc = need_f32(n.in[0], &X, "Softmax");
+        if (rc) return rc;
+        const int64_t rank = (int64_t)X->shape.size();
+        const int64_t axis = n.attr_or("axis", -1);
+        if (rank == 0 || (axis != -1 && axis != rank - 1)) {
+            set_error("Softmax: only the last axis is on this path (axis %lld of rank %lld)", (long long)axis,
+                      (long long)rank);
+            return ICX_ERR_UNSUPPORTED;
+        }
+        const std::vector<int64_t> shape = X->shape;
+        const float* x = static_cast<const float*>(X->ptr);
+        DevTensor* Y;
+        rc = alloc(n.out[0], ICX_F32, shape, &Y);
+        if (rc) return rc;
+        const int64_t cols = shape.back();
+        return icx_softmax_f32(s_, x, cols ? numel(shape) / cols : 0, cols, static_cast<float*>(Y->ptr));
+    }
+
+    int run_transpose(const Node& n) {
+        const DevTensor* X;
+        int rc = need(n.in[0], &X, "Transpose");
+        if (rc) return rc;
+        const int rank = (int)X->shape.size();
+        std::vector<int> perm(rank);
+        auto it = n.iattrs.find("perm");
+        for (int d = 0; d < rank; ++d) perm[d] = it == n.iattrs.end() ? rank - 1 - d : (int)it->second[d];
+        if (it != n.iattrs.end() && (int)it->second.size() != rank) {
+            set_error("Transpose: perm of length %zu for a rank-%d input", it->second.size(), rank);
+            return ICX_ERR_SHAPE;
+        }
+        std::vector<int64_t> oshape(rank);
+        for (int d = 0; d < rank; ++d) {
+            if (perm[d] < 0 || perm[d] >= rank) {
+                set_error("Transpose: perm is not a permutation");
+                return ICX_ERR_INVALID_ARG;
+            }
+            oshape[d] = X->shape[perm[d]];
+        }
+        const std::vector<int64_t> ishape = X->shape;
+        const void* x = X->ptr;
+        const int dt = X->dtype;
+        DevTensor* Y;
+        rc = alloc(n.out[0], dt, oshape, &Y);
+        if (rc) return rc;
+        return icx_transpose(s_, x, dtype_size(dt), rank, ishape.data(), perm.data(), Y->ptr);
+    }
+
+    // Reshape: the output names the input's buffer with a new shape (no copy).
+    int run_reshape(const Node& n) {
+        if (n.in.size() != 2) {
+            set_error("Reshape requires 2 inputs, got %zu", n.in.size());
+            return ICX_ERR_INVALID_ARG;
+        }
+        const DevTensor* X;
+        int rc = need(n.in[0], &X, "Reshape");
+        if (rc) return rc;
+        std::vector<int64_t> spec, tgt;
+        rc = shape_init(n.in[1], &spec);
+        if (!rc) rc = reshape_target(X->shape, spec, n.attr_or("allowzero", 0) != 0, &tgt);
+        if (rc) return rc;
+        DevTensor t = *X;
+        t.shape = tgt;
+        t.pooled = false;  // the buffer belongs to the input (kept alive by its last use)
+        g_.values[n.out[0]] = t;
+        return ICX_OK;
+    }
+
+    // f32 MatMul with the reference's batch rules (src/operators/matmul.rs:60-90).
+    int run_matmul_f32(const Node& n) {
+        const DevTensor *A, *B;
+        int rc = need_f32(n.in[0], &A, "MatMul");
+        if (!rc) rc = need_f32(n.in[1], &B, "MatMul");
+        if (rc) return rc;
+        if (A->shape.size() < 2 || B->shape.size() < 2) {
+            set_error("MatMul: 1-D operands are not on this path (%s x %s)", shape_str(A->shape).c_str(),
+                      shape_str(B->shape).c_str());
+            return ICX_ERR_UNSUPPORTED;
+        }
+        const int64_t M = A->shape[A->shape.size() - 2], K = A->shape.back();
+        const int64_t Kb = B->shape[B->shape.size() - 2], N = B->shape.back();
+        if (K != Kb) {
+            set_error("MatMul: inner dimensions must match: %lld != %lld", (long long)K, (long long)Kb);
+            return ICX_ERR_SHAPE;
+        }
+        const std::vector<int64_t> ab(A->shape.begin(), A->shape.end() - 2), bb(B->shape.begin(), B->shape.end() - 2);
+        std::vector<int64_t> ob;
+        int b_bcast = 0;
+        bool a_bcast = false;
+        if (ab.empty() && !bb.empty()) {
+            ob = bb;
+            a_bcast = true;
+        } else if (!ab.empty() && bb.empty()) {
+            ob = ab;
+            b_bcast = 1;
+        } else if (ab == bb) {
+            ob = ab;
+        } else {
+            set_error("MatMul: batch dimensions must be compatible for broadcasting: %s vs %s",
+                      shape_str(ab).c_str(), shape_str(bb).c_str());
+            return ICX_ERR_SHAPE;
+        }
+        if (a_bcast) {
+            set_error("MatMul: a 2-D left operand with a batched right operand is not on this path");
+            return ICX_ERR_UNSUPPORTED;
+        }
+        std::vector<int64_t> oshape = ob;
+        oshape.push_back(M);
+        oshape.push_back(N);
+        const float *a = static_cast<const float*>(A->ptr), *b = static_cast<const float*>(B->ptr);
+        DevTensor* C;
+        rc = alloc(n.out[0], ICX_F32, oshape, &C);
+        if (rc) return rc;
+        return icx_matmul_f32(s_, a, b, (size_t)numel(ob), b_bcast, M, K, N, static_cast<float*>(C->ptr));
+    }
+
     int run_matmul_integer(const Node& n) {
         if (n.in.size() < 2 || n.in.size() > 4) {
             set_error("MatMulInteger requires 2, 3, or 4 inputs, got %zu", n.in.size());
@@ -880,12 +1434,8 @@ class Runner {
     int run_chain(const std::string& in_name, const std::vector<Step>& steps, const std::string& out_name,
                   const char* who) {
         const DevTensor* X;
-        int rc = need(in_name, &X, who);
+        int rc = need_f32(in_name, &X, who);
         if (rc) return rc;
-        if (X->dtype != ICX_F32) {
-            set_error("%s: input '%s' must be Float32, got %s", who, in_name.c_str(), dtype_name(X->dtype));
-            return ICX_ERR_DTYPE;
-        }
         const std::vector<int64_t> shape = X->shape;
         const float* x = static_cast<const float*>(X->ptr);
         const int64_t cols = shape.empty() ? 1 : shape.back();
@@ -1046,7 +1596,8 @@ extern "C" int icx_graph_add_initializer(icx_graph* g, const char* name, int dty
                                          const int64_t* dims, const void* host_data) {
     icx::clear_error();
     if (!g || !name || rank < 0 || (rank && !dims)) ICX_FAIL(ICX_ERR_INVALID_ARG, "add_initializer: bad arguments");
-    if (!valid_dtype(dtype)) ICX_FAIL(ICX_ERR_DTYPE, "add_initializer: '%s' has unsupported dtype %d", name, dtype);
+    if (!valid_dtype(dtype) && dtype != ICX_I64)
+        ICX_FAIL(ICX_ERR_DTYPE, "add_initializer: '%s' has unsupported dtype %d", name, dtype);
     HostTensor t;
     t.dtype = dtype;
     t.shape.assign(dims, dims + rank);
@@ -1068,6 +1619,7 @@ extern "C" int icx_graph_add_node(icx_graph* g, const char* name, const char* op
     if (!g || !name || !op_type || n_in < 0 || n_out < 1 || !outputs || n_attr < 0 ||
         (n_attr && (!attr_names || !attr_values)))
         ICX_FAIL(ICX_ERR_INVALID_ARG, "add_node: bad arguments");
+    if (g->find_node(name)) ICX_FAIL(ICX_ERR_INVALID_ARG, "add_node: a node named '%s' exists", name);
     Node n;
     n.name = name;
     n.op = op_type;
@@ -1075,6 +1627,28 @@ extern "C" int icx_graph_add_node(icx_graph* g, const char* name, const char* op
     n.out = names_of(n_out, outputs);
     for (int i = 0; i < n_attr; ++i) n.attr[attr_names[i] ? attr_names[i] : ""] = attr_values[i];
     g->nodes.push_back(std::move(n));
+    g->invalidate();
+    return ICX_OK;
+}
+
+extern "C" int icx_graph_set_node_attr_float(icx_graph* g, const char* node, const char* attr, double value) {
+    icx::clear_error();
+    if (!g || !node || !attr) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_node_attr_float: bad arguments");
+    Node* n = g->find_node(node);
+    if (!n) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_node_attr_float: no node '%s'", node);
+    n->fattr[attr] = value;
+    g->invalidate();
+    return ICX_OK;
+}
+
+extern "C" int icx_graph_set_node_attr_ints(icx_graph* g, const char* node, const char* attr, int count,
+                                            const int64_t* values) {
+    icx::clear_error();
+    if (!g || !node || !attr || count < 0 || (count && !values))
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "set_node_attr_ints: bad arguments");
+    Node* n = g->find_node(node);
+    if (!n) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_node_attr_ints: no node '%s'", node);
+    n->iattrs[attr] = std::vector<int64_t>(values, values + count);
     g->invalidate();
     return ICX_OK;
 }
@@ -1090,7 +1664,6 @@ extern "C" int icx_graph_add_output(icx_graph* g, const char* name) {
 }
 
 static int icx_graph_plan_impl(icx_graph* g, char* buf, size_t buf_len) {
-    icx::clear_error();
     if (!g) ICX_FAIL(ICX_ERR_INVALID_ARG, "plan: null graph");
     if (!g->planned) {
         Planner p(*g);
@@ -1110,7 +1683,7 @@ static int icx_graph_plan_impl(icx_graph* g, char* buf, size_t buf_len) {
             }
             o << "\n";
             for (auto& m : op.members)
-                o << m.first << " " << m.second << " " << kind_name(Kind::Skip) << " " << pattern_name(op.pattern) << "\n";
+                o << m.name << " " << m.op << " " << kind_name(Kind::Skip) << " " << pattern_name(op.pattern) << "\n";
         }
         for (auto& r : g->rowsum_wanted) o << "rowsum " << r << "\n";
         const std::string s = o.str();
@@ -1122,7 +1695,6 @@ static int icx_graph_plan_impl(icx_graph* g, char* buf, size_t buf_len) {
 }
 
 static int icx_graph_compile_impl(icx_graph* g, icx_stream_t stream) {
-    icx::clear_error();
     if (!g) ICX_FAIL(ICX_ERR_INVALID_ARG, "compile: null graph");
     int rc = icx_graph_plan_impl(g, nullptr, 0);
     if (rc) return rc;
@@ -1143,6 +1715,7 @@ static int icx_graph_compile_impl(icx_graph* g, icx_stream_t stream) {
     }
     for (auto& kv : g->inits) {
         const HostTensor& h = kv.second;
+        if (h.dtype == ICX_I64) continue;  // shapes: read on the host only
         DevTensor t;
         t.dtype = h.dtype;
         t.shape = h.shape;
@@ -1197,7 +1770,6 @@ extern "C" int icx_graph_set_input(icx_graph* g, const char* name, int dtype, in
 }
 
 static int icx_graph_run_impl(icx_graph* g, icx_stream_t stream) {
-    icx::clear_error();
     if (!g) ICX_FAIL(ICX_ERR_INVALID_ARG, "run: null graph");
     int rc = icx_graph_compile_impl(g, stream);
     if (rc) return rc;
@@ -1262,6 +1834,7 @@ extern "C" int icx_graph_pool_stats(icx_graph* g, int64_t* hipmallocs, int64_t* 
 }
 
 extern "C" int icx_graph_plan(icx_graph* g, char* buf, size_t buf_len) {
+    icx::clear_error();
     try {
         return icx_graph_plan_impl(g, buf, buf_len);
     } catch (const std::exception& e) {
@@ -1271,6 +1844,7 @@ extern "C" int icx_graph_plan(icx_graph* g, char* buf, size_t buf_len) {
 }
 
 extern "C" int icx_graph_compile(icx_graph* g, icx_stream_t stream) {
+    icx::clear_error();
     try {
         return icx_graph_compile_impl(g, stream);
     } catch (const std::exception& e) {
@@ -1280,6 +1854,7 @@ extern "C" int icx_graph_compile(icx_graph* g, icx_stream_t stream) {
 }
 
 extern "C" int icx_graph_run(icx_graph* g, icx_stream_t stream) {
+    icx::clear_error();
     try {
         return icx_graph_run_impl(g, stream);
     } catch (const std::exception& e) {

@@ -8,11 +8,14 @@ the memory pool and per-op dispatch all live in the native library
 device tensors across the boundary.
 
 Differences from the reference that a caller can see:
-  * only the ops of the quantized-linear path dispatch (DynamicQuantizeLinear,
-    MatMulInteger, DequantizeLinear, Cast to FLOAT, Mul/Add/Sub/Div); any other op raises
+  * only the ops of the quantized-linear path and the encoder around it dispatch
+    (DynamicQuantizeLinear, MatMulInteger, DequantizeLinear, Cast to FLOAT, Mul/Add/Sub/Div,
+    LayerNormalization, Softmax, Erf, Transpose, Reshape, f32 MatMul); any other op raises
     IconnxError at run naming the node;
-  * ``MatMulInteger -> Cast -> Mul(scale) [-> Add(bias)] [-> Mul/Add/Sub/Div]*`` runs as one
-    fused GEMM (pattern ``QuantizedLinear``); the reference leaves it unfused;
+  * ``MatMulInteger -> Cast -> Mul(scale) [-> Add(bias)] [-> chain] [-> erf-GELU]`` runs as
+    one fused GEMM (pattern ``QuantizedLinear``), a BERT self-attention subgraph as one
+    kernel (``Attention``), and ``LayerNormalization(Add(a, b))`` as one (``AddLayerNorm``);
+    the reference leaves these unfused;
   * ``run_device`` returns device tensors without the host round trip.
 """
 import ctypes
@@ -20,10 +23,11 @@ from collections import namedtuple
 
 import numpy as np
 
-from ._lib import ICX_F32, ICX_I8, ICX_I32, ICX_U8, IconnxError, check, lib
+from ._lib import ICX_F32, ICX_I8, ICX_I32, ICX_I64, ICX_U8, IconnxError, check, lib
 
 _NP_DT = {np.dtype(np.int8): ICX_I8, np.dtype(np.uint8): ICX_U8,
           np.dtype(np.int32): ICX_I32, np.dtype(np.float32): ICX_F32}
+_INIT_DT = {**_NP_DT, np.dtype(np.int64): ICX_I64}
 _DT_NP = {v: k for k, v in _NP_DT.items()}
 
 PlanEntry = namedtuple("PlanEntry", "node op_type kind pattern steps out wzp_folded")
@@ -103,11 +107,12 @@ class GpuGraphExecutor:
         check(self._L.icx_graph_add_input(self._g, name.encode(), len(dims), _dims(dims)))
 
     def add_initializer(self, name, tensor):
-        """Host array (numpy or CPU torch).  Int8 / UInt8 / Int32 / Float32 are kept; other
-        dtypes are skipped, so a node reading one fails at run (as the reference does)."""
+        """Host array (numpy or CPU torch).  Int8 / UInt8 / Int32 / Float32 are kept, Int64
+        too (shape constants, read on the host); other dtypes are skipped, so a node reading
+        one fails at run (as the reference does)."""
         arr = tensor.numpy() if hasattr(tensor, "numpy") and not isinstance(tensor, np.ndarray) \
             else np.asarray(tensor)
-        code = _NP_DT.get(arr.dtype)
+        code = _INIT_DT.get(arr.dtype)
         if code is None:
             return
         arr = np.ascontiguousarray(arr)
@@ -116,15 +121,24 @@ class GpuGraphExecutor:
             arr.ctypes.data_as(ctypes.c_void_p)))
 
     def add_node(self, name, op_type, inputs, outputs, attributes=None):
-        """Attributes: integer-valued ones (``to``, ``axis``) are passed; others are not on
-        this path and are ignored."""
-        attrs = {k: int(v) for k, v in (attributes or {}).items()
+        """Attributes: ints (``to``, ``axis``), floats (``epsilon``) and int lists
+        (``perm``); others are not read by any op here and are ignored."""
+        attributes = attributes or {}
+        attrs = {k: int(v) for k, v in attributes.items()
                  if isinstance(v, (int, np.integer)) and not isinstance(v, bool)}
         keys = list(attrs)
         vals = (ctypes.c_int64 * max(len(keys), 1))(*[attrs[k] for k in keys])
         check(self._L.icx_graph_add_node(
             self._g, name.encode(), op_type.encode(), len(inputs), _cstrs(list(inputs)),
             len(outputs), _cstrs(list(outputs)), len(keys), _cstrs(keys), vals))
+        for k, v in attributes.items():
+            if isinstance(v, (float, np.floating)):
+                check(self._L.icx_graph_set_node_attr_float(self._g, name.encode(), k.encode(),
+                                                            float(v)))
+            elif isinstance(v, (list, tuple)) and all(isinstance(x, (int, np.integer)) for x in v):
+                arr = (ctypes.c_int64 * max(len(v), 1))(*[int(x) for x in v])
+                check(self._L.icx_graph_set_node_attr_ints(self._g, name.encode(), k.encode(),
+                                                           len(v), arr))
 
     def add_output(self, name):
         if name not in self._outputs:

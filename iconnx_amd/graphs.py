@@ -16,6 +16,7 @@ src/cuda/executor/layout.rs:978-1095, 1254-1271; elementwise.rs:54-200):
 import numpy as np
 
 from . import configs
+from .synth import seeded_normal, seeded_uniform
 
 
 def add_dynamic_quantize(ex, x, prefix):
@@ -26,12 +27,28 @@ def add_dynamic_quantize(ex, x, prefix):
     return tuple(outs)
 
 
-def add_quantized_linear(ex, x, w, w_zp, w_scale, bias, chain=(), prefix="ql", dql=None):
+def add_gelu(ex, x, prefix):
+    """x * 0.5 * (1 + erf(x / sqrt 2)) as PyTorch exports it: Div, Erf, Add, Mul(x, .),
+    Mul(., 0.5).  Returns the output name."""
+    p = prefix
+    for name, val in (("sqrt2", 1.4142135381698608), ("one", 1.0), ("half", 0.5)):
+        ex.add_initializer("%s.%s" % (p, name), np.array(val, np.float32))
+    ex.add_node(p + ".div", "Div", [x, p + ".sqrt2"], [p + ".d"])
+    ex.add_node(p + ".erf", "Erf", [p + ".d"], [p + ".e"])
+    ex.add_node(p + ".add1", "Add", [p + ".e", p + ".one"], [p + ".a"])
+    ex.add_node(p + ".mulx", "Mul", [x, p + ".a"], [p + ".m"])
+    ex.add_node(p + ".mulhalf", "Mul", [p + ".m", p + ".half"], [p + ".gelu"])
+    return p + ".gelu"
+
+
+def add_quantized_linear(ex, x, w, w_zp, w_scale, bias, chain=(), prefix="ql", dql=None,
+                         gelu=False):
     """Add one quantized linear (+ chain) reading tensor ``x``; returns the output name.
 
     ``w`` int8/uint8 [K, N]; ``w_zp`` scalar or [N] (None: absent input); ``w_scale``
     scalar or [N]; ``bias`` [N] or None; ``chain`` items are (op, constant) or
-    (op, constant, constant_is_lhs).  ``dql`` reuses an existing quantization of x."""
+    (op, constant, constant_is_lhs); ``gelu`` appends an erf-GELU.  ``dql`` reuses an
+    existing quantization of x."""
     xq, xs, xzp = dql if dql is not None else add_dynamic_quantize(ex, x, prefix)
     p = prefix
     ex.add_initializer(p + ".W", np.asarray(w))
@@ -57,6 +74,8 @@ def add_quantized_linear(ex, x, w, w_zp, w_scale, bias, chain=(), prefix="ql", d
         out = "%s.chain%d" % (p, i)
         ex.add_node("%s.%s%d" % (p, op.lower(), i), op, [cname, y] if lhs else [y, cname], [out])
         y = out
+    if gelu:
+        y = add_gelu(ex, y, p + ".gelu")
     return y
 
 
@@ -71,3 +90,98 @@ def config_graph(ex, cfg, x_name="x", x_shape=None):
     y = add_quantized_linear(ex, x_name, d["w"], w_zp, d["w_scale"], d["bias"], d["chain"],
                              prefix=cfg)
     return y, d
+
+
+# ---------------------------------------------------------------------------------------
+# DistilBERT-shaped encoder: 6 layers, hidden 768, 12 heads of 64,
+# FFN 3072, random-init weights, every linear quantized dynamically.
+# ---------------------------------------------------------------------------------------
+ENCODER = dict(layers=6, hidden=768, heads=12, ffn=3072, batch=32, seq=128, eps=1e-12)
+
+
+def encoder_layer_params(layer, hidden=768, ffn=3072, seed=3000):
+    """Seeded random-init weights of one layer: int8 weights uniform in [-127, 127] with a
+    per-tensor scale of 5e-4 (std ~0.036 = 1/sqrt(768)) and zero point 0, biases and
+    LayerNorm shifts ~ N(0, 0.02), LayerNorm gains ~ U(0.9, 1.1)."""
+    base = seed + 100 * layer
+    p = {}
+    shapes = {"q": (hidden, hidden), "k": (hidden, hidden), "v": (hidden, hidden),
+              "o": (hidden, hidden), "ff1": (hidden, ffn), "ff2": (ffn, hidden)}
+    for i, (name, (K, N)) in enumerate(shapes.items()):
+        p[name] = dict(w=configs.weight_i8(K, N, base + 10 * i),
+                       w_zp=np.array(0, np.int8), w_scale=np.array(5e-4, np.float32),
+                       bias=(0.02 * seeded_normal(N, base + 10 * i + 1).astype(np.float64)).astype(np.float32))
+    for i, name in enumerate(("ln1", "ln2")):
+        p[name] = dict(scale=seeded_uniform(hidden, base + 80 + 2 * i, 0.9, 1.1),
+                       bias=(0.02 * seeded_normal(hidden, base + 81 + 2 * i).astype(np.float64)).astype(np.float32))
+    return p
+
+
+def add_self_attention(ex, q, k, v, heads, head_dim, prefix):
+    """The exported BERT attention subgraph over [B, S, H*D] tensors q, k, v (DistilBERT
+    scales q by 1/sqrt(D) before the product).  Returns the [B, S, H*D] context name."""
+    p = prefix
+    ex.add_initializer(p + ".split", np.array([0, 0, heads, head_dim], np.int64))
+    ex.add_initializer(p + ".merge", np.array([0, 0, heads * head_dim], np.int64))
+    ex.add_initializer(p + ".sqrt_d", np.array(np.sqrt(head_dim), np.float32))
+    for t, perm in ((q, [0, 2, 1, 3]), (k, [0, 2, 3, 1]), (v, [0, 2, 1, 3])):
+        tag = {q: "q", k: "k", v: "v"}[t]
+        ex.add_node("%s.reshape_%s" % (p, tag), "Reshape", [t, p + ".split"], ["%s.%s4" % (p, tag)])
+        ex.add_node("%s.transpose_%s" % (p, tag), "Transpose", ["%s.%s4" % (p, tag)],
+                    ["%s.%st" % (p, tag)], {"perm": perm})
+    ex.add_node(p + ".scale_q", "Div", [p + ".qt", p + ".sqrt_d"], [p + ".qs"])
+    ex.add_node(p + ".scores", "MatMul", [p + ".qs", p + ".kt"], [p + ".s"])
+    ex.add_node(p + ".softmax", "Softmax", [p + ".s"], [p + ".p"], {"axis": -1})
+    ex.add_node(p + ".context", "MatMul", [p + ".p", p + ".vt"], [p + ".c"])
+    ex.add_node(p + ".transpose_c", "Transpose", [p + ".c"], [p + ".ct"], {"perm": [0, 2, 1, 3]})
+    ex.add_node(p + ".reshape_c", "Reshape", [p + ".ct", p + ".merge"], [p + ".ctx"])
+    return p + ".ctx"
+
+
+def add_layer_norm(ex, x, residual, scale, bias, eps, prefix):
+    """LayerNormalization(Add(x, residual)); returns the output name."""
+    p = prefix
+    ex.add_initializer(p + ".gamma", np.asarray(scale, np.float32))
+    ex.add_initializer(p + ".beta", np.asarray(bias, np.float32))
+    ex.add_node(p + ".residual", "Add", [x, residual], [p + ".sum"])
+    ex.add_node(p + ".norm", "LayerNormalization", [p + ".sum", p + ".gamma", p + ".beta"],
+                [p + ".out"], {"axis": -1, "epsilon": float(eps)})
+    return p + ".out"
+
+
+def add_encoder_layer(ex, x, params, heads, eps, prefix):
+    """One post-LN transformer layer; returns a dict of the layer's tensor names."""
+    p = prefix
+    hidden = params["q"]["w"].shape[0]
+    lin = lambda name, inp, **kw: add_quantized_linear(
+        ex, inp, params[name]["w"], params[name]["w_zp"], params[name]["w_scale"],
+        params[name]["bias"], prefix="%s.%s" % (p, name), **kw)
+    dql = add_dynamic_quantize(ex, x, p + ".qkv")
+    q, k, v = (lin(n, x, dql=dql) for n in ("q", "k", "v"))
+    ctx = add_self_attention(ex, q, k, v, heads, hidden // heads, p + ".attn")
+    o = lin("o", ctx)
+    x1 = add_layer_norm(ex, o, x, params["ln1"]["scale"], params["ln1"]["bias"], eps, p + ".ln1")
+    h = lin("ff1", x1, gelu=True)
+    f = lin("ff2", h)
+    x2 = add_layer_norm(ex, f, x1, params["ln2"]["scale"], params["ln2"]["bias"], eps, p + ".ln2")
+    return dict(x=x, xq=dql[0], q=q, k=k, v=v, ctx=ctx, o=o, x1=x1, h=h, f=f, out=x2)
+
+
+def encoder_graph(ex, layers=6, heads=12, hidden=768, ffn=3072, eps=1e-12, x_name="x",
+                  x_shape=None, seed=3000):
+    """The DistilBERT-shaped encoder on executor ``ex``.  Returns (output name, per-layer
+    tensor names, per-layer params)."""
+    ex.add_input(x_name, x_shape if x_shape is not None else [None, None, hidden])
+    x, names, params = x_name, [], []
+    for l in range(layers):
+        prm = encoder_layer_params(l, hidden, ffn, seed)
+        t = add_encoder_layer(ex, x, prm, heads, eps, "L%d" % l)
+        names.append(t)
+        params.append(prm)
+        x = t["out"]
+    return x, names, params
+
+
+def encoder_input(batch=32, seq=128, hidden=768, seed=2999):
+    """Input embeddings ~ N(0, 1), [batch, seq, hidden] float32."""
+    return seeded_normal(batch * seq * hidden, seed).reshape(batch, seq, hidden)

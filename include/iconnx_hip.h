@@ -34,7 +34,8 @@ typedef enum {
     ICX_ERR_UNSUPPORTED = 6, /* outside what this build implements */
 } icx_status;
 
-typedef enum { ICX_I8 = 0, ICX_U8 = 1, ICX_I32 = 2, ICX_F32 = 3 } icx_dtype;
+/* ICX_I64 is accepted for graph initializers only (Reshape shapes, read on the host). */
+typedef enum { ICX_I8 = 0, ICX_U8 = 1, ICX_I32 = 2, ICX_F32 = 3, ICX_I64 = 4 } icx_dtype;
 
 const char* icx_status_str(int status);
 /* Message of the last failing call on this host thread ("" if none). */
@@ -188,15 +189,21 @@ int icx_attention_f32(icx_stream_t stream, const float* q, const float* k, const
  * Mirrors GpuGraphExecutor (src/cuda/inference/mod.rs:208-659): add_input (:306),
  * add_initializer (:317), add_node (:331), a lowering step (ir::lower,
  * src/ir/lowering.rs:31-238: topological sort, fusion decision, initializer upload) and run
- * (:428) with the input-shape guard (:441-460).  Only the ops of the quantized-linear path
- * are dispatched: DynamicQuantizeLinear, MatMulInteger (2-D and 3-D x 2-D,
- * layout.rs:1034-1095), DequantizeLinear, Cast (to FLOAT), Mul / Add / Sub / Div;
- * anything else is an ICX_ERR_UNSUPPORTED error naming the op.
+ * (:428) with the input-shape guard (:441-460).  Ops dispatched: DynamicQuantizeLinear,
+ * MatMulInteger (2-D and 3-D x 2-D, layout.rs:1034-1095), DequantizeLinear, Cast (to
+ * FLOAT), Mul / Add / Sub / Div, and the encoder's LayerNormalization, Softmax, Erf,
+ * Transpose, Reshape (Int64 shape initializer; the output aliases the input) and f32
+ * MatMul; anything else is an ICX_ERR_UNSUPPORTED error naming the node.
  * Fused patterns (src/cuda/inference/fusion/patterns.rs:15-109 plus one new head):
  *   QuantizedLinear  MatMulInteger -> Cast -> Mul(scale or Mul(x_scale, w_scale)) [-> Add]
- *                    [-> Mul/Add/Sub/Div with static operands]*  => icx_qlinear_f32
- *   MulAdd / AddMul / SubMul / DivMul / ElementwiseChain — chains of binary elementwise ops
+ *                    [-> Mul/Add/Sub/Div with static operands]*
+ *                    [-> erf-GELU: Div, Erf, Add, Mul(x, .), Mul]      => icx_qlinear_f32
+ *   MulAdd / AddMul / SubMul / DivMul / ElementwiseChain / Gelu — chains of elementwise ops
  *                    with static operands (scalar, [last dim], same shape) => icx_fused_chain_f32
+ *   Attention        Reshape -> Transpose -> MatMul -> Div|Mul -> Softmax -> MatMul ->
+ *                    Transpose -> Reshape of a self-attention => icx_attention_f32, or the
+ *                    nodes one by one when the shapes fall outside that kernel
+ *   AddLayerNorm     LayerNormalization(Add(a, b)) => icx_layer_norm_f32 with a residual
  * Attribute values are int64 (axis, to); names of absent optional inputs are "". */
 typedef struct icx_graph icx_graph;
 
@@ -210,6 +217,11 @@ int icx_graph_add_initializer(icx_graph* g, const char* name, int dtype, int ran
 int icx_graph_add_node(icx_graph* g, const char* name, const char* op_type, int n_in,
                        const char* const* inputs, int n_out, const char* const* outputs,
                        int n_attr, const char* const* attr_names, const int64_t* attr_values);
+/* Non-integer attributes of an added node: a float (LayerNormalization epsilon) or a list
+ * of ints (Transpose perm). */
+int icx_graph_set_node_attr_float(icx_graph* g, const char* node, const char* attr, double value);
+int icx_graph_set_node_attr_ints(icx_graph* g, const char* node, const char* attr, int count,
+                                 const int64_t* values);
 int icx_graph_add_output(icx_graph* g, const char* name);
 /* Host passes only (topological sort, fusion decision, zero-point folding); no GPU work.
  * Writes a text summary into buf (may be NULL): one "<node> <op> <kind> <pattern> [k=v...]"

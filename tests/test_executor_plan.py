@@ -241,3 +241,77 @@ def test_configs_plan_to_one_fused_gemm_each():
         assert live[1].wzp_folded == (not per_channel_zp), cfg
         assert rowsums == (["%s.x_q" % cfg] if per_channel_zp else []), cfg
         assert live[1].steps == 2 + len(d["chain"]), cfg
+
+
+# ---- encoder patterns -------------------------------------------------------------------
+def test_encoder_layer_plan():
+    ex = GpuGraphExecutor()
+    out, names, _ = graphs.encoder_graph(ex, layers=2)
+    ex.add_output(out)
+    entries, rowsums = ex.plan()
+    live = [(e.op_type, e.pattern, e.steps) for e in entries if e.kind != "Skip"]
+    layer = [("DynamicQuantizeLinear", "-", 0)] + [("MatMulInteger", "QuantizedLinear", 2)] * 3 + [
+        ("Softmax", "Attention", 0), ("DynamicQuantizeLinear", "-", 0),
+        ("MatMulInteger", "QuantizedLinear", 2), ("LayerNormalization", "AddLayerNorm", 0),
+        ("DynamicQuantizeLinear", "-", 0), ("MatMulInteger", "QuantizedLinear", 8),
+        ("DynamicQuantizeLinear", "-", 0), ("MatMulInteger", "QuantizedLinear", 2),
+        ("LayerNormalization", "AddLayerNorm", 0)]
+    assert live == layer * 2
+    assert rowsums == []  # zero int8 weight zero points are folded
+    heads = {e.node: e for e in entries if e.kind == "FusedHead"}
+    assert heads["L0.ff1.mmi"].out == "L0.ff1.gelu.gelu"
+    assert heads["L1.attn.softmax"].out == "L1.attn.ctx"
+    skipped = {e.node for e in entries if e.kind == "Skip"}
+    for n in ("L0.attn.reshape_q", "L0.attn.transpose_k", "L0.attn.scale_q", "L0.attn.scores",
+              "L0.attn.context", "L0.attn.transpose_c", "L0.attn.reshape_c", "L0.ln1.residual",
+              "L0.ff1.gelu.erf", "L0.ff1.gelu.mulx"):
+        assert n in skipped, n
+
+
+def _gelu_graph(with_add):
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [4, 16])
+    src = "x"
+    if with_add:
+        ex.add_initializer("b", np.ones(16, np.float32))
+        ex.add_node("bias", "Add", ["x", "b"], ["xb"])
+        src = "xb"
+    y = graphs.add_gelu(ex, src, "g")
+    ex.add_output(y)
+    return ex, y
+
+
+@pytest.mark.parametrize("with_add,steps", [(False, 6), (True, 7)])
+def test_standalone_gelu_chain(with_add, steps):
+    ex, y = _gelu_graph(with_add)
+    entries, _ = ex.plan()
+    (h,) = heads(entries)
+    assert h.pattern == "Gelu" and h.steps == steps and h.out == y
+    assert sum(e.kind != "Skip" for e in entries) == 1
+
+
+def test_attention_needs_its_intermediates_private():
+    ex = GpuGraphExecutor()
+    for n in "qkv":
+        ex.add_input(n, [None, None, 128])
+    ctx = graphs.add_self_attention(ex, "q", "k", "v", 2, 64, "att")
+    ex.add_output(ctx)
+    assert [h.pattern for h in heads(ex.plan()[0])] == ["Attention"]
+    ex.add_output("att.s")  # the scores must materialise: no fusion
+    entries, _ = ex.plan()
+    assert not [h for h in heads(entries) if h.pattern == "Attention"]
+    assert [e.op_type for e in entries if e.kind != "Skip"].count("MatMul") == 2
+
+
+def test_layer_norm_without_add_is_regular_and_attrs_are_checked():
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [2, 8])
+    ex.add_initializer("g", np.ones(8, np.float32))
+    ex.add_initializer("b", np.zeros(8, np.float32))
+    ex.add_node("ln", "LayerNormalization", ["x", "g", "b"], ["y"], {"epsilon": 1e-6})
+    ex.add_output("y")
+    entries, _ = ex.plan()
+    assert [(e.op_type, e.kind) for e in entries] == [("LayerNormalization", "Regular")]
+    L = ex._L
+    assert L.icx_graph_set_node_attr_float(ex._g, b"missing", b"epsilon", 1.0) != 0
+    assert b"missing" in L.icx_last_error()
