@@ -355,8 +355,13 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// 128x128 tiles: three blocks per CU (12 waves, <= 168 registers each) so that a chip-full
+// of tiles (768 at the DistilBERT FFN shapes) runs in one round; the general per-element
+// epilogue keeps the default budget (it would spill).
 template <int BM, int BN, int WGM, int WGN, int NS, int OUT, int CH>
-__global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(64 * WGM * WGN)
+__attribute__((amdgpu_waves_per_eu(BM == 128 && CH != CH_GENERAL ? 3 : 1)))
+gemm_i8_dma_kernel(GemmArgs g) {
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
@@ -478,6 +483,289 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma_kernel(GemmArgs g)
     wait_vmcnt<0>();
     __syncthreads();  // all copies landed and all fragment reads done: LDS is free
     gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0);
+}
+
+// ---- main loop C: persistent producer / consumer (K % 64 == 0, column-only epilogue) ----
+// One block per CU slot loops over tiles (virtual tile ids blockIdx.x, +gridDim.x, ...,
+// mapped XCD-contiguous like tile_coords).  The K steps of all of a block's tiles form
+// one flat sequence of S = tiles x KT steps:
+//   * one producer wave (the last) issues every LDS DMA copy, NS-1 steps ahead, and is
+//     the only wave that waits on vmcnt;
+//   * the WGM x WGN consumer waves read fragments and run the MFMAs, and after a tile's
+//     last K step convert, correct, chain and store their accumulators straight from
+//     registers with non-temporal stores.  Consumers issue no loads the main loop waits
+//     for, so those stores drain while the next tile's MFMAs run.
+// The per-tile epilogue operands (column sums, per-column zero points, column factors,
+// row sums) are loaded by each consumer at the start of the tile and first used after
+// its last K step, by which time the previous tile's stores have long left.
+// Barrier protocol (every wave executes exactly S + 1 barriers, all at top level):
+//   barrier(-1): stage 0 has landed;
+//   barrier(s):  stage s+1 has landed, and every consumer is done reading stage s-1, so
+//                after it the producer refills stage s-1's buffer with step s+NS-1.
+// Steps past the end re-copy the last step into the free buffer so that every step
+// issues exactly P copies and the counted vmcnt waits stay exact.
+template <int BM, int BN, int WGM, int WGN>
+struct StreamLayout {
+    static constexpr int NC = WGM * WGN;          // consumer waves
+    static constexpr int WN = BN / WGN;
+    static constexpr int OPND_BYTES = NC * ICX_MAX_CHAIN * WN * 4;  // per-wave operand rows
+};
+
+__device__ __forceinline__ void stream_tile(const GemmArgs& g, int v, int T, int& tm, int& tn) {
+    int bid = v;
+    if ((T & 7) == 0 && (gridDim.x & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
+    const int per_group = GROUP_M * g.tiles_n;
+    const int group = bid / per_group;
+    const int first_m = group * GROUP_M;
+    const int gsz = min(g.tiles_m - first_m, GROUP_M);
+    const int in_group = bid - group * per_group;
+    tm = first_m + in_group % gsz;
+    tn = in_group / gsz;
+}
+
+template <int BM, int BN, int WGM, int WGN, int NP, int NS, int OUT, int CH>
+__global__ void __launch_bounds__(64 * (WGM * WGN + NP))
+gemm_i8_stream_kernel(GemmArgs g) {
+    using SL = StreamLayout<BM, BN, WGM, WGN>;
+    constexpr int NC = SL::NC;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TI = WM / 32, TJ = WN / 32;
+    constexpr int ROWB = 64;
+    constexpr int STAGE = (BM + BN) * ROWB;
+    constexpr int PA = BM / 16 / NP, PB = BN / 16 / NP, P = PA + PB;  // copies per producer per step
+    static_assert(PA * 16 * NP == BM && PB * 16 * NP == BN, "tile rows must split over the producers");
+    static_assert(NS >= 3, "the protocol reads stages s and s+1 while s+2.. are in flight");
+    static_assert(P * (NS - 2) <= 63, "outstanding copies must fit the 6-bit vmcnt");
+    constexpr int MODE = CH == CH_COL_EXT ? 2 : 0;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[NS * STAGE + SL::OPND_BYTES];
+
+    const int T = g.tiles_m * g.tiles_n;
+    const int G = gridDim.x;
+    const int ntiles = (T - (int)blockIdx.x + G - 1) / G;  // >= 1: the host launches G <= T
+    const int KT = g.K / ROWB;
+    const int S = ntiles * KT;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+
+    if (wid >= NC) {
+        // ------------------------------ producers -----------------------------------------
+        // Producer p copies rows [p*BM/NP, (p+1)*BM/NP) of the A tile and the same share of
+        // the B tile.  Row pointers are computed once per tile; a step only adds its K offset.
+        const int p = __builtin_amdgcn_readfirstlane(wid - NC);
+        const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr_of(smem));
+        const uint32_t ldsA = lds0 + p * PA * 16 * ROWB, ldsB = lds0 + BM * ROWB + p * PB * 16 * ROWB;
+        int rowA[PA], rowB[PB], kcA[PA], kcB[PB];
+#pragma unroll
+        for (int i = 0; i < PA; ++i) {
+            rowA[i] = (p * PA + i) * 16 + (lane >> 2);
+            kcA[i] = 16 * ((lane & 3) ^ ((rowA[i] >> 2) & 3));
+        }
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            rowB[i] = (p * PB + i) * 16 + (lane >> 2);
+            kcB[i] = 16 * ((lane & 3) ^ ((rowB[i] >> 2) & 3));
+        }
+        const int8_t* srcA[PA];
+        const int8_t* srcB[PB];
+        auto set_tile = [&](int ordinal) {
+            int tm, tn;
+            stream_tile(g, (int)blockIdx.x + ordinal * G, T, tm, tn);
+#pragma unroll
+            for (int i = 0; i < PA; ++i)
+                srcA[i] = g.A + (size_t)min(tm * BM + rowA[i], g.M - 1) * g.K + kcA[i];
+#pragma unroll
+            for (int i = 0; i < PB; ++i)
+                srcB[i] = g.Bp + (size_t)min(tn * BN + rowB[i], g.N - 1) * g.K + kcB[i];
+        };
+        // Issue state: the step being issued, as (tile ordinal, K step).
+        int it = 0, ik = 0, buf = 0;
+        set_tile(0);
+        auto issue_next = [&]() {
+            const uint32_t off = __builtin_amdgcn_readfirstlane(buf * STAGE);
+            const int k0 = ik * ROWB;
+#pragma unroll
+            for (int i = 0; i < PA; ++i)
+                dma16(srcA[i] + k0, __builtin_amdgcn_readfirstlane(ldsA + off + i * 16 * ROWB));
+#pragma unroll
+            for (int i = 0; i < PB; ++i)
+                dma16(srcB[i] + k0, __builtin_amdgcn_readfirstlane(ldsB + off + i * 16 * ROWB));
+            buf = buf + 1 == NS ? 0 : buf + 1;
+            // advance to the next step; past the last one keep re-copying it
+            if (it * KT + ik + 1 < S) {
+                if (++ik == KT) {
+                    ik = 0;
+                    set_tile(++it);
+                }
+            }
+        };
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s) issue_next();
+        wait_vmcnt<P * (NS - 2)>();  // stage 0
+        __syncthreads();               // barrier(-1)
+        for (int s = 0; s < S; ++s) {
+            wait_vmcnt<P * (NS - 3)>();  // stage s+1
+            __syncthreads();               // barrier(s)
+            issue_next();                  // step s+NS-1 into stage s-1's buffer
+        }
+        wait_vmcnt<0>();  // no copy may still target this block's LDS when it exits
+        return;
+    }
+
+    // -------------------------------- consumers --------------------------------------------
+    const int wm = wid / WGN, wn = wid % WGN;
+    const int lr = lane & 31;
+    float* opnd = reinterpret_cast<float*>(smem + NS * STAGE) + wid * ICX_MAX_CHAIN * WN;
+
+    // scalars, loaded before any store is issued
+    const int azp = load_zp(g.a_zp, g.a_zp_u8, 0);
+    const int bzp_scalar = (g.b_zp && g.b_zp_len == 1) ? load_zp(g.b_zp, g.b_zp_u8, 0) : 0;
+    const uint32_t amz = (uint32_t)(g.alpha - azp);
+    const uint32_t aK = (uint32_t)g.alpha * (uint32_t)g.K;
+
+    const uint32_t axr = g.a_xor;
+    v4i fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+    auto read_half = [&](int stage, int half, v4i (&fa)[TI], v4i (&fb)[TJ]) {
+        const int8_t* sa = smem + stage * STAGE;
+        const int8_t* sb = sa + BM * ROWB;
+        const int kc = half * 2 + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int row = wm * WM + i * 32 + lr;
+            fa[i] = *reinterpret_cast<const v4i*>(sa + row * ROWB + 16 * (kc ^ ((row >> 2) & 3)));
+        }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int row = wn * WN + j * 32 + lr;
+            fb[j] = *reinterpret_cast<const v4i*>(sb + row * ROWB + 16 * (kc ^ ((row >> 2) & 3)));
+        }
+    };
+    v16i acc[TI][TJ];
+    auto mfma_half = [&](const v4i (&fa)[TI], const v4i (&fb)[TJ]) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const v4i a = fa[i] ^ (int)axr;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, fb[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    __syncthreads();  // barrier(-1)
+    read_half(0, 0, fa0, fb0);
+    int cur = 0;  // stage buffer of step s
+    int s = 0;
+    for (int t = 0; t < ntiles; ++t) {
+        int tm, tn;
+        stream_tile(g, (int)blockIdx.x + t * G, T, tm, tn);
+        const int m0 = tm * BM + wm * WM, n0 = tn * BN + wn * WN;
+        // epilogue operands of this tile (first used after the last K step)
+        int cs[TJ], bz[TJ];
+        float ov[TJ][ICX_MAX_CHAIN];
+        int rs[TI];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int col = min(n0 + j * 32 + lr, g.N - 1);
+            cs[j] = g.colsum[col];
+            bz[j] = (g.b_zp && g.b_zp_len != 1) ? load_zp(g.b_zp, g.b_zp_u8, col) : bzp_scalar;
+            if (OUT == OUT_F32) {
+#pragma unroll
+                for (int k = 0; k < ICX_MAX_CHAIN; ++k) {
+                    float a = 0.0f;
+                    if (k < g.chain.n_ops && icx::op_takes_operand(g.chain.ops[k].op)) {
+                        const icx_chain_op& op = g.chain.ops[k];
+                        a = icx::col_factor(op.p0, op.kind0, col);
+                        if (op.p1) a = __fmul_rn(a, icx::col_factor(op.p1, op.kind1, col));
+                    }
+                    ov[j][k] = a;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+            rs[i] = g.rowsum_raw ? g.rowsum_raw[min(m0 + i * 32 + lr, g.M - 1)] : 0;
+        // keep those loads here, ahead of the main loop
+        asm volatile("" ::: "memory");
+
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+        for (int kt = 0; kt < KT; ++kt, ++s) {
+            const int nxt = cur + 1 == NS ? 0 : cur + 1;
+            read_half(cur, 1, fa1, fb1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_half(fa0, fb0);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();  // barrier(s)
+            if (s + 1 < S) read_half(nxt, 0, fa0, fb0);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_half(fa1, fb1);
+            __builtin_amdgcn_sched_barrier(0);
+            cur = nxt;
+        }
+
+        // ---- epilogue straight from the accumulators -------------------------------------
+        // lane = column (n0 + j*32 + lr); register r of tile (i, j) = row
+        // m0 + i*32 + 8*(r>>2) + 4*(lane>>5) + (r&3).
+        uint32_t colfac[TJ], colterm[TJ];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            colfac[j] = (uint32_t)(g.beta - bz[j]);
+            colterm[j] = amz * (uint32_t)cs[j] + (uint32_t)g.K * amz * colfac[j];
+            if (OUT == OUT_F32) {
+#pragma unroll
+                for (int k = 0; k < ICX_MAX_CHAIN; ++k)
+                    if (k < g.chain.n_ops) opnd[k * WN + j * 32 + lr] = ov[j][k];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int rbase = m0 + i * 32 + 4 * (lane >> 5);
+            uint32_t rt[16];  // row term of each register's row (row sums are held by lane = row)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                rt[r] = g.rowsum_raw
+                            ? (uint32_t)__shfl(rs[i], 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), 64) - aK
+                            : 0u;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const int col = n0 + j * 32 + lr;
+                float4 v[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float* w = reinterpret_cast<float*>(&v[q]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * q + e;
+                        const uint32_t x = (uint32_t)acc[i][j][r] + colterm[j] + colfac[j] * rt[r];
+                        if (OUT == OUT_I32) w[e] = __int_as_float((int32_t)x);
+                        else w[e] = (float)(int32_t)x;  // Cast INT32 -> FLOAT (RNE)
+                    }
+                }
+                if (OUT == OUT_F32) {
+                    icx::run_chain4<MODE>(g.codes, g.chain.n_ops, v, [&](int k) {
+                        const float o = opnd[k * WN + j * 32 + lr];
+                        return make_float4(o, o, o, o);
+                    });
+                }
+                if (col < g.N) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float* w = reinterpret_cast<const float*>(&v[q]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int row = rbase + 8 * q + e;
+                            if (row < g.M)
+                                __builtin_nontemporal_store(
+                                    w[e], reinterpret_cast<float*>(g.C) + (size_t)row * g.N + col);
+                        }
+                    }
+                }
+            }
+        }
+    }
 }
 
 // ---- weight packing -------------------------------------------------------------------
@@ -645,6 +933,52 @@ void launch_dma_big(int out_kind, unsigned blocks, hipStream_t s, const GemmArgs
         hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 256, WGM, WGN, NS, OUT_F32, CH_COL>), grid, block, 0, s, g);
 }
 
+// Persistent producer / consumer kernel: grid = min(tiles, resident blocks), resident
+// blocks from the occupancy calculator (cached per instantiation and device).
+int num_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <int BM, int BN, int WGM, int WGN, int NP, int NS, int OUT, int CH>
+int launch_stream_one(unsigned tiles, hipStream_t s, const GemmArgs& g) {
+    auto kern = gemm_i8_stream_kernel<BM, BN, WGM, WGN, NP, NS, OUT, CH>;
+    constexpr int threads = 64 * (WGM * WGN + NP);
+    static int per_cu[64] = {0};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const int d = (dev >= 0 && dev < 64) ? dev : 0;
+    if (!per_cu[d]) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), threads, 0) !=
+                hipSuccess || nb <= 0)
+            nb = 1;
+        per_cu[d] = nb;
+    }
+    unsigned grid = (unsigned)(per_cu[d] * num_cus());
+    if (grid > tiles) grid = tiles;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), 0, s, g);
+    return 0;
+}
+
+template <int BM, int BN, int WGM, int WGN, int NP, int NS>
+void launch_stream(int out_kind, int ch, unsigned tiles, hipStream_t s, const GemmArgs& g) {
+    if (out_kind == OUT_I32)
+        launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_I32, CH_GENERAL>(tiles, s, g);
+    else if (ch == CH_COL_EXT)
+        launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_F32, CH_COL_EXT>(tiles, s, g);
+    else
+        launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_F32, CH_COL>(tiles, s, g);
+}
+
 int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,
                 int b_packed, const int32_t* b_colsum, size_t M, size_t K, size_t N,
                 const void* a_zp, const void* b_zp, size_t b_zp_len, const int32_t* a_rowsum,
@@ -732,6 +1066,18 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     // otherwise 128x128 so that every CU gets tiles.  Row / full-tensor chain operands
     // take the general per-element path, kept on the 128x128 tile.
     const bool big = icx::cdiv(M, 256) * icx::cdiv(N, 256) >= 512 && (out_kind == OUT_I32 || ch == CH_COL);
+    // K-heavy shapes with fewer 128x128 tiles than CUs (the encoder's FFN-down projection):
+    // the persistent producer / consumer kernel, whose 8 MFMA waves per tile hide the long
+    // K loop better than 4.
+    const bool stream = dma && (out_kind == OUT_I32 || ch != CH_GENERAL) && K >= 2048 &&
+                        icx::cdiv(M, 128) * icx::cdiv(N, 128) < (size_t)num_cus();
+    if (stream) {
+        g.tiles_m = (int)icx::cdiv(M, 128);
+        g.tiles_n = (int)icx::cdiv(N, 128);
+        launch_stream<128, 128, 4, 2, 2, 4>(out_kind, ch, (unsigned)(g.tiles_m * g.tiles_n), s, g);
+        ICX_LAUNCH_CHECK("gemm_i8_stream_kernel");
+        return ICX_OK;
+    }
     if (big) {
         g.tiles_m = (int)icx::cdiv(M, 256);
         g.tiles_n = (int)icx::cdiv(N, 256);

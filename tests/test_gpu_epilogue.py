@@ -188,3 +188,51 @@ def test_dequantize_i32_large_values_follow_cpu_semantics():
     s = np.array(0.5, np.float32)
     got = ops.gpu_dequantize_linear(dev(x), dev(s), dev(zp)).cpu().numpy()
     np.testing.assert_array_equal(bits(got), bits(oracle.dequantize_linear(x, s, zp)))
+
+
+def test_persistent_kernel_fused_epilogue():
+    """FFN-down shape (K = 3072, 192 tiles < CUs: the persistent kernel) with the dequant
+    scale, bias and a Sub/Div/Mul chain with an operand on the left, bit-exact vs the oracle's
+    op-by-op graph; per-channel scale and zero point included."""
+    rng = np.random.default_rng(31)
+    M, K, N = 4096, 3072, 768
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    w_zp = rng.integers(-8, 9, N).astype(np.int8)
+    w_scale = rng.uniform(0.005, 0.03, N).astype(np.float32)
+    bias = (0.02 * rng.standard_normal(N)).astype(np.float32)
+    c = [rng.uniform(0.5, 2.0, N).astype(np.float32) for _ in range(3)]
+    chain = [("Sub", c[0], True), ("Div", c[1], False), ("Mul", c[2], False)]
+    xq, xs, xzp, rs = ops.gpu_dynamic_quantize_linear(dev(x), rowsum_row_len=K)
+    pw = ops.PackedWeight(dev(w))
+    epi = [("Mul", (xs, dev(w_scale)), False), ("Add", dev(bias), False)]
+    epi += [(op, dev(v), lhs) for op, v, lhs in chain]
+    y = ops.gpu_qlinear(xq, pw, xzp, dev(w_zp), epilogue=epi, a_rowsum=rs)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    for r0, r1 in [(0, 24), (2048, 2056), (M - 16, M)]:
+        ref = oracle.qlinear_graph(x, w, w_zp, w_scale, bias, chain, rows=(r0, r1))
+        assert_f32_equal(y[r0:r1], ref["y"][r0:r1], "rows %d:%d" % (r0, r1))
+
+
+def test_persistent_kernel_gelu_epilogue():
+    """The operand-free erf / save steps through the persistent kernel (K = 2048)."""
+    rng = np.random.default_rng(37)
+    M, K, N = 256, 2048, 384
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    w_scale, bias = np.float32(0.01), (0.02 * rng.standard_normal(N)).astype(np.float32)
+    xq, xs, xzp, rs = ops.gpu_dynamic_quantize_linear(dev(x), rowsum_row_len=K)
+    pw = ops.PackedWeight(dev(w))
+    c0, c1, c2 = (dev(np.array(v, np.float32)) for v in (1.4142135, 1.0, 0.5))
+    epi = [("Mul", (xs, dev(np.array(w_scale))), False), ("Add", dev(bias), False),
+           ("Save", None, False), ("Div", c0, False), ("Erf", None, False), ("Add", c1, False),
+           ("MulSaved", None, False), ("Mul", c2, False)]
+    y = ops.gpu_qlinear(xq, pw, xzp, None, epilogue=epi, a_rowsum=rs)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    t = oracle.qlinear_graph(x, w, np.array(0, np.int8), np.array(w_scale), bias)["linear"]
+    want = oracle.mul(oracle.mul(t, oracle.add(oracle.erf(oracle.div(t, np.float32(1.4142135))),
+                                               np.float32(1.0))), np.float32(0.5))
+    err = float(np.max(np.abs(y.astype(np.float64) - want)) / np.max(np.abs(want)))
+    assert err < 1e-6, err

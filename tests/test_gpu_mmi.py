@@ -148,3 +148,36 @@ def test_baseline_gemm_shapes(cfg):
     ra = (a.astype(np.int64) - int(azp)).sum(0)
     rhs = ra @ (b.astype(np.int64) - np.asarray(bzp, np.int64))
     np.testing.assert_array_equal(lhs, rhs)
+
+
+# Shapes with K >= 2048 and fewer 128x128 tiles than CUs take the persistent producer /
+# consumer kernel; the rest of this file covers the multi-block kernels.
+@pytest.mark.parametrize("adt,bdt", [(np.uint8, np.int8), (np.int8, np.uint8)])
+def test_persistent_kernel_shapes(adt, bdt):
+    rng = np.random.default_rng(23)
+    for M, K, N in [(512, 2048, 384), (300, 3072, 520), (64, 4096, 64), (129, 2112, 257)]:
+        a = rng.integers(np.iinfo(adt).min, np.iinfo(adt).max + 1, (M, K)).astype(adt)
+        b = rng.integers(np.iinfo(bdt).min, np.iinfo(bdt).max + 1, (K, N)).astype(bdt)
+        azp = np.array(rng.integers(np.iinfo(adt).min, np.iinfo(adt).max + 1), adt)
+        bzp = np.array(rng.integers(np.iinfo(bdt).min, np.iinfo(bdt).max + 1), bdt)
+        bzp_col = rng.integers(-8, 9, N).astype(bdt)
+        for zps in ((None, None), (azp, bzp), (azp, bzp_col)):
+            per_col = zps[1] is not None and np.asarray(zps[1]).ndim == 1
+            want = oracle.matmul_integer(a, b, *zps, per_column_b_zp=per_col)
+            assert np.array_equal(gpu_mmi(a, b, *zps, packed=True), want), (M, K, N, per_col)
+        rs = a.astype(np.int64).sum(1).astype(np.int32)
+        want = oracle.matmul_integer(a, b, azp, bzp_col, per_column_b_zp=True)
+        assert np.array_equal(gpu_mmi(a, b, azp, bzp_col, True, rowsum=rs), want)
+
+
+def test_persistent_kernel_encoder_ffn_down_shape():
+    """The DistilBERT FFN-down GEMM (4096 x 3072 x 768) at full size: every element against
+    the exact float64 product, rows against the oracle."""
+    rng = np.random.default_rng(29)
+    a = rng.integers(0, 256, (4096, 3072)).astype(np.uint8)
+    b = rng.integers(-127, 128, (3072, 768)).astype(np.int8)
+    azp, bzp = np.array(117, np.uint8), np.array(0, np.int8)
+    got = gpu_mmi(a, b, azp, bzp, packed=True)
+    np.testing.assert_array_equal(got.astype(np.int64), _exact_f64(a, b, azp, bzp))
+    for r in (0, 2049, 4095):
+        assert np.array_equal(got[r:r + 1], oracle.matmul_integer(a[r:r + 1], b, azp, bzp))
