@@ -136,7 +136,25 @@ __device__ __forceinline__ uint32_t quant1(float x, const DqlParams& p) {
     return (uint32_t)v;
 }
 
+// Four elements at once.  With `fast` (a scale in [1e-30, 1e30]) the f32 quotient q and
+// r = rne(q) decide every element with |q - r| < 0.4999 (the condition of quant1 written
+// without its tie-distance arithmetic: |q - r| <= 0.5 always).  Subnormal x need no
+// separate test here: |q| < 2e-8 then, so r = 0 = rne of the exact quotient.  NaN and inf
+// make q - r NaN, which fails the test and goes to quant1.
 __device__ __forceinline__ uint32_t quant4(float4 v, const DqlParams& p) {
+    if (p.fast) {
+        const float q0 = v.x * p.inv32, q1 = v.y * p.inv32, q2 = v.z * p.inv32, q3 = v.w * p.inv32;
+        const float r0 = rintf(q0), r1 = rintf(q1), r2 = rintf(q2), r3 = rintf(q3);
+        const bool ok = fabsf(q0 - r0) < 0.4999f && fabsf(q1 - r1) < 0.4999f &&
+                        fabsf(q2 - r2) < 0.4999f && fabsf(q3 - r3) < 0.4999f;
+        if (ok) {
+            const uint32_t a = (uint32_t)__builtin_amdgcn_fmed3f(r0 + (float)p.zp, 0.0f, 255.0f);
+            const uint32_t b = (uint32_t)__builtin_amdgcn_fmed3f(r1 + (float)p.zp, 0.0f, 255.0f);
+            const uint32_t c = (uint32_t)__builtin_amdgcn_fmed3f(r2 + (float)p.zp, 0.0f, 255.0f);
+            const uint32_t d = (uint32_t)__builtin_amdgcn_fmed3f(r3 + (float)p.zp, 0.0f, 255.0f);
+            return a | (b << 8) | (c << 16) | (d << 24);
+        }
+    }
     return quant1(v.x, p) | (quant1(v.y, p) << 8) | (quant1(v.z, p) << 16) |
            (quant1(v.w, p) << 24);
 }
@@ -207,11 +225,6 @@ __global__ void __launch_bounds__(kThreads)
 dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size_t tail, int vec,
                     uint8_t* __restrict__ y, const float2* __restrict__ part, int G,
                     float* __restrict__ y_scale, uint8_t* __restrict__ y_zp) {
-    const DqlParams p = fold_partials(part, G);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        *y_scale = (float)p.s;
-        *y_zp = (uint8_t)p.zp;
-    }
     const Slice sl = slice_of(units, unit, tail);
     const size_t t = threadIdx.x;
     size_t scalar_from = sl.e0;
@@ -220,6 +233,22 @@ dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size
         uint32_t* y4 = reinterpret_cast<uint32_t*>(y);
         const size_t b4 = sl.e0 / 4, end4 = b4 + (sl.e1 - sl.e0) / 4;
         size_t i = b4 + t;
+        // the lane's first four float4 are requested before the partials are folded, so
+        // the fold's loads and barriers overlap them
+        float4 v0[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (i + j * kThreads < end4) v0[j] = x4[i + j * kThreads];
+        const DqlParams p = fold_partials(part, G);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            *y_scale = (float)p.s;
+            *y_zp = (uint8_t)p.zp;
+        }
+        if (i + 3 * kThreads < end4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y4[i + j * kThreads] = quant4(v0[j], p);
+            i += 4 * kThreads;
+        }
         for (; i + 3 * kThreads < end4; i += 4 * kThreads) {
             const float4 a = x4[i], b = x4[i + kThreads], c = x4[i + 2 * kThreads],
                          d = x4[i + 3 * kThreads];
@@ -229,7 +258,13 @@ dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size
             y4[i + 3 * kThreads] = quant4(d, p);
         }
         for (; i < end4; i += kThreads) y4[i] = quant4(x4[i], p);
-        scalar_from = end4 * 4;
+        for (size_t j = end4 * 4 + t; j < sl.e1; j += kThreads) y[j] = (uint8_t)quant1(x[j], p);
+        return;
+    }
+    const DqlParams p = fold_partials(part, G);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *y_scale = (float)p.s;
+        *y_zp = (uint8_t)p.zp;
     }
     for (size_t j = scalar_from + t; j < sl.e1; j += kThreads) y[j] = (uint8_t)quant1(x[j], p);
 }
@@ -286,8 +321,11 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
     }
 }
 
+
 }  // namespace
 
+// The single-launch path: aligned operands, whole float4s, and a slice that fits kFRegs
+// float4 per lane (flat) or whole rows that do (row mode).
 extern "C" size_t icx_dql_workspace_size(size_t) { return sizeof(float2) * kMaxBlocks; }
 
 extern "C" int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, size_t n,

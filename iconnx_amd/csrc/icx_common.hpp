@@ -50,6 +50,10 @@ __device__ __forceinline__ void store_nt(float4* p, float4 v) {
     __builtin_nontemporal_store(w, reinterpret_cast<f4v*>(p));
 }
 
+__device__ __forceinline__ void store_nt_u32(uint32_t* p, uint32_t v) {
+    __builtin_nontemporal_store(v, p);
+}
+
 // int8 / uint8 operand description used by the GEMM entry points.
 inline bool is_int8_kind(int dt) { return dt == ICX_I8 || dt == ICX_U8; }
 
