@@ -6,8 +6,10 @@ A step is one pass of the hot path over one batch of synthetic, HBM-resident inp
 default workload is BASELINE configs[1] (cfg2): x [32,128,768] f32 ->
 DynamicQuantizeLinear -> MatMulInteger with W int8 [768,3072] -> Cast -> Mul(x_scale *
 w_scale) -> Add(bias) -> Mul/Add/Div/Mul chain, i.e. three kernel launches (DQL min/max,
-DQL quantize + row sums, fused GEMM).  Other configs (--config cfg1|cfg4|cfg5a|cfg5b) are
-for the per-kernel roofline figures.
+DQL quantize + row sums, fused GEMM).  The same run also reports the metric's second part,
+encoder seq/s (cfg3: the 6-layer DistilBERT-int8-shaped encoder at batch 32, seq 128, one
+captured forward replayed per step).  --config cfg3 makes that the primary line; the other
+configs (cfg1|cfg4|cfg5a|cfg5b) are for the per-kernel roofline figures.
 
 Timing: W untimed warmup steps, then exactly K steps, each a replay of a HIP graph that
 holds one step (so host launch overhead is not measured), bracketed by synchronize.  The
@@ -35,7 +37,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2",
-                    choices=["cfg1", "cfg2", "cfg4", "cfg5a", "cfg5b", "copy"],
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5a", "cfg5b", "copy"],
                     help="copy: the chain kernel with no ops over f32[65536,768] — a plain copy "
                          "of known size, the scale for the rocprofv3 FETCH_SIZE/WRITE_SIZE counters")
     ap.add_argument("--kernel-reps", type=int, default=100,
@@ -44,6 +46,8 @@ def parse():
                     help="rows of the CPU-baseline sample (default: config-specific)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
+    ap.add_argument("--no-encoder", action="store_true",
+                    help="cfg2: skip the secondary encoder seq/s measurement")
     return ap.parse_args()
 
 
@@ -180,6 +184,107 @@ class Runner:
         return b
 
 
+class EncoderRunner:
+    """cfg3: the DistilBERT-int8-shaped encoder (6 layers, hidden 768, 12 heads, FFN 3072)
+    through GpuGraphExecutor with random-init weights, input [32, 128, 768] ~ N(0, 1) on the
+    device; one forward is recorded once (icx_graph_capture) and a step is one replay."""
+
+    def __init__(self):
+        import torch
+
+        from iconnx_amd import graphs
+        from iconnx_amd.executor import GpuGraphExecutor
+
+        cfg = graphs.ENCODER
+        self.B, self.S = cfg["batch"], cfg["seq"]
+        self.ex = GpuGraphExecutor()
+        self.out, _, self.params = graphs.encoder_graph(self.ex, layers=cfg["layers"], heads=cfg["heads"])
+        self.x = torch.from_numpy(graphs.encoder_input(self.B, self.S)).cuda()
+        self.ex.capture({"x": self.x}, [self.out])
+        torch.cuda.synchronize()
+        # int8 work of one forward: 4 x (M x 768 x 768) + 2 x (M x 768 x 3072) per layer
+        M = self.B * self.S
+        self.int8_ops = cfg["layers"] * 2.0 * M * (4 * 768 * 768 + 2 * 768 * 3072)
+
+    def step(self):
+        self.ex.replay()
+
+
+class FfnUpGeluRunner:
+    """The encoder's largest kernel on its own: the FFN-up quantized linear (x [4096, 768]
+    -> [4096, 3072]) with the dequant, bias and erf-GELU in the GEMM store."""
+
+    def __init__(self, params):
+        import numpy as np
+        import torch
+
+        from iconnx_amd import graphs, ops
+        from iconnx_amd._lib import ICX_I8, ICX_U8, check, lib
+
+        self.L, self.check, self.torch = lib(), check, torch
+        p = params["ff1"]
+        x = graphs.encoder_input(32, 128).reshape(-1, 768)
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+        self.M, self.K, self.N = 4096, 768, 3072
+        self.xq, xs, self.xzp = ops.gpu_dynamic_quantize_linear(dev(x))
+        self.w = ops.PackedWeight(dev(p["w"]))
+        c = [dev(np.array(v, np.float32)) for v in (1.4142135381698608, 1.0, 0.5)]
+        epi = [("Mul", (xs, dev(p["w_scale"])), False), ("Add", dev(p["bias"]), False),
+               ("Save", None, False), ("Div", c[0], False), ("Erf", None, False),
+               ("Add", c[1], False), ("MulSaved", None, False), ("Mul", c[2], False)]
+        self.chain, self.keep = ops.build_chain(epi, self.M, self.N)
+        self.y = torch.empty((self.M, self.N), dtype=torch.float32, device="cuda")
+        self.ws = torch.empty(max(1, self.L.icx_matmul_integer_workspace_size(self.M, self.K, self.N, 1)),
+                              dtype=torch.uint8, device="cuda")
+        self.a_dtype, self.b_dtype = ICX_U8, ICX_I8
+        torch.cuda.synchronize()
+
+    def launch(self, stream):
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        self.check(self.L.icx_qlinear_f32(
+            stream, p(self.xq), self.a_dtype, p(self.w.packed), self.b_dtype, 1, p(self.w.colsum),
+            self.M, self.K, self.N, p(self.xzp), None, 1, None, ctypes.byref(self.chain), p(self.y),
+            p(self.ws), self.ws.numel()))
+
+    def algorithmic_bytes(self):
+        return self.M * self.K + self.K * self.N + 4.0 * self.M * self.N + 4.0 * self.N * 2
+
+
+def time_replays(step, steps, warmup, torch):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, time.perf_counter() - t0
+
+
+def encoder_cpu_baseline():
+    """The oracle (single-threaded C restatement of the reference CPU ops, composed op by op)
+    running the same 6-layer encoder on one sequence [1, 128, 768] — a bounded sample of the
+    batch-32 workload (per-tensor quantization then spans that sequence only)."""
+    import numpy as npx
+
+    from iconnx_amd import graphs
+    from oracle.encoder import layer_ref
+
+    cfg = graphs.ENCODER
+    x = graphs.encoder_input(1, cfg["seq"])
+    params = [graphs.encoder_layer_params(l) for l in range(cfg["layers"])]
+    t0 = time.perf_counter()
+    for l in range(cfg["layers"]):
+        x = layer_ref(x, params[l], cfg["heads"], cfg["eps"])["out"]
+    dt = time.perf_counter() - t0
+    assert npx.all(npx.isfinite(x))
+    return {"value": round(1.0 / dt, 4), "unit": "seq/s", "cores": 1, "kind": "port",
+            "sample": "one sequence [1,128,768] through the 6 layers op by op (%.1f s measured)" % dt}
+
+
 def measured_traffic(cfg):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE, scaled by the plain-copy calibration), or None."""
@@ -298,6 +403,8 @@ def main():
     import torch
 
     torch.cuda.set_device(0)
+    if args.config == "cfg3":
+        return main_encoder(args, torch)
     r = Runner(args.config)
     sync = torch.cuda.synchronize
 
@@ -399,10 +506,60 @@ def main():
     }
     if args.config in ("cfg5b", "copy"):
         out["dtype"] = "f32"
+    if args.config == "cfg2" and not args.no_encoder:
+        # the metric's second part, encoder seq/s, measured in the same run
+        enc = EncoderRunner()
+        ms_e, _ = time_replays(enc.step, 50, 5, torch)
+        out["encoder"] = {"metric": "encoder seq/s", "value": round(enc.B / (ms_e * 1e-3), 1),
+                          "unit": "seq/s", "ms_per_forward": round(ms_e, 4),
+                          "int8_TOPS": round(enc.int8_ops / (ms_e * 1e-3) / 1e12, 2),
+                          "workload": ENCODER_WORKLOAD, "graph_replay": True}
     if not args.no_cpu_baseline and args.config != "copy":
         cb = cpu_baseline(args.config, args.cpu_rows)
         cb["cores"] = 1
         out["cpu_baseline"] = cb
+    print(json.dumps(out), flush=True)
+
+
+ENCODER_WORKLOAD = ("cfg3: 6-layer DistilBERT-int8-shaped encoder, hidden 768, 12 heads, FFN 3072, "
+                    "batch 32, seq 128; every linear DQL + MatMulInteger + dequant Mul + bias Add, "
+                    "LayerNorm / Softmax / erf-GELU in fp32")
+
+
+def main_encoder(args, torch):
+    enc = EncoderRunner()
+    ms_step, wall = time_replays(enc.step, args.steps, args.warmup, torch)
+    seq_s = enc.B / (ms_step * 1e-3)
+    # dominant kernel: the FFN-up GEMM with its erf-GELU epilogue, R launches in one graph
+    ffn = FfnUpGeluRunner(enc.params[0])
+    g = graph_of(ffn.launch, args.kernel_reps, torch)
+    g.replay()
+    torch.cuda.synchronize()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record()
+    g.replay()
+    k1.record()
+    torch.cuda.synchronize()
+    k_us = k0.elapsed_time(k1) * 1e3 / args.kernel_reps
+    alg = ffn.algorithmic_bytes()
+    ach = alg / (k_us * 1e-6) / 1e9
+    out = {
+        "metric": METRIC, "value": round(seq_s, 2), "unit": "seq/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: input embeddings ~ N(0,1) (SplitMix64 + Box-Muller), random-init int8 "
+                "weights (per-tensor scale), N(0,0.02) biases",
+        "config": {"workload": ENCODER_WORKLOAD, "batch": enc.B, "seq": enc.S, "layers": 6},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "gemm_i8_dma_kernel (FFN-up 4096x768x3072, erf-GELU epilogue)",
+                     "kernel_avg_us": round(k_us, 3), "algorithmic_bytes": alg,
+                     "kernel_int8_TOPS": round(2.0 * ffn.M * ffn.N * ffn.K / (k_us * 1e-6) / 1e12, 2)},
+        "timing": {"graph_replay": True, "wall_s": round(wall, 4),
+                   "encoder_int8_TOPS": round(enc.int8_ops / (ms_step * 1e-3) / 1e12, 2)},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = encoder_cpu_baseline()
     print(json.dumps(out), flush=True)
 
 

@@ -74,6 +74,8 @@ SIGNATURES = {
     "icx_graph_run": ([P, P], I),
     "icx_graph_get_output": ([P, C, ctypes.POINTER(I), ctypes.POINTER(I), P, ctypes.POINTER(P)], I),
     "icx_graph_pool_stats": ([P, P, P, P], I),
+    "icx_graph_capture": ([P, P], I),
+    "icx_graph_replay": ([P, P], I),
 }
 
 

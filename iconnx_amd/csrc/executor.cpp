@@ -252,11 +252,24 @@ struct icx_graph {
     Pool pool;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // a captured run (icx_graph_capture): the HIP graph, its executable form and the output
+    // tensors it writes
+    hipGraph_t hip_graph = nullptr;
+    hipGraphExec_t hip_exec = nullptr;
+    std::map<std::string, DevTensor> captured_values;
 
     ~icx_graph() {
         if (ran && last_stream) (void)hipStreamSynchronize(last_stream);
+        drop_capture();
         clear_run();
         free_weights();
+    }
+    void drop_capture() {
+        if (hip_exec) (void)hipGraphExecDestroy(hip_exec);
+        if (hip_graph) (void)hipGraphDestroy(hip_graph);
+        hip_exec = nullptr;
+        hip_graph = nullptr;
+        captured_values.clear();
     }
     void free_weights() {
         for (auto& kv : weights) (void)hipFree(kv.second.ptr);
@@ -276,7 +289,10 @@ struct icx_graph {
         values.clear();
         rowsum_of.clear();
     }
-    void invalidate() { planned = compiled = false; }
+    void invalidate() {
+        planned = compiled = false;
+        drop_capture();
+    }
     Node* find_node(const std::string& name) {
         for (auto& n : nodes)
             if (n.name == name) return &n;
@@ -1756,6 +1772,12 @@ extern "C" int icx_graph_set_input(icx_graph* g, const char* name, int dtype, in
         if (d < 0) ICX_FAIL(ICX_ERR_SHAPE, "set_input: '%s' has a negative dimension", name);
     const size_t bytes = (size_t)numel(b.shape) * dtype_size(dtype);
     if (bytes && !data) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_input: '%s' has no data", name);
+    if (g->hip_exec) {  // a captured run reads the bound device pointers in place
+        auto old = g->bound.find(name);
+        if (!on_device || old == g->bound.end() || old->second.dev != data || old->second.shape != b.shape ||
+            old->second.dtype != dtype)
+            g->drop_capture();
+    }
     if (on_device) {
         b.dev = data;
     } else if (bytes) {
@@ -1805,6 +1827,78 @@ static int icx_graph_run_impl(icx_graph* g, icx_stream_t stream) {
         }
         r.release_dead(i);
     }
+    return ICX_OK;
+}
+
+// Capture: a warm-up run sizes the pool and the workspace, so that a second run reaches no
+// hipMalloc, synchronisation or memset; that run is recorded into a HIP graph (nothing
+// executes while recording) and instantiated.  Replay launches it; the outputs are then in
+// the buffers the recording run assigned, which the replay restores as the graph's values.
+static int icx_graph_capture_impl(icx_graph* g, icx_stream_t stream) {
+    if (!g) ICX_FAIL(ICX_ERR_INVALID_ARG, "capture: null graph");
+    for (auto& b : g->bound)
+        if (!b.second.dev)
+            ICX_FAIL(ICX_ERR_INVALID_ARG,
+                     "capture: input '%s' is bound from host memory; a captured run reads its "
+                     "inputs in place, so bind them on the device", b.first.c_str());
+    if (!stream) ICX_FAIL(ICX_ERR_INVALID_ARG, "capture: the legacy default stream cannot be captured; pass a created stream");
+    g->drop_capture();
+    int rc = icx_graph_run_impl(g, stream);  // warm-up (executes)
+    if (rc) return rc;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    ICX_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
+    rc = icx_graph_run_impl(g, stream);  // recorded
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(s, &graph);
+    if (rc) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    if (e != hipSuccess || !graph)
+        ICX_FAIL(ICX_ERR_HIP, "capture: hipStreamEndCapture: %s", hipGetErrorString(e));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        ICX_FAIL(ICX_ERR_HIP, "capture: hipGraphInstantiate: %s", hipGetErrorString(ie));
+    }
+    g->hip_graph = graph;
+    g->hip_exec = exec;
+    g->captured_values = g->values;
+    return ICX_OK;
+}
+
+extern "C" int icx_graph_capture(icx_graph* g, icx_stream_t stream) {
+    icx::clear_error();
+    try {
+        return icx_graph_capture_impl(g, stream);
+    } catch (const std::exception& e) {
+        set_error("icx_graph_capture: %s", e.what());
+        return ICX_ERR_INVALID_ARG;
+    }
+}
+
+extern "C" int icx_graph_replay(icx_graph* g, icx_stream_t stream) {
+    icx::clear_error();
+    if (!g) ICX_FAIL(ICX_ERR_INVALID_ARG, "replay: null graph");
+    if (!g->hip_exec) ICX_FAIL(ICX_ERR_INVALID_ARG, "replay: nothing captured (call icx_graph_capture)");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (g->ran && g->last_stream && g->last_stream != s) ICX_HIP_CHECK(hipStreamSynchronize(g->last_stream));
+    if (g->values.size() != g->captured_values.size() ||
+        !std::equal(g->values.begin(), g->values.end(), g->captured_values.begin(),
+                    [](const auto& a, const auto& b) { return a.first == b.first && a.second.ptr == b.second.ptr; })) {
+        // an eager run since the capture moved the outputs: return its buffers to the pool
+        // and restore the captured ones (they are the pool's free buffers the graph writes)
+        g->clear_run();
+        for (auto& kv : g->captured_values) {
+            DevTensor t = kv.second;
+            t.pooled = false;  // owned by the pool's free list, written by the graph
+            g->values[kv.first] = t;
+        }
+    }
+    ICX_HIP_CHECK(hipGraphLaunch(g->hip_exec, s));
+    g->last_stream = s;
+    g->ran = true;
     return ICX_OK;
 }
 

@@ -226,6 +226,58 @@ class GpuGraphExecutor:
         dev = self.run_device(inputs, output_names)
         return {k: v.cpu().numpy() for k, v in dev.items()}
 
+    def capture(self, inputs, output_names):
+        """Record one run into a HIP graph on ``torch.cuda.current_stream()``.  ``inputs``
+        must be device tensors: the graph reads them in place, so a caller writes new data
+        into the same tensors before :meth:`replay`.  A warm-up run executes first; the
+        recorded run does not."""
+        torch = _torch()
+        for n, t in inputs.items():
+            if not (isinstance(t, torch.Tensor) and t.is_cuda and t.is_contiguous()):
+                raise IconnxError(1, "capture: input '%s' must be a contiguous device tensor" % n)
+        for n in output_names:
+            self.add_output(n)
+        self._bind(inputs)
+        # recorded on a stream of the executor's own (the legacy default stream cannot be
+        # captured), ordered after and before the caller's stream
+        if getattr(self, "_stream", None) is None:
+            self._stream = torch.cuda.Stream()
+        cur = torch.cuda.current_stream()
+        self._stream.wait_stream(cur)
+        check(self._L.icx_graph_capture(self._g, ctypes.c_void_p(self._stream.cuda_stream)))
+        cur.wait_stream(self._stream)
+
+    def replay(self):
+        """Launch the recorded run, ordered after the current stream's work and before its
+        later work (asynchronous)."""
+        torch = _torch()
+        if getattr(self, "_stream", None) is None:
+            raise IconnxError(1, "replay: nothing captured (call capture first)")
+        cur = torch.cuda.current_stream()
+        self._stream.wait_stream(cur)
+        check(self._L.icx_graph_replay(self._g, ctypes.c_void_p(self._stream.cuda_stream)))
+        cur.wait_stream(self._stream)
+
+    def outputs(self, output_names):
+        """{name: device tensor}: copies of the outputs of the last run or replay (ordered
+        after it on the current stream)."""
+        torch = _torch()
+        out = {}
+        for n in output_names:
+            dt, rank = ctypes.c_int(), ctypes.c_int()
+            dims = (ctypes.c_int64 * 8)()
+            ptr = ctypes.c_void_p()
+            check(self._L.icx_graph_get_output(self._g, n.encode(), ctypes.byref(dt),
+                                               ctypes.byref(rank), dims, ctypes.byref(ptr)))
+            shape = [dims[i] for i in range(rank.value)]
+            t = torch.empty(shape, dtype=_torch_dt(dt.value), device="cuda")
+            nbytes = t.numel() * t.element_size()
+            if nbytes:
+                _hip_memcpy_d2d(ctypes.c_void_p(t.data_ptr()), ptr, nbytes,
+                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            out[n] = t
+        return out
+
     def pool_stats(self):
         """(hipMalloc calls, pool hits, bytes held by the pool)."""
         a, b, c = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()

@@ -240,6 +240,18 @@ int icx_graph_get_output(icx_graph* g, const char* name, int* dtype, int* rank, 
                          const void** device_ptr);
 /* Memory pool statistics: allocations from hipMalloc, pool hits, bytes held. */
 int icx_graph_pool_stats(icx_graph* g, int64_t* hipmallocs, int64_t* hits, int64_t* bytes_held);
+/* Record one run into a HIP graph for repeated inference (no counterpart in the reference,
+ * whose GpuGraphExecutor::run, src/cuda/inference/mod.rs:428, launches every kernel from
+ * the host on each call).  Every input must be bound
+ * on the device (icx_graph_set_input with on_device = 1): the graph reads those pointers in
+ * place, so new data is written into the same buffers before a replay.  A warm-up run
+ * executes first (sizing the pool and the workspace); the recorded run does not execute.
+ * Changing a bound device pointer, shape or dtype, or adding to the graph, drops the
+ * recording.  `stream` must be a created stream (the legacy default stream cannot be
+ * captured).  Replays and runs of one graph must be ordered on one stream. */
+int icx_graph_capture(icx_graph* g, icx_stream_t stream);
+/* Launch the recorded run on `stream`; outputs as after icx_graph_run. */
+int icx_graph_replay(icx_graph* g, icx_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -162,3 +162,40 @@ def test_shared_dql_three_projections_per_channel():
         w, zp, sc, b = params[p]
         ref = oracle.qlinear_graph(x, w, zp, sc, b)
         assert_bits_equal(got[o].reshape(-1, 96), ref["y"], p)
+
+
+def test_capture_and_replay_match_eager_runs():
+    """A recorded run replayed several times, with eager work and synchronisations between
+    the replays and new data written into the bound input in between, matches eager runs
+    bit for bit; a host-bound input is refused."""
+    from iconnx_amd import graphs
+
+    ex = GpuGraphExecutor()
+    out, _, _ = graphs.encoder_graph(ex, layers=2, seed=4100)
+    xs = [torch.from_numpy(graphs.encoder_input(2, 16, seed=s)).cuda() for s in (1, 2, 3)]
+    want = [ex.run({"x": x}, [out])[out] for x in xs]
+    xin = xs[0].clone()
+    ex.capture({"x": xin}, [out])
+    for rep in range(6):
+        i = rep % 3
+        xin.copy_(xs[i])
+        ex.replay()
+        got = ex.outputs([out])[out].cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want[i].view(np.uint32)), "replay %d" % rep
+        # eager work on the same stream between replays
+        _ = (xs[i] * 2.0).sum().item()
+        torch.cuda.synchronize()
+    # an eager run after the capture (same bound tensor), then replays again
+    assert np.array_equal(ex.run({"x": xin}, [out])[out].view(np.uint32), want[2].view(np.uint32))
+    xin.copy_(xs[1])
+    ex.replay()
+    assert np.array_equal(ex.outputs([out])[out].cpu().numpy().view(np.uint32), want[1].view(np.uint32))
+    # rebinding another tensor drops the recording; a new capture reads the new tensor
+    other = xs[0].clone()
+    ex.capture({"x": other}, [out])
+    ex.replay()
+    assert np.array_equal(ex.outputs([out])[out].cpu().numpy().view(np.uint32), want[0].view(np.uint32))
+    ex2 = GpuGraphExecutor()
+    out2, _, _ = graphs.encoder_graph(ex2, layers=1, seed=4100)
+    with pytest.raises(IconnxError):
+        ex2.capture({"x": graphs.encoder_input(2, 16, seed=1)}, [out2])
