@@ -76,6 +76,48 @@ layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ res, si
     }
 }
 
+// The same arithmetic, in the same order, with each lane's PER = cols / 8 elements held in
+// registers: all of a lane's loads are issued at once (one memory latency per row instead
+// of one per dependent step), x + residual is formed once, and the three passes run from
+// registers.  One wave (8 rows) per block spreads the rows over every CU.
+template <int PER>
+__global__ void __launch_bounds__(64)
+layer_norm_reg_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t rows,
+                      const float* __restrict__ scale, const float* __restrict__ bias, float eps,
+                      float* __restrict__ y) {
+    constexpr int cols = 8 * PER;
+    const int j = threadIdx.x & 7;
+    const size_t row = (size_t)blockIdx.x * 8 + (threadIdx.x >> 3);
+    if (row >= rows) return;  // a whole 8-lane group leaves together
+    const float* xr = x + row * cols + j;
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) v[k] = xr[8 * k];
+    if (res) {
+        const float* rr = res + row * cols + j;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k] = __fadd_rn(v[k], rr[8 * k]);
+    }
+    float p = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) p = __fadd_rn(p, v[k]);
+    const float mean = __fdiv_rn(combine8(p), (float)cols);
+    p = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const float c = __fsub_rn(v[k], mean);
+        p = __fadd_rn(p, __fmul_rn(c, c));
+    }
+    const float var = __fdiv_rn(combine8(p), (float)cols);
+    const float sd = sqrtf(__fadd_rn(var, eps));
+    float* yr = y + row * cols + j;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const float c = __fsub_rn(v[k], mean);
+        yr[8 * k] = __fadd_rn(__fmul_rn(__fdiv_rn(c, sd), scale[j + 8 * k]), bias[j + 8 * k]);
+    }
+}
+
 __global__ void __launch_bounds__(kThreads)
 softmax_kernel(const float* __restrict__ x, size_t rows, size_t cols, float* __restrict__ y) {
     const int lane = threadIdx.x & 63, j = lane & 7;
@@ -334,9 +376,16 @@ extern "C" int icx_layer_norm_f32(icx_stream_t stream, const float* x, const flo
     if (!x || !scale || !bias || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "LayerNormalization: null pointer argument");
     if (cols == 0 && rows) ICX_FAIL(ICX_ERR_SHAPE, "LayerNormalization: empty normalized axis");
     if (rows == 0) return ICX_OK;
-    hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)icx::cdiv(rows, 32)), dim3(kThreads), 0,
-                       reinterpret_cast<hipStream_t>(stream), x, residual, rows, cols, scale, bias,
-                       eps, y);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const dim3 g8((unsigned)icx::cdiv(rows, 8));
+    switch (cols) {  // the hidden sizes of the BERT family: row in registers
+        case 512: hipLaunchKernelGGL(layer_norm_reg_kernel<64>, g8, dim3(64), 0, s, x, residual, rows, scale, bias, eps, y); break;
+        case 768: hipLaunchKernelGGL(layer_norm_reg_kernel<96>, g8, dim3(64), 0, s, x, residual, rows, scale, bias, eps, y); break;
+        case 1024: hipLaunchKernelGGL(layer_norm_reg_kernel<128>, g8, dim3(64), 0, s, x, residual, rows, scale, bias, eps, y); break;
+        default:
+            hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)icx::cdiv(rows, 32)), dim3(kThreads), 0, s, x,
+                               residual, rows, cols, scale, bias, eps, y);
+    }
     ICX_LAUNCH_CHECK("layer_norm_kernel");
     return ICX_OK;
 }
