@@ -76,45 +76,99 @@ layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ res, si
     }
 }
 
-// The same arithmetic, in the same order, with each lane's PER = cols / 8 elements held in
-// registers: all of a lane's loads are issued at once (one memory latency per row instead
-// of one per dependent step), x + residual is formed once, and the three passes run from
-// registers.  One wave (8 rows) per block spreads the rows over every CU.
+// The same arithmetic, in the same order, for the BERT hidden sizes (cols = 8 * PER): a
+// block of four waves normalises 8 consecutive rows.  All four stage the rows (x +
+// residual, formed once) into LDS with float4 loads; wave 0 then runs the order-fixed
+// reductions — lane (r, j) walks its strided partial x[j], x[j+8], ... of row r from LDS
+// into registers — and leaves each row's mean and standard deviation in LDS; the output
+// pass, independent per element, is spread over all 256 lanes with coalesced stores.  A
+// staged row is cols + 8 floats long, so the strided reads of the 8 rows fall into
+// distinct banks.
 template <int PER>
-__global__ void __launch_bounds__(64)
-layer_norm_reg_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t rows,
-                      const float* __restrict__ scale, const float* __restrict__ bias, float eps,
-                      float* __restrict__ y) {
-    constexpr int cols = 8 * PER;
-    const int j = threadIdx.x & 7;
-    const size_t row = (size_t)blockIdx.x * 8 + (threadIdx.x >> 3);
-    if (row >= rows) return;  // a whole 8-lane group leaves together
-    const float* xr = x + row * cols + j;
-    float v[PER];
+__global__ void __launch_bounds__(256)
+layer_norm_rows8_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t rows,
+                        const float* __restrict__ scale, const float* __restrict__ bias, float eps,
+                        float* __restrict__ y) {
+    constexpr int cols = 8 * PER, C4 = cols / 4, STRIDE = cols + 8;
+    constexpr int PL = 8 * C4 / 256;  // float4 per lane for 8 rows
+    static_assert(PL * 256 == 8 * C4, "8 rows split evenly over the block");
+    __shared__ __attribute__((aligned(16))) float tile[8 * STRIDE];
+    __shared__ float stat[2][8];  // mean, sd per row
+    const int t = threadIdx.x;
+    const size_t row0 = (size_t)blockIdx.x * 8;
+    const int nr = (int)(rows - row0 < 8 ? rows - row0 : 8);
+    const float4* x4 = reinterpret_cast<const float4*>(x + row0 * cols);
+    const float4* r4 = res ? reinterpret_cast<const float4*>(res + row0 * cols) : nullptr;
+    {
+        float4 v[PL], w[PL];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) v[k] = xr[8 * k];
-    if (res) {
-        const float* rr = res + row * cols + j;
+        for (int u = 0; u < PL; ++u) {
+            const int q = t + u * 256;
+            if (q < nr * C4) v[u] = x4[q];
+        }
+        if (r4) {
 #pragma unroll
-        for (int k = 0; k < PER; ++k) v[k] = __fadd_rn(v[k], rr[8 * k]);
+            for (int u = 0; u < PL; ++u) {
+                const int q = t + u * 256;
+                if (q < nr * C4) w[u] = r4[q];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < PL; ++u) {
+            const int q = t + u * 256;
+            if (q < nr * C4) {
+                float4 a = v[u];
+                if (r4)
+                    a = make_float4(__fadd_rn(a.x, w[u].x), __fadd_rn(a.y, w[u].y), __fadd_rn(a.z, w[u].z),
+                                    __fadd_rn(a.w, w[u].w));
+                *reinterpret_cast<float4*>(&tile[(q / C4) * STRIDE + (q % C4) * 4]) = a;
+            }
+        }
     }
-    float p = 0.0f;
+    __syncthreads();
+    if (t < 64) {
+        const int r = t >> 3, j = t & 7;
+        if (r < nr) {  // whole 8-lane groups
+            const float* tr = tile + r * STRIDE + j;
+            float v[PER];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) p = __fadd_rn(p, v[k]);
-    const float mean = __fdiv_rn(combine8(p), (float)cols);
-    p = 0.0f;
+            for (int k = 0; k < PER; ++k) v[k] = tr[8 * k];
+            float p = 0.0f;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const float c = __fsub_rn(v[k], mean);
-        p = __fadd_rn(p, __fmul_rn(c, c));
+            for (int k = 0; k < PER; ++k) p = __fadd_rn(p, v[k]);
+            const float mean = __fdiv_rn(combine8(p), (float)cols);
+            p = 0.0f;
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const float c = __fsub_rn(v[k], mean);
+                p = __fadd_rn(p, __fmul_rn(c, c));
+            }
+            const float var = __fdiv_rn(combine8(p), (float)cols);
+            if (j == 0) {
+                stat[0][r] = mean;
+                stat[1][r] = sqrtf(__fadd_rn(var, eps));
+            }
+        }
     }
-    const float var = __fdiv_rn(combine8(p), (float)cols);
-    const float sd = sqrtf(__fadd_rn(var, eps));
-    float* yr = y + row * cols + j;
+    __syncthreads();
+    float4* y4 = reinterpret_cast<float4*>(y + row0 * cols);
+    const float4* s4 = reinterpret_cast<const float4*>(scale);
+    const float4* b4 = reinterpret_cast<const float4*>(bias);
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const float c = __fsub_rn(v[k], mean);
-        yr[8 * k] = __fadd_rn(__fmul_rn(__fdiv_rn(c, sd), scale[j + 8 * k]), bias[j + 8 * k]);
+    for (int u = 0; u < PL; ++u) {
+        const int q = t + u * 256;
+        if (q < nr * C4) {
+            const int r = q / C4, c4 = q % C4;
+            const float mean = stat[0][r], sd = stat[1][r];
+            const float4 a = *reinterpret_cast<const float4*>(&tile[r * STRIDE + c4 * 4]);
+            const float4 sc = s4[c4], bi = b4[c4];
+            float4 o;
+            o.x = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(a.x, mean), sd), sc.x), bi.x);
+            o.y = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(a.y, mean), sd), sc.y), bi.y);
+            o.z = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(a.z, mean), sd), sc.z), bi.z);
+            o.w = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(a.w, mean), sd), sc.w), bi.w);
+            icx::store_nt(&y4[q], o);
+        }
     }
 }
 
@@ -378,10 +432,13 @@ extern "C" int icx_layer_norm_f32(icx_stream_t stream, const float* x, const flo
     if (rows == 0) return ICX_OK;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const dim3 g8((unsigned)icx::cdiv(rows, 8));
-    switch (cols) {  // the hidden sizes of the BERT family: row in registers
-        case 512: hipLaunchKernelGGL(layer_norm_reg_kernel<64>, g8, dim3(64), 0, s, x, residual, rows, scale, bias, eps, y); break;
-        case 768: hipLaunchKernelGGL(layer_norm_reg_kernel<96>, g8, dim3(64), 0, s, x, residual, rows, scale, bias, eps, y); break;
-        case 1024: hipLaunchKernelGGL(layer_norm_reg_kernel<128>, g8, dim3(64), 0, s, x, residual, rows, scale, bias, eps, y); break;
+    // the hidden sizes of the BERT family, float4-aligned: rows staged through LDS
+    const bool a16 = icx::aligned16(x) && icx::aligned16(y) && icx::aligned16(scale) &&
+                     icx::aligned16(bias) && (!residual || icx::aligned16(residual));
+    switch (a16 ? cols : 0) {
+        case 512: hipLaunchKernelGGL(layer_norm_rows8_kernel<64>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y); break;
+        case 768: hipLaunchKernelGGL(layer_norm_rows8_kernel<96>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y); break;
+        case 1024: hipLaunchKernelGGL(layer_norm_rows8_kernel<128>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y); break;
         default:
             hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)icx::cdiv(rows, 32)), dim3(kThreads), 0, s, x,
                                residual, rows, cols, scale, bias, eps, y);
