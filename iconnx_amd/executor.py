@@ -115,7 +115,8 @@ class GpuGraphExecutor:
         code = _INIT_DT.get(arr.dtype)
         if code is None:
             return
-        arr = np.ascontiguousarray(arr)
+        if not arr.flags.c_contiguous:  # (np.ascontiguousarray would make a 0-d array 1-d)
+            arr = arr.copy(order="C")
         check(self._L.icx_graph_add_initializer(
             self._g, name.encode(), code, arr.ndim, _dims(arr.shape),
             arr.ctypes.data_as(ctypes.c_void_p)))
@@ -189,7 +190,9 @@ class GpuGraphExecutor:
                 check(self._L.icx_graph_set_input(self._g, name.encode(), code, t.dim(),
                                                   _dims(t.shape), ctypes.c_void_p(t.data_ptr()), 1))
                 continue
-            arr = np.ascontiguousarray(t.numpy() if isinstance(t, torch.Tensor) else np.asarray(t))
+            arr = np.asarray(t.numpy() if isinstance(t, torch.Tensor) else t)
+            if not arr.flags.c_contiguous:  # (np.ascontiguousarray would make a 0-d input 1-d)
+                arr = arr.copy(order="C")
             code = _NP_DT.get(arr.dtype)
             if code is None:
                 raise IconnxError(3, "input '%s': dtype %s unsupported" % (name, arr.dtype))

@@ -185,3 +185,18 @@ def encoder_graph(ex, layers=6, heads=12, hidden=768, ffn=3072, eps=1e-12, x_nam
 def encoder_input(batch=32, seq=128, hidden=768, seed=2999):
     """Input embeddings ~ N(0, 1), [batch, seq, hidden] float32."""
     return seeded_normal(batch * seq * hidden, seed).reshape(batch, seq, hidden)
+
+
+def write_model(path, build, *args, **kwargs):
+    """Serialise a graph built by one of the builders above into an .onnx file:
+    ``build(writer, *args, **kwargs)`` records the nodes (e.g. ``config_graph`` with a config
+    name, or ``encoder_graph``) and its first return value is the graph output.  Returns the
+    builder's return value."""
+    from .onnx import ModelWriter
+
+    w = ModelWriter()
+    ret = build(w, *args, **kwargs)
+    out = ret[0] if isinstance(ret, tuple) else ret
+    w.add_output(out)
+    w.save(path)
+    return ret

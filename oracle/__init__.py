@@ -171,9 +171,16 @@ def cast_i32_f32(x):
     return y
 
 
+def _contig(x, dtype):
+    """C-contiguous array of ``dtype`` keeping a 0-d input 0-d (np.ascontiguousarray would
+    make it 1-d; the reference's scalar tensors stay rank 0 through Mul / Add / Div)."""
+    x = np.asarray(x, dtype=dtype)
+    return x if x.flags.c_contiguous else x.copy(order="C")
+
+
 def _binary(op, a, b):
-    a = np.ascontiguousarray(a, dtype=np.float32)
-    b = np.ascontiguousarray(b, dtype=np.float32)
+    a = _contig(a, np.float32)
+    b = _contig(b, np.float32)
     r = max(a.ndim, b.ndim)
     out_shape = np.zeros(8, np.uintp)
     out_rank = ctypes.c_int(0)
@@ -284,7 +291,7 @@ def qlinear_graph(x, w, w_zp, x_scale_times_w_scale_inputs, bias, chain=(), rows
 
 # ---- encoder ops (fp32) ------------------------------------------------------------------
 def _f32(x):
-    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    return _contig(x, np.float32)
 
 
 def sum_unrolled8(x):

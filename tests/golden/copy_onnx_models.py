@@ -1,0 +1,40 @@
+"""Copy the ONNX 1.18 node-test models of the ops on this path, with their test_data_set_0
+input / output tensors, from the reference's vendored conformance data
+(tests/conformance_data/onnx-1.18/node/<test>/) into tests/golden/onnx_node/<test>/.
+These are data files (protobuf ModelProto / TensorProto), committed as fixtures; the GPU
+tests parse and execute them with iconnx_amd.onnx and GpuGraphExecutor.
+
+    python tests/golden/copy_onnx_models.py [/root/reference]
+"""
+import os
+import shutil
+import sys
+
+TESTS = [
+    "test_dynamicquantizelinear", "test_dynamicquantizelinear_max_adjusted",
+    "test_dynamicquantizelinear_min_adjusted", "test_matmulinteger", "test_dequantizelinear",
+    "test_dequantizelinear_axis", "test_mul", "test_mul_bcast", "test_add", "test_add_bcast",
+    "test_div", "test_div_bcast", "test_sub", "test_sub_bcast",
+    "test_layer_normalization_2d_axis_negative_1",
+    "test_layer_normalization_3d_axis_negative_1_epsilon", "test_softmax_axis_2",
+    "test_softmax_example", "test_erf", "test_transpose_default",
+    "test_transpose_all_permutations_0", "test_matmul_2d", "test_matmul_3d",
+]
+
+
+def main(ref):
+    src_root = os.path.join(ref, "tests", "conformance_data", "onnx-1.18", "node")
+    dst_root = os.path.join(os.path.dirname(os.path.abspath(__file__)), "onnx_node")
+    for t in TESTS:
+        src, dst = os.path.join(src_root, t), os.path.join(dst_root, t)
+        os.makedirs(os.path.join(dst, "test_data_set_0"), exist_ok=True)
+        shutil.copyfile(os.path.join(src, "model.onnx"), os.path.join(dst, "model.onnx"))
+        for f in sorted(os.listdir(os.path.join(src, "test_data_set_0"))):
+            if f.endswith(".pb"):
+                shutil.copyfile(os.path.join(src, "test_data_set_0", f),
+                                os.path.join(dst, "test_data_set_0", f))
+    print("copied %d models to %s" % (len(TESTS), dst_root))
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
