@@ -25,6 +25,7 @@
 // [1e-30, 1e30] — the f64 division is performed as the reference does.  The f64 path itself
 // uses x * (1/scale) and falls back to the correctly rounded division within 1e-9 of a tie.
 #include "icx_common.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -327,6 +328,43 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
 // The single-launch path: aligned operands, whole float4s, and a slice that fits kFRegs
 // float4 per lane (flat) or whole rows that do (row mode).
 extern "C" size_t icx_dql_workspace_size(size_t) { return sizeof(float2) * kMaxBlocks; }
+
+// The quantize launch alone, folding partials a producing kernel left (the same grid choice
+// and kernels as the second launch below).
+int icx::dql_from_parts(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                        int32_t* rowsum, size_t row_len, const float2* part, int n_part) {
+    if (!x || !y || !y_scale || !y_zp || !part || n_part <= 0)
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "DynamicQuantizeLinear: null pointer or no partials");
+    if (rowsum && (row_len == 0 || n % row_len != 0))
+        ICX_FAIL(ICX_ERR_SHAPE, "DynamicQuantizeLinear: row_len %zu does not divide n = %zu", row_len, n);
+    const bool x16 = icx::aligned16(x), y4 = (reinterpret_cast<uintptr_t>(y) & 3u) == 0;
+    if (rowsum) {
+        const size_t units = n / row_len;
+        const size_t rpw = std::max<size_t>(1, icx::cdiv(units, (size_t)4 * kMaxBlocks));
+        const int G = (int)std::max<size_t>(1, std::min<size_t>({(size_t)kMaxBlocks, icx::cdiv(units, 4 * rpw), units}));
+        const int rvec = (x16 && y4 && row_len % 4 == 0) ? 1 : 0;
+        hipLaunchKernelGGL(dql_quantize_rows_kernel, dim3(G), dim3(kThreads), 0, s, x, units, row_len, rvec, y,
+                           rowsum, part, n_part, y_scale, y_zp);
+        ICX_LAUNCH_CHECK("dql_quantize_rows_kernel");
+        return ICX_OK;
+    }
+    size_t units, unit, tail;
+    if (x16 && y4) {
+        units = n / 4;
+        unit = 4;
+        tail = n % 4;
+    } else {
+        units = n;
+        unit = 1;
+        tail = 0;
+    }
+    const int G = (int)std::max<size_t>(1, std::min<size_t>({(size_t)kMaxBlocks, icx::cdiv(n, (size_t)kThreads * 16), units}));
+    const int qvec = (x16 && y4 && unit == 4) ? 1 : 0;
+    hipLaunchKernelGGL(dql_quantize_kernel, dim3(G), dim3(kThreads), 0, s, x, units, unit, tail, qvec, y, part,
+                       n_part, y_scale, y_zp);
+    ICX_LAUNCH_CHECK("dql_quantize_kernel");
+    return ICX_OK;
+}
 
 extern "C" int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, size_t n,
                                            uint8_t* y, float* y_scale, uint8_t* y_zp,

@@ -12,6 +12,7 @@
 //       MatMul/Transpose/Reshape subgraph of a BERT self-attention, over [B, S, H*D]
 //       activations, with fp32 MFMA (v_mfma_f32_32x32x2f32) and the softmax in registers.
 #include "icx_common.hpp"
+#include "internal.hpp"
 
 #include <algorithm>
 
@@ -88,7 +89,7 @@ template <int PER>
 __global__ void __launch_bounds__(256)
 layer_norm_rows8_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t rows,
                         const float* __restrict__ scale, const float* __restrict__ bias, float eps,
-                        float* __restrict__ y) {
+                        float* __restrict__ y, float2* __restrict__ part) {
     constexpr int cols = 8 * PER, C4 = cols / 4, STRIDE = cols + 8;
     constexpr int PL = 8 * C4 / 256;  // float4 per lane for 8 rows
     static_assert(PL * 256 == 8 * C4, "8 rows split evenly over the block");
@@ -154,6 +155,7 @@ layer_norm_rows8_kernel(const float* __restrict__ x, const float* __restrict__ r
     float4* y4 = reinterpret_cast<float4*>(y + row0 * cols);
     const float4* s4 = reinterpret_cast<const float4*>(scale);
     const float4* b4 = reinterpret_cast<const float4*>(bias);
+    float mn = 0.0f, mx = 0.0f;  // DQL range of y (when `part` is given)
 #pragma unroll
     for (int u = 0; u < PL; ++u) {
         const int q = t + u * 256;
@@ -168,8 +170,15 @@ layer_norm_rows8_kernel(const float* __restrict__ x, const float* __restrict__ r
             o.z = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(a.z, mean), sd), sc.z), bi.z);
             o.w = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(a.w, mean), sd), sc.w), bi.w);
             icx::store_nt(&y4[q], o);
+            if (part) {
+                icx::range_acc(o.x, mn, mx);
+                icx::range_acc(o.y, mn, mx);
+                icx::range_acc(o.z, mn, mx);
+                icx::range_acc(o.w, mn, mx);
+            }
         }
     }
+    if (part) icx::block_range_store<256>(mn, mx, part);
 }
 
 __global__ void __launch_bounds__(kThreads)
@@ -298,6 +307,7 @@ struct AttnArgs {
     float scale;
     int scale_div;  // 1: x / scale, 0: x * scale
     int scale_q;    // 1: applied to Q before the product, 0: to the scores
+    float2* part;   // DQL range partials of out, one per block, or null
 };
 
 __device__ __forceinline__ float apply_scale(float x, const AttnArgs& a) {
@@ -403,14 +413,19 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
             o2[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, o2[j], 0, 0, 0);
         }
     }
+    float mn = 0.0f, mx = 0.0f;  // DQL range of out (when a.part is given)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int row = 32 * w + 8 * (r / 4) + 4 * lh + (r % 4);
         if (row >= S) continue;
         float* dst = a.out + ((size_t)b * S + row) * a.ldo + h * ATT_D;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) dst[32 * j + lr] = o2[j][r];
+        for (int j = 0; j < 2; ++j) {
+            dst[32 * j + lr] = o2[j][r];
+            if (a.part) icx::range_acc(o2[j][r], mn, mx);
+        }
     }
+    if (a.part) icx::block_range_store<kThreads>(mn, mx, a.part);
 }
 
 constexpr size_t kAttnSmem = (size_t)3 * ATT_S * QK_STRIDE * sizeof(float);
@@ -423,28 +438,39 @@ unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
 
 }  // namespace
 
-extern "C" int icx_layer_norm_f32(icx_stream_t stream, const float* x, const float* residual,
-                                  size_t rows, size_t cols, const float* scale,
-                                  const float* bias, float eps, float* y) {
-    icx::clear_error();
+int icx::layer_norm_f32(hipStream_t s, const float* x, const float* residual, size_t rows, size_t cols,
+                        const float* scale, const float* bias, float eps, float* y, float2* part,
+                        int* n_part) {
+    if (n_part) *n_part = 0;
     if (!x || !scale || !bias || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "LayerNormalization: null pointer argument");
     if (cols == 0 && rows) ICX_FAIL(ICX_ERR_SHAPE, "LayerNormalization: empty normalized axis");
     if (rows == 0) return ICX_OK;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const dim3 g8((unsigned)icx::cdiv(rows, 8));
+    // partials only from the LDS-staged kernel, one per block of 8 rows
+    float2* pp = (part && g8.x <= (unsigned)icx::kMaxRangeParts) ? part : nullptr;
     // the hidden sizes of the BERT family, float4-aligned: rows staged through LDS
     const bool a16 = icx::aligned16(x) && icx::aligned16(y) && icx::aligned16(scale) &&
                      icx::aligned16(bias) && (!residual || icx::aligned16(residual));
     switch (a16 ? cols : 0) {
-        case 512: hipLaunchKernelGGL(layer_norm_rows8_kernel<64>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y); break;
-        case 768: hipLaunchKernelGGL(layer_norm_rows8_kernel<96>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y); break;
-        case 1024: hipLaunchKernelGGL(layer_norm_rows8_kernel<128>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y); break;
+        case 512: hipLaunchKernelGGL(layer_norm_rows8_kernel<64>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y, pp); break;
+        case 768: hipLaunchKernelGGL(layer_norm_rows8_kernel<96>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y, pp); break;
+        case 1024: hipLaunchKernelGGL(layer_norm_rows8_kernel<128>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y, pp); break;
         default:
+            pp = nullptr;
             hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)icx::cdiv(rows, 32)), dim3(kThreads), 0, s, x,
                                residual, rows, cols, scale, bias, eps, y);
     }
     ICX_LAUNCH_CHECK("layer_norm_kernel");
+    if (pp && n_part) *n_part = (int)g8.x;
     return ICX_OK;
+}
+
+extern "C" int icx_layer_norm_f32(icx_stream_t stream, const float* x, const float* residual,
+                                  size_t rows, size_t cols, const float* scale,
+                                  const float* bias, float eps, float* y) {
+    icx::clear_error();
+    return icx::layer_norm_f32(reinterpret_cast<hipStream_t>(stream), x, residual, rows, cols, scale, bias,
+                               eps, y, nullptr, nullptr);
 }
 
 extern "C" int icx_softmax_f32(icx_stream_t stream, const float* x, size_t rows, size_t cols,
@@ -515,11 +541,10 @@ extern "C" int icx_matmul_f32(icx_stream_t stream, const float* a, const float* 
     return ICX_OK;
 }
 
-extern "C" int icx_attention_f32(icx_stream_t stream, const float* q, const float* k,
-                                 const float* v, size_t B, size_t S, size_t H, size_t D,
-                                 size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
-                                 int scale_div, int scale_q, float* out) {
-    icx::clear_error();
+int icx::attention_f32(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
+                       size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
+                       int scale_div, int scale_q, float* out, float2* part, int* n_part) {
+    if (n_part) *n_part = 0;
     if (!q || !k || !v || !out) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention: null pointer argument");
     if (D != (size_t)ATT_D || S == 0 || S > (size_t)ATT_S)
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention: head size %zu / sequence %zu unsupported (D = 64, S <= 128)", D, S);
@@ -528,8 +553,9 @@ extern "C" int icx_attention_f32(icx_stream_t stream, const float* q, const floa
         ICX_FAIL(ICX_ERR_SHAPE, "Attention: row strides must cover H*D and keep 16-byte alignment");
     if (B * H == 0) return ICX_OK;
     if (B * H > 0x7fffffff) ICX_FAIL(ICX_ERR_SHAPE, "Attention: too many (batch, head) pairs");
+    float2* pp = (part && B * H <= (size_t)icx::kMaxRangeParts) ? part : nullptr;
     AttnArgs a{q, k, v, out, (int)S, (int)H, (int64_t)ldq, (int64_t)ldk, (int64_t)ldv, (int64_t)ldo,
-               scale, scale_div ? 1 : 0, scale_q ? 1 : 0};
+               scale, scale_div ? 1 : 0, scale_q ? 1 : 0, pp};
     static bool smem_set = false;  // ~98 KB of dynamic LDS is above the default limit
     if (!smem_set) {
         ICX_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
@@ -537,8 +563,17 @@ extern "C" int icx_attention_f32(icx_stream_t stream, const float* q, const floa
                                           (int)kAttnSmem));
         smem_set = true;
     }
-    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)(B * H)), dim3(kThreads), kAttnSmem,
-                       reinterpret_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)(B * H)), dim3(kThreads), kAttnSmem, s, a);
     ICX_LAUNCH_CHECK("attention_kernel");
+    if (pp && n_part) *n_part = (int)(B * H);
     return ICX_OK;
+}
+
+extern "C" int icx_attention_f32(icx_stream_t stream, const float* q, const float* k,
+                                 const float* v, size_t B, size_t S, size_t H, size_t D,
+                                 size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
+                                 int scale_div, int scale_q, float* out) {
+    icx::clear_error();
+    return icx::attention_f32(reinterpret_cast<hipStream_t>(stream), q, k, v, B, S, H, D, ldq, ldk, ldv, ldo,
+                              scale, scale_div, scale_q, out, nullptr, nullptr);
 }

@@ -32,6 +32,7 @@
 #include <vector>
 
 #include "icx_common.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -240,6 +241,7 @@ struct icx_graph {
     std::set<std::string> keep;                // tensors that stay until the next run
     std::map<std::string, size_t> last_use;    // tensor -> plan index of its last reader
     std::set<std::string> rowsum_wanted;       // DQL outputs whose row sums a GEMM reads
+    std::set<std::string> range_wanted;        // DQL inputs whose producer leaves their range
 
     // device state
     std::map<std::string, DevTensor> weights;      // uploaded initializers
@@ -247,6 +249,7 @@ struct icx_graph {
     std::map<std::string, BoundInput> bound;       // inputs for the next run
     std::map<std::string, DevTensor> values;       // tensors of the current / last run
     std::map<std::string, std::string> rowsum_of;  // DQL y -> its row-sum tensor
+    std::map<std::string, std::pair<std::string, int>> range_of;  // DQL x -> (partials tensor, count)
     hipStream_t last_stream = nullptr;
     bool ran = false;
     Pool pool;
@@ -288,6 +291,7 @@ struct icx_graph {
             if (kv.second.pooled) pool.put(kv.second.ptr, kv.second.cls);
         values.clear();
         rowsum_of.clear();
+        range_of.clear();
     }
     void invalidate() {
         planned = compiled = false;
@@ -387,6 +391,22 @@ class Planner {
             auto p = gi_.producer.find(op.a);
             if (p != gi_.producer.end() && nodes_[p->second].op == "DynamicQuantizeLinear")
                 g_.rowsum_wanted.insert(op.a);
+        }
+        // a DynamicQuantizeLinear whose input is the output of a LayerNorm, attention or
+        // quantized-linear head takes that input's range from the head's kernel and runs its
+        // quantize launch only
+        g_.range_wanted.clear();
+        {
+            std::set<std::string> heads_out;
+            for (auto& op : g_.plan)
+                if (op.kind == Kind::FusedHead && (op.pattern == Pattern::AddLayerNorm ||
+                                                   op.pattern == Pattern::Attention ||
+                                                   op.pattern == Pattern::QuantizedLinear))
+                    heads_out.insert(op.out);
+            for (auto& op : g_.plan)
+                if (op.kind == Kind::Regular && op.node.op == "DynamicQuantizeLinear" && op.node.in.size() == 1 &&
+                    heads_out.count(op.node.in[0]))
+                    g_.range_wanted.insert(op.node.in[0]);
         }
         // last readers; a Reshape output aliases its input's buffer, so uses of the alias
         // extend the buffer's life, and a live alias keeps it until the next run
@@ -918,7 +938,8 @@ class Runner {
         for (auto it = g_.values.begin(); it != g_.values.end();) {
             const std::string& name = it->first;
             std::string key = name;
-            const size_t sfx = name.rfind("::rowsum");
+            size_t sfx = name.rfind("::rowsum");
+            if (sfx == std::string::npos) sfx = name.rfind("::range");
             if (sfx != std::string::npos) key = name.substr(0, sfx);
             auto lu = g_.last_use.find(key);
             const bool dead = !g_.keep.count(name) && (lu == g_.last_use.end() || lu->second <= i);
@@ -997,6 +1018,20 @@ class Runner {
         *out = &(g_.values[name] = t);
         return ICX_OK;
     }
+    // Partials buffer of `out` when a DynamicQuantizeLinear reads it (null otherwise).
+    int range_parts(const std::string& out, float2** part) {
+        *part = nullptr;
+        if (!g_.range_wanted.count(out)) return ICX_OK;
+        DevTensor* P;
+        int rc = alloc(out + "::range", ICX_F32, {2 * (int64_t)icx::kMaxRangeParts}, &P);
+        if (rc) return rc;
+        *part = static_cast<float2*>(P->ptr);
+        return ICX_OK;
+    }
+    void record_range(const std::string& out, int n_part) {
+        if (n_part > 0) g_.range_of[out] = {out + "::range", n_part};
+    }
+
     int workspace(size_t bytes) {
         if (bytes <= g_.ws_bytes) return ICX_OK;
         if (g_.ws) {
@@ -1136,8 +1171,14 @@ class Runner {
         if (rc) return rc;
         rc = workspace(icx_matmul_integer_workspace_size(M, pw.K, pw.N, 1));
         if (rc) return rc;
-        return icx_qlinear_f32(s_, a_ptr, a_dt, pw.packed, pw.dtype, 1, pw.colsum, M, pw.K, pw.N, azp, bzp, blen,
-                               rowsum, &ch, static_cast<float*>(Y->ptr), g_.ws, g_.ws_bytes);
+        float2* part;
+        rc = range_parts(op.out, &part);
+        if (rc) return rc;
+        int n_part = 0;
+        rc = icx::qlinear_f32(s_, a_ptr, a_dt, pw.packed, pw.dtype, 1, pw.colsum, M, pw.K, pw.N, azp, bzp, blen,
+                              rowsum, &ch, static_cast<float*>(Y->ptr), g_.ws, g_.ws_bytes, part, &n_part);
+        if (!rc) record_range(op.out, n_part);
+        return rc;
     }
 
     int shape_init(const std::string& name, std::vector<int64_t>* v) const {
@@ -1189,8 +1230,14 @@ class Runner {
         rc = alloc(op.out, ICX_F32, shape, &O);
         if (rc) return rc;
         const size_t hd = (size_t)shape[2];
-        return icx_attention_f32(s_, q, k, v, shape[0], shape[1], op.heads, op.head_dim, hd, hd, hd, hd, op.scale,
-                                 op.scale_div ? 1 : 0, op.scale_q ? 1 : 0, static_cast<float*>(O->ptr));
+        float2* part;
+        rc = range_parts(op.out, &part);
+        if (rc) return rc;
+        int n_part = 0;
+        rc = icx::attention_f32(s_, q, k, v, shape[0], shape[1], op.heads, op.head_dim, hd, hd, hd, hd, op.scale,
+                                op.scale_div ? 1 : 0, op.scale_q ? 1 : 0, static_cast<float*>(O->ptr), part, &n_part);
+        if (!rc) record_range(op.out, n_part);
+        return rc;
     }
 
     int run_layer_norm(const std::string& xn, const std::string& resn, const std::string& sn, const std::string& bn,
@@ -1231,8 +1278,14 @@ class Runner {
         DevTensor* Y;
         rc = alloc(out, ICX_F32, shape, &Y);
         if (rc) return rc;
-        return icx_layer_norm_f32(s_, x, r, cols ? numel(shape) / cols : 0, cols, sc, bi, eps,
-                                  static_cast<float*>(Y->ptr));
+        float2* part;
+        rc = range_parts(out, &part);
+        if (rc) return rc;
+        int n_part = 0;
+        rc = icx::layer_norm_f32(s_, x, r, cols ? numel(shape) / cols : 0, cols, sc, bi, eps,
+                                 static_cast<float*>(Y->ptr), part, &n_part);
+        if (!rc) record_range(out, n_part);
+        return rc;
     }
 
     int run_softmax(const Node& n) {
@@ -1439,6 +1492,14 @@ class Runner {
             rc = alloc(rname, ICX_I32, {cnt / (int64_t)row_len}, &R);
             if (rc) return rc;
             g_.rowsum_of[n.out[0]] = rname;
+        }
+        auto rg = g_.range_of.find(n.in[0]);
+        if (rg != g_.range_of.end() && cnt > 0) {  // the producer left the range: quantize only
+            const DevTensor* P = find(rg->second.first);
+            if (P)
+                return icx::dql_from_parts(s_, x, cnt, static_cast<uint8_t*>(Y->ptr), static_cast<float*>(S->ptr),
+                                           static_cast<uint8_t*>(Z->ptr), R ? static_cast<int32_t*>(R->ptr) : nullptr,
+                                           row_len, static_cast<const float2*>(P->ptr), rg->second.second);
         }
         rc = workspace(icx_dql_workspace_size(cnt));
         if (rc) return rc;
@@ -1702,6 +1763,7 @@ static int icx_graph_plan_impl(icx_graph* g, char* buf, size_t buf_len) {
                 o << m.name << " " << m.op << " " << kind_name(Kind::Skip) << " " << pattern_name(op.pattern) << "\n";
         }
         for (auto& r : g->rowsum_wanted) o << "rowsum " << r << "\n";
+        for (auto& r : g->range_wanted) o << "range " << r << "\n";
         const std::string s = o.str();
         if (s.size() + 1 > buf_len)
             ICX_FAIL(ICX_ERR_INVALID_ARG, "plan: summary needs %zu bytes, buffer has %zu", s.size() + 1, buf_len);

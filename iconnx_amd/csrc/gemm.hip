@@ -25,6 +25,7 @@
 // per MFMA.  Blocks are remapped so each XCD (blockIdx % 8) works on a contiguous,
 // M-grouped range of tiles that shares A/B panels in its own L2.
 #include "chain.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -56,6 +57,7 @@ struct GemmArgs {
     int a_zp_u8, b_zp_u8, b_zp_len;
     uint32_t codes;  // icx::chain_codes(chain)
     icx_chain chain;
+    float2* part;    // DQL range partials of the f32 output, one per block, or null
 };
 
 __device__ __forceinline__ int load_zp(const void* p, int is_u8, int idx) {
@@ -134,7 +136,7 @@ struct EpiLayout {
 template <int BM, int BN, int WGM, int WGN, int OUT, int CH>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
                                               v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
-                                              int8_t* smem, int m0, int n0) {
+                                              int8_t* smem, int m0, int n0, float& mn, float& mx) {
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
     constexpr int NT = 64 * WGM * WGN;
@@ -177,6 +179,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
         }
     }
     const bool vec_out = (g.N % 4 == 0) && ((reinterpret_cast<uintptr_t>(g.C) & 15u) == 0);
+    const bool rng = OUT == OUT_F32 && g.part != nullptr;  // uniform: track the DQL range
     float* stage = reinterpret_cast<float*>(smem) + wid * 32 * SROW;
 
 #pragma unroll
@@ -229,11 +232,20 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
             const size_t off = (size_t)grow * g.N + gcol;
             if (vec_out && gcol + 3 < g.N) {
                 icx::store_nt(reinterpret_cast<float4*>(reinterpret_cast<float*>(g.C) + off), v[q]);
+                if (rng) {
+                    icx::range_acc(v[q].x, mn, mx);
+                    icx::range_acc(v[q].y, mn, mx);
+                    icx::range_acc(v[q].z, mn, mx);
+                    icx::range_acc(v[q].w, mn, mx);
+                }
             } else {
                 const float* w = reinterpret_cast<const float*>(&v[q]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (gcol + e < g.N) reinterpret_cast<float*>(g.C)[off + e] = w[e];
+                    if (gcol + e < g.N) {
+                        reinterpret_cast<float*>(g.C)[off + e] = w[e];
+                        if (rng) icx::range_acc(w[e], mn, mx);
+                    }
             }
         }
     }
@@ -323,7 +335,9 @@ __global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
         __syncthreads();
     }
 
-    gemm_epilogue<BM, BN, 2, 2, OUT, CH>(g, acc, smem, m0, n0);
+    float mn = 0.0f, mx = 0.0f;
+    gemm_epilogue<BM, BN, 2, 2, OUT, CH>(g, acc, smem, m0, n0, mn, mx);
+    if (OUT == OUT_F32 && g.part) icx::block_range_store<kThreads>(mn, mx, g.part);
 }
 
 // ---- main loop B: LDS DMA (K % 64 == 0, 16-byte aligned operands) ---------------------
@@ -482,7 +496,9 @@ gemm_i8_dma_kernel(GemmArgs g) {
     }
     wait_vmcnt<0>();
     __syncthreads();  // all copies landed and all fragment reads done: LDS is free
-    gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0);
+    float mn = 0.0f, mx = 0.0f;
+    gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0, mn, mx);
+    if (OUT == OUT_F32 && g.part) icx::block_range_store<64 * WGM * WGN>(mn, mx, g.part);
 }
 
 // ---- main loop C: persistent producer / consumer (K % 64 == 0, column-only epilogue) ----
@@ -545,6 +561,7 @@ gemm_i8_stream_kernel(GemmArgs g) {
     const int KT = g.K / ROWB;
     const int S = ntiles * KT;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    float rmn = 0.0f, rmx = 0.0f;  // DQL range of the output (consumers; when g.part is given)
 
     if (wid >= NC) {
         // ------------------------------ producers -----------------------------------------
@@ -607,9 +624,7 @@ gemm_i8_stream_kernel(GemmArgs g) {
             issue_next();                  // step s+NS-1 into stage s-1's buffer
         }
         wait_vmcnt<0>();  // no copy may still target this block's LDS when it exits
-        return;
-    }
-
+    } else {
     // -------------------------------- consumers --------------------------------------------
     const int wm = wid / WGN, wn = wid % WGN;
     const int lr = lane & 31;
@@ -757,15 +772,19 @@ gemm_i8_stream_kernel(GemmArgs g) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int row = rbase + 8 * q + e;
-                            if (row < g.M)
+                            if (row < g.M) {
                                 __builtin_nontemporal_store(
                                     w[e], reinterpret_cast<float*>(g.C) + (size_t)row * g.N + col);
+                                if (OUT == OUT_F32 && g.part) icx::range_acc(w[e], rmn, rmx);
+                            }
                         }
                     }
                 }
             }
         }
     }
+    }  // consumers
+    if (OUT == OUT_F32 && g.part) icx::block_range_store<64 * (WGM * WGN + NP)>(rmn, rmx, g.part);
 }
 
 // ---- weight packing -------------------------------------------------------------------
@@ -949,7 +968,7 @@ int num_cus() {
 }
 
 template <int BM, int BN, int WGM, int WGN, int NP, int NS, int OUT, int CH>
-int launch_stream_one(unsigned tiles, hipStream_t s, const GemmArgs& g) {
+int launch_stream_one(unsigned tiles, hipStream_t s, GemmArgs g) {
     auto kern = gemm_i8_stream_kernel<BM, BN, WGM, WGN, NP, NS, OUT, CH>;
     constexpr int threads = 64 * (WGM * WGN + NP);
     static int per_cu[64] = {0};
@@ -965,25 +984,28 @@ int launch_stream_one(unsigned tiles, hipStream_t s, const GemmArgs& g) {
     }
     unsigned grid = (unsigned)(per_cu[d] * num_cus());
     if (grid > tiles) grid = tiles;
+    if (grid > (unsigned)icx::kMaxRangeParts) g.part = nullptr;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), 0, s, g);
-    return 0;
+    return g.part ? (int)grid : 0;
 }
 
+// Returns the number of range partials written (0: none).
 template <int BM, int BN, int WGM, int WGN, int NP, int NS>
-void launch_stream(int out_kind, int ch, unsigned tiles, hipStream_t s, const GemmArgs& g) {
+int launch_stream(int out_kind, int ch, unsigned tiles, hipStream_t s, const GemmArgs& g) {
     if (out_kind == OUT_I32)
-        launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_I32, CH_GENERAL>(tiles, s, g);
+        return launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_I32, CH_GENERAL>(tiles, s, g);
     else if (ch == CH_COL_EXT)
-        launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_F32, CH_COL_EXT>(tiles, s, g);
+        return launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_F32, CH_COL_EXT>(tiles, s, g);
     else
-        launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_F32, CH_COL>(tiles, s, g);
+        return launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_F32, CH_COL>(tiles, s, g);
 }
 
 int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,
                 int b_packed, const int32_t* b_colsum, size_t M, size_t K, size_t N,
                 const void* a_zp, const void* b_zp, size_t b_zp_len, const int32_t* a_rowsum,
                 const icx_chain* chain, void* C, int out_kind, void* ws, size_t ws_bytes,
-                const char* who) {
+                const char* who, float2* part = nullptr, int* n_part = nullptr) {
+    if (n_part) *n_part = 0;
     if (!A || !B || !C) ICX_FAIL(ICX_ERR_INVALID_ARG, "%s: null A, B or output pointer", who);
     if (!icx::is_int8_kind(a_dtype))
         ICX_FAIL(ICX_ERR_DTYPE, "%s: a dtype %d unsupported (must be Int8 or UInt8)", who, a_dtype);
@@ -1074,8 +1096,10 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     if (stream) {
         g.tiles_m = (int)icx::cdiv(M, 128);
         g.tiles_n = (int)icx::cdiv(N, 128);
-        launch_stream<128, 128, 4, 2, 2, 4>(out_kind, ch, (unsigned)(g.tiles_m * g.tiles_n), s, g);
+        if (out_kind == OUT_F32) g.part = part;
+        const int np = launch_stream<128, 128, 4, 2, 2, 4>(out_kind, ch, (unsigned)(g.tiles_m * g.tiles_n), s, g);
         ICX_LAUNCH_CHECK("gemm_i8_stream_kernel");
+        if (n_part) *n_part = np;
         return ICX_OK;
     }
     if (big) {
@@ -1083,6 +1107,7 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
         g.tiles_n = (int)icx::cdiv(N, 256);
     }
     const unsigned blocks = (unsigned)(g.tiles_m * g.tiles_n);
+    if (out_kind == OUT_F32 && part && blocks <= (unsigned)icx::kMaxRangeParts) g.part = part;
     if (dma) {
         if (big) launch_dma_big<2, 4, 4>(out_kind, blocks, s, g);
         else launch_dma<128, 128, 2, 2, 3>(out_kind, ch, blocks, s, g);
@@ -1091,6 +1116,7 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
         else launch_reg<128, 128>(vec, out_kind, ch, blocks, s, g);
     }
     ICX_LAUNCH_CHECK("gemm_i8_kernel");
+    if (n_part && g.part) *n_part = (int)blocks;
     return ICX_OK;
 }
 
@@ -1122,6 +1148,14 @@ extern "C" int icx_matmul_integer(icx_stream_t stream, const void* A, int a_dtyp
     return gemm_common(reinterpret_cast<hipStream_t>(stream), A, a_dtype, B, b_dtype, b_packed,
                        b_colsum, M, K, N, a_zp, b_zp, b_zp_len, a_rowsum, nullptr, C, OUT_I32,
                        ws, ws_bytes, "MatMulInteger");
+}
+
+int icx::qlinear_f32(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype, int b_packed,
+                     const int32_t* b_colsum, size_t M, size_t K, size_t N, const void* a_zp, const void* b_zp,
+                     size_t b_zp_len, const int32_t* a_rowsum, const icx_chain* chain, float* Y, void* ws,
+                     size_t ws_bytes, float2* part, int* n_part) {
+    return gemm_common(s, A, a_dtype, B, b_dtype, b_packed, b_colsum, M, K, N, a_zp, b_zp, b_zp_len, a_rowsum,
+                       chain, Y, OUT_F32, ws, ws_bytes, "QLinear", part, n_part);
 }
 
 extern "C" int icx_qlinear_f32(icx_stream_t stream, const void* A, int a_dtype, const void* B,

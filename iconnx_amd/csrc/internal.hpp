@@ -1,0 +1,31 @@
+// Library-internal entry points the graph executor uses (not part of the C ABI): the
+// producers of a DynamicQuantizeLinear input can leave the DQL range partials of their
+// output (see range_acc in icx_common.hpp), and the DQL then runs its quantize launch only.
+#pragma once
+
+#include "icx_common.hpp"
+
+namespace icx {
+
+// icx_layer_norm_f32 leaving up to kMaxRangeParts (min, max) partials of y in `part`
+// (may be null); *n_part = partials written, 0 when this shape's kernel leaves none.
+int layer_norm_f32(hipStream_t s, const float* x, const float* residual, size_t rows, size_t cols,
+                   const float* scale, const float* bias, float eps, float* y, float2* part, int* n_part);
+
+// icx_attention_f32 with the same partial output.
+int attention_f32(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
+                  size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
+                  int scale_div, int scale_q, float* out, float2* part, int* n_part);
+
+// icx_qlinear_f32 with the same partial output.
+int qlinear_f32(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype, int b_packed,
+                const int32_t* b_colsum, size_t M, size_t K, size_t N, const void* a_zp, const void* b_zp,
+                size_t b_zp_len, const int32_t* a_rowsum, const icx_chain* chain, float* Y, void* ws,
+                size_t ws_bytes, float2* part, int* n_part);
+
+// DynamicQuantizeLinear of x from the n_part partials its producer left: one launch (the
+// quantize pass of icx_dynamic_quantize_linear, which folds them).
+int dql_from_parts(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                   int32_t* rowsum, size_t row_len, const float2* part, int n_part);
+
+}  // namespace icx

@@ -160,17 +160,27 @@ class GpuGraphExecutor:
             if "buffer has" not in msg or size > (1 << 26):
                 check(rc)
             size *= 4
-        entries, rowsums = [], []
+        entries, rowsums, ranges = [], [], []
         for line in buf.value.decode().splitlines():
             parts = line.split()
             if parts[0] == "rowsum":
                 rowsums.append(parts[1])
                 continue
+            if parts[0] == "range":
+                ranges.append(parts[1])
+                continue
             extra = dict(p.split("=", 1) for p in parts[4:])
             entries.append(PlanEntry(parts[0], parts[1], parts[2], parts[3],
                                      int(extra.get("steps", 0)), extra.get("out"),
                                      extra.get("wzp") == "folded"))
+        self._range_inputs = ranges
         return entries, rowsums
+
+    def range_inputs(self):
+        """DynamicQuantizeLinear inputs whose producing kernel (LayerNorm, attention, a
+        quantized linear) leaves their min / max, so that DQL runs its quantize pass only."""
+        self.plan()
+        return list(self._range_inputs)
 
     def compile(self):
         torch = _torch()

@@ -315,3 +315,20 @@ def test_layer_norm_without_add_is_regular_and_attrs_are_checked():
     L = ex._L
     assert L.icx_graph_set_node_attr_float(ex._g, b"missing", b"epsilon", 1.0) != 0
     assert b"missing" in L.icx_last_error()
+
+
+def test_encoder_dql_ranges_come_from_producers():
+    """Every DynamicQuantizeLinear of the encoder except the first reads a tensor written by
+    a LayerNorm, attention or quantized-linear head, which leaves its min / max for it."""
+    from iconnx_amd import graphs
+
+    ex = GpuGraphExecutor()
+    out, names, _ = graphs.encoder_graph(ex, layers=2)
+    got = set(ex.range_inputs())
+    want = set()
+    for l, t in enumerate(names):
+        if l > 0:
+            want.add(t["x"])   # the previous layer's LayerNorm output
+        want |= {t["ctx"], t["x1"], t["h"]}
+    assert got == want
+    assert names[0]["x"] not in got  # the graph input has no producing kernel
