@@ -161,6 +161,13 @@ struct PlannedOp {
     // AddLayerNorm: LN(x + res)
     std::string ln_x, ln_res, ln_scale, ln_bias;
     float eps = 1e-5f;
+    // QuantizedLinear sibling group (heads over one activation, e.g. Q / K / V): the first
+    // in plan order (the lead) runs every member's GEMM as one launch over the
+    // column-concatenated weight; the other members run nothing.
+    std::string group;              // lead's node name, on every member; empty: no group
+    std::vector<int> group_members; // lead: plan indices of all members, lead first
+    std::string group_w;            // lead: key of the concatenated packed weight
+    std::vector<Step> group_steps;  // lead: the chain over the concatenated columns
 };
 
 struct DevTensor {
@@ -383,6 +390,7 @@ class Planner {
             }
         }
         g_.plan = ops;
+        group_siblings();
         g_.rowsum_wanted.clear();
         for (auto& op : g_.plan) {
             if (op.pattern != Pattern::QuantizedLinear) continue;
@@ -399,9 +407,9 @@ class Planner {
         {
             std::set<std::string> heads_out;
             for (auto& op : g_.plan)
-                if (op.kind == Kind::FusedHead && (op.pattern == Pattern::AddLayerNorm ||
-                                                   op.pattern == Pattern::Attention ||
-                                                   op.pattern == Pattern::QuantizedLinear))
+                if (op.kind == Kind::FusedHead && op.group.empty() &&
+                    (op.pattern == Pattern::AddLayerNorm || op.pattern == Pattern::Attention ||
+                     op.pattern == Pattern::QuantizedLinear))
                     heads_out.insert(op.out);
             for (auto& op : g_.plan)
                 if (op.kind == Kind::Regular && op.node.op == "DynamicQuantizeLinear" && op.node.in.size() == 1 &&
@@ -452,6 +460,88 @@ class Planner {
     std::vector<Node> nodes_;
     std::set<std::string> outs_;
     std::set<int> claimed_;
+
+    // ---- sibling quantized linears -------------------------------------------------------
+    // Heads that read the same activation and zero point, with weights of one dtype and
+    // shape [K, Nh] (Nh a multiple of 256), no weight zero point (absent or all zero), and
+    // chains of the same steps whose operands are either one shared scalar or static f32
+    // scalars / [Nh] vectors, become one GEMM over the concatenated [K, n*Nh] weight with
+    // each head's operands concatenated into [n*Nh] column vectors.  Every column then
+    // goes through exactly the arithmetic of its own head: a product operand is still
+    // p0 * p1 rounded once, and a scalar expanded to a column is the same value.
+    bool scalar_tensor(const std::string& t) const {
+        auto it = g_.inits.find(t);
+        if (it != g_.inits.end()) return it->second.dtype == ICX_F32 && numel(it->second.shape) == 1;
+        const int p = producer(t);  // y_scale of a DynamicQuantizeLinear is a scalar
+        return p >= 0 && nodes_[p].op == "DynamicQuantizeLinear" && nodes_[p].out.size() > 1 && nodes_[p].out[1] == t;
+    }
+    bool column_init(const std::string& t, int64_t nh) const {
+        auto it = g_.inits.find(t);
+        if (it == g_.inits.end() || it->second.dtype != ICX_F32) return false;
+        const auto& sh = it->second.shape;
+        return numel(sh) == 1 || (!sh.empty() && sh.back() == nh && numel(sh) == nh);
+    }
+    // operand slot shared by name (a scalar) or concatenable across the heads
+    bool groupable_operand(const std::vector<const PlannedOp*>& hs, size_t k, int which, int64_t nh) const {
+        auto name = [&](const PlannedOp* h) { return which ? h->steps[k].opnd1 : h->steps[k].opnd0; };
+        const std::string first = name(hs[0]);
+        bool same = true;
+        for (auto* h : hs) same = same && name(h) == first;
+        if (same) return first.empty() || scalar_tensor(first);
+        for (auto* h : hs)
+            if (name(h).empty() || !column_init(name(h), nh)) return false;
+        return true;
+    }
+    bool siblings(const PlannedOp& a, const PlannedOp& b) const {
+        if (a.a != b.a || a.a_zp != b.a_zp || a.steps.size() != b.steps.size()) return false;
+        const HostTensor& wa = g_.inits.at(a.w);
+        const HostTensor& wb = g_.inits.at(b.w);
+        if (wa.dtype != wb.dtype || wa.shape != wb.shape) return false;
+        for (size_t k = 0; k < a.steps.size(); ++k)
+            if (a.steps[k].op != b.steps[k].op || a.steps[k].lhs != b.steps[k].lhs ||
+                a.steps[k].opnd1.empty() != b.steps[k].opnd1.empty())
+                return false;
+        return true;
+    }
+    void group_siblings() {
+        std::vector<PlannedOp>& plan = g_.plan;
+        auto candidate = [&](const PlannedOp& op) {
+            if (op.kind != Kind::FusedHead || op.pattern != Pattern::QuantizedLinear || !op.group.empty()) return false;
+            const HostTensor& w = g_.inits.at(op.w);
+            return (op.w_zp.empty() || op.w_zp_folded) && w.shape.size() == 2 && w.shape[1] % 256 == 0 &&
+                   w.shape[1] > 0;
+        };
+        for (size_t i = 0; i < plan.size(); ++i) {
+            if (!candidate(plan[i])) continue;
+            std::vector<int> idx = {(int)i};
+            for (size_t j = i + 1; j < plan.size() && idx.size() < (size_t)icx::kMaxSegments; ++j)
+                if (candidate(plan[j]) && siblings(plan[i], plan[j])) idx.push_back((int)j);
+            if (idx.size() < 2) continue;
+            std::vector<const PlannedOp*> hs;
+            for (int k : idx) hs.push_back(&plan[k]);
+            const int64_t nh = g_.inits.at(plan[i].w).shape[1];
+            bool ok = true;
+            for (size_t k = 0; ok && k < plan[i].steps.size(); ++k) {
+                if (plan[i].steps[k].op > ICX_OP_DIV) continue;  // operand-free step
+                ok = groupable_operand(hs, k, 0, nh) && groupable_operand(hs, k, 1, nh);
+            }
+            if (!ok) continue;
+            PlannedOp& lead = plan[i];
+            lead.group_members = idx;
+            lead.group_w = lead.out + "::group.w";
+            lead.group_steps = lead.steps;
+            for (size_t k = 0; k < lead.steps.size(); ++k) {
+                if (lead.steps[k].op > ICX_OP_DIV) continue;
+                for (int which = 0; which < 2; ++which) {
+                    std::string& nm = which ? lead.group_steps[k].opnd1 : lead.group_steps[k].opnd0;
+                    bool same = true;
+                    for (auto* h : hs) same = same && (which ? h->steps[k].opnd1 : h->steps[k].opnd0) == nm;
+                    if (!same) nm = lead.out + "::group.c" + std::to_string(k) + "." + std::to_string(which);
+                }
+            }
+            for (int k : idx) plan[k].group = lead.node.name;
+        }
+    }
 
     // Requested outputs, or every node output that no node reads (mod.rs:505-519).
     void choose_outputs() {
@@ -1132,7 +1222,56 @@ class Runner {
         return ICX_OK;
     }
 
+    // A sibling group: one launch writes every member's output (segment s = member s).
+    int run_qlinear_group(const PlannedOp& op) {
+        const DevTensor* A;
+        int rc = need(op.a, &A, "QuantizedLinear");
+        if (rc) return rc;
+        auto pk = g_.packed.find(op.group_w);
+        if (pk == g_.packed.end()) {
+            set_error("QuantizedLinear: group weight of '%s' was not packed at compile", op.node.name.c_str());
+            return ICX_ERR_INVALID_ARG;
+        }
+        const PackedW& pw = pk->second;
+        const int n_seg = (int)op.group_members.size();
+        int64_t M;
+        std::vector<int64_t> lead;
+        rc = gemm_rows(A, pw.K, &M, &lead);
+        if (rc) return rc;
+        const void *azp, *bzp = nullptr;
+        size_t alen;
+        rc = zero_point(op.a_zp, A->dtype, false, pw.N, &azp, &alen);
+        if (rc) return rc;
+        const int32_t* rowsum = nullptr;
+        auto rs = g_.rowsum_of.find(op.a);
+        if (rs != g_.rowsum_of.end()) {
+            const DevTensor* r = find(rs->second);
+            if (r) rowsum = static_cast<const int32_t*>(r->ptr);
+        }
+        std::vector<int64_t> full = lead, part = lead;
+        full.push_back(pw.N);
+        part.push_back(pw.N / n_seg);
+        icx_chain ch;
+        rc = make_chain(op.group_steps, full, ch, "QuantizedLinear");
+        if (rc) return rc;
+        const void* a_ptr = A->ptr;
+        const int a_dt = A->dtype;
+        float* ys[icx::kMaxSegments] = {};
+        for (int i = 0; i < n_seg; ++i) {
+            DevTensor* Y;
+            rc = alloc(g_.plan[op.group_members[i]].out, ICX_F32, part, &Y);
+            if (rc) return rc;
+            ys[i] = static_cast<float*>(Y->ptr);
+        }
+        rc = workspace(icx_matmul_integer_workspace_size(M, pw.K, pw.N, 1));
+        if (rc) return rc;
+        return icx::qlinear_f32_seg(s_, a_ptr, a_dt, pw.packed, pw.dtype, pw.colsum, M, pw.K, pw.N, azp, bzp, 1,
+                                    rowsum, &ch, ys, n_seg, g_.ws, g_.ws_bytes);
+    }
+
     int run_qlinear(const PlannedOp& op) {
+        if (!op.group.empty())  // members other than the lead were written by its launch
+            return op.group_members.empty() ? ICX_OK : run_qlinear_group(op);
         const DevTensor* A;
         int rc = need(op.a, &A, "QuantizedLinear");
         if (rc) return rc;
@@ -1756,6 +1895,7 @@ static int icx_graph_plan_impl(icx_graph* g, char* buf, size_t buf_len) {
             if (op.kind == Kind::FusedHead) {
                 o << " steps=" << op.steps.size();
                 if (op.w_zp_folded) o << " wzp=folded";
+                if (!op.group.empty()) o << " group=" << op.group;
                 o << " out=" << op.out;
             }
             o << "\n";
@@ -1785,7 +1925,7 @@ static int icx_graph_compile_impl(icx_graph* g, icx_stream_t stream) {
     std::set<std::string> gemm_w;
     for (auto& op : g->plan) {
         if (op.kind == Kind::Skip) continue;
-        if (op.pattern == Pattern::QuantizedLinear) gemm_w.insert(op.w);
+        if (op.pattern == Pattern::QuantizedLinear && op.group.empty()) gemm_w.insert(op.w);
         if (op.kind == Kind::Regular && op.node.op == "MatMulInteger" && op.node.in.size() > 1) {
             auto it = g->inits.find(op.node.in[1]);
             if (it != g->inits.end() && it->second.shape.size() == 2) gemm_w.insert(op.node.in[1]);
@@ -1816,6 +1956,68 @@ static int icx_graph_compile_impl(icx_graph* g, icx_stream_t stream) {
             rc = icx_pack_weight(stream, t.ptr, h.dtype, pw.K, pw.N, pw.packed, pw.colsum);
             if (rc) return rc;
         }
+    }
+    // sibling groups: the column-concatenated weight, packed, and the concatenated column
+    // operands of their chains
+    for (auto& lead : g->plan) {
+        if (lead.group_members.empty()) continue;
+        std::vector<const PlannedOp*> hs;
+        for (int k : lead.group_members) hs.push_back(&g->plan[k]);
+        const HostTensor& w0 = g->inits.at(lead.w);
+        const int64_t K = w0.shape[0], nh = w0.shape[1], n = (int64_t)hs.size();
+        HostTensor cat;
+        cat.dtype = w0.dtype;
+        cat.shape = {K, n * nh};
+        cat.data.resize((size_t)(K * n * nh));
+        for (int64_t s_i = 0; s_i < n; ++s_i) {
+            const HostTensor& w = g->inits.at(hs[s_i]->w);
+            for (int64_t k = 0; k < K; ++k)
+                std::memcpy(&cat.data[(size_t)(k * n * nh + s_i * nh)], &w.data[(size_t)(k * nh)], (size_t)nh);
+        }
+        int8_t* raw = nullptr;
+        ICX_HIP_CHECK(hipMalloc(&raw, std::max<size_t>(cat.data.size(), 16)));
+        DevTensor rt;
+        rt.ptr = raw;
+        rt.dtype = cat.dtype;
+        rt.shape = cat.shape;
+        rt.bytes = cat.data.size();
+        g->weights[lead.group_w + ".raw"] = rt;
+        ICX_HIP_CHECK(hipMemcpyAsync(raw, cat.data.data(), cat.data.size(), hipMemcpyHostToDevice, s));
+        PackedW pw;
+        pw.K = K;
+        pw.N = n * nh;
+        pw.dtype = cat.dtype;
+        ICX_HIP_CHECK(hipMalloc(&pw.packed, std::max<size_t>(icx_packed_weight_bytes(pw.K, pw.N), 16)));
+        ICX_HIP_CHECK(hipMalloc(&pw.colsum, std::max<size_t>(4 * (size_t)pw.N, 4)));
+        g->packed[lead.group_w] = pw;
+        rc = icx_pack_weight(stream, raw, cat.dtype, pw.K, pw.N, pw.packed, pw.colsum);
+        if (rc) return rc;
+        // the host copies must outlive the asynchronous uploads: synchronise per group
+        std::vector<std::vector<float>> host_ops;
+        for (size_t k = 0; k < lead.group_steps.size(); ++k) {
+            for (int which = 0; which < 2; ++which) {
+                const std::string& nm = which ? lead.group_steps[k].opnd1 : lead.group_steps[k].opnd0;
+                if (nm.empty() || g->weights.count(nm) || g->inits.count(nm) ||
+                    nm.compare(0, lead.out.size() + 2, lead.out + "::") != 0)
+                    continue;
+                std::vector<float> col((size_t)(n * nh));
+                for (int64_t s_i = 0; s_i < n; ++s_i) {
+                    const HostTensor& c = g->inits.at(which ? hs[s_i]->steps[k].opnd1 : hs[s_i]->steps[k].opnd0);
+                    const float* src = reinterpret_cast<const float*>(c.data.data());
+                    const bool sc = numel(c.shape) == 1;
+                    for (int64_t j = 0; j < nh; ++j) col[(size_t)(s_i * nh + j)] = sc ? src[0] : src[j];
+                }
+                DevTensor t;
+                t.dtype = ICX_F32;
+                t.shape = {n * nh};
+                t.bytes = col.size() * 4;
+                ICX_HIP_CHECK(hipMalloc(&t.ptr, t.bytes));
+                g->weights[nm] = t;
+                ICX_HIP_CHECK(hipMemcpyAsync(t.ptr, col.data(), t.bytes, hipMemcpyHostToDevice, s));
+                host_ops.push_back(std::move(col));
+            }
+        }
+        ICX_HIP_CHECK(hipStreamSynchronize(s));
     }
     ICX_HIP_CHECK(hipStreamSynchronize(s));
     g->compiled = true;

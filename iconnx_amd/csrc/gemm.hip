@@ -58,7 +58,25 @@ struct GemmArgs {
     uint32_t codes;  // icx::chain_codes(chain)
     icx_chain chain;
     float2* part;    // DQL range partials of the f32 output, one per block, or null
+    // Segmented output (seg_n > 0): columns [s*seg_n, (s+1)*seg_n) go to the row-major
+    // [M, seg_n] tensor seg[s] instead of C.  seg_n is a multiple of the block tile width,
+    // so a tile lies in one segment.
+    void* seg[icx::kMaxSegments];
+    int seg_n;
 };
+
+// Output of the tile whose first column is n0: base pointer, row stride and the global
+// column that is column 0 of that output.
+struct OutView {
+    float* base;
+    int ld;
+    int c0;
+};
+__device__ __forceinline__ OutView out_view(const GemmArgs& g, int n0) {
+    if (g.seg_n <= 0) return {reinterpret_cast<float*>(g.C), g.N, 0};
+    const int s = n0 / g.seg_n;
+    return {reinterpret_cast<float*>(g.seg[s]), g.seg_n, s * g.seg_n};
+}
 
 __device__ __forceinline__ int load_zp(const void* p, int is_u8, int idx) {
     if (!p) return 0;
@@ -178,7 +196,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
             }
         }
     }
-    const bool vec_out = (g.N % 4 == 0) && ((reinterpret_cast<uintptr_t>(g.C) & 15u) == 0);
+    const OutView ov = out_view(g, n0);
+    const bool vec_out = (ov.ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(ov.base) & 15u) == 0);
     const bool rng = OUT == OUT_F32 && g.part != nullptr;  // uniform: track the DQL range
     float* stage = reinterpret_cast<float*>(smem) + wid * 32 * SROW;
 
@@ -229,9 +248,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
         for (int q = 0; q < NQ; ++q) {
             const int grow = rbase + q * RPI + rsub;
             if (grow >= g.M || gcol >= g.N) continue;
-            const size_t off = (size_t)grow * g.N + gcol;
+            const size_t off = (size_t)grow * ov.ld + (gcol - ov.c0);
             if (vec_out && gcol + 3 < g.N) {
-                icx::store_nt(reinterpret_cast<float4*>(reinterpret_cast<float*>(g.C) + off), v[q]);
+                icx::store_nt(reinterpret_cast<float4*>(ov.base + off), v[q]);
                 if (rng) {
                     icx::range_acc(v[q].x, mn, mx);
                     icx::range_acc(v[q].y, mn, mx);
@@ -243,7 +262,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     if (gcol + e < g.N) {
-                        reinterpret_cast<float*>(g.C)[off + e] = w[e];
+                        ov.base[off + e] = w[e];
                         if (rng) icx::range_acc(w[e], mn, mx);
                     }
             }
@@ -724,6 +743,7 @@ gemm_i8_stream_kernel(GemmArgs g) {
         // ---- epilogue straight from the accumulators -------------------------------------
         // lane = column (n0 + j*32 + lr); register r of tile (i, j) = row
         // m0 + i*32 + 8*(r>>2) + 4*(lane>>5) + (r&3).
+        const OutView ow = out_view(g, tn * BN);
         uint32_t colfac[TJ], colterm[TJ];
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
@@ -774,7 +794,7 @@ gemm_i8_stream_kernel(GemmArgs g) {
                             const int row = rbase + 8 * q + e;
                             if (row < g.M) {
                                 __builtin_nontemporal_store(
-                                    w[e], reinterpret_cast<float*>(g.C) + (size_t)row * g.N + col);
+                                    w[e], ow.base + (size_t)row * ow.ld + (col - ow.c0));
                                 if (OUT == OUT_F32 && g.part) icx::range_acc(w[e], rmn, rmx);
                             }
                         }
@@ -1004,8 +1024,18 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
                 int b_packed, const int32_t* b_colsum, size_t M, size_t K, size_t N,
                 const void* a_zp, const void* b_zp, size_t b_zp_len, const int32_t* a_rowsum,
                 const icx_chain* chain, void* C, int out_kind, void* ws, size_t ws_bytes,
-                const char* who, float2* part = nullptr, int* n_part = nullptr) {
+                const char* who, float2* part = nullptr, int* n_part = nullptr,
+                float* const* segs = nullptr, int n_seg = 0) {
     if (n_part) *n_part = 0;
+    if (n_seg) {
+        if (out_kind != OUT_F32 || n_seg < 1 || n_seg > icx::kMaxSegments || N % n_seg != 0 ||
+            (N / n_seg) % 256 != 0 || part)
+            ICX_FAIL(ICX_ERR_INVALID_ARG, "%s: %d output segments over N = %zu (segments must be equal, a "
+                     "multiple of 256 columns, at most %d, no range partials)", who, n_seg, N, icx::kMaxSegments);
+        for (int i = 0; i < n_seg; ++i)
+            if (!segs[i]) ICX_FAIL(ICX_ERR_INVALID_ARG, "%s: null output segment %d", who, i);
+        C = segs[0];
+    }
     if (!A || !B || !C) ICX_FAIL(ICX_ERR_INVALID_ARG, "%s: null A, B or output pointer", who);
     if (!icx::is_int8_kind(a_dtype))
         ICX_FAIL(ICX_ERR_DTYPE, "%s: a dtype %d unsupported (must be Int8 or UInt8)", who, a_dtype);
@@ -1079,6 +1109,8 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     if (chain) g.chain = *chain;
     else g.chain.n_ops = 0;
     g.codes = icx::chain_codes(g.chain);
+    g.seg_n = n_seg ? (int)(N / n_seg) : 0;
+    for (int i = 0; i < n_seg; ++i) g.seg[i] = segs[i];
 
     const bool vec = K >= 16 && (K % 16 == 0) && icx::aligned16(A) && icx::aligned16(Bp);
     const bool dma = vec && K >= 64 && K % 64 == 0;
@@ -1156,6 +1188,14 @@ int icx::qlinear_f32(hipStream_t s, const void* A, int a_dtype, const void* B, i
                      size_t ws_bytes, float2* part, int* n_part) {
     return gemm_common(s, A, a_dtype, B, b_dtype, b_packed, b_colsum, M, K, N, a_zp, b_zp, b_zp_len, a_rowsum,
                        chain, Y, OUT_F32, ws, ws_bytes, "QLinear", part, n_part);
+}
+
+int icx::qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,
+                         const int32_t* b_colsum, size_t M, size_t K, size_t N, const void* a_zp,
+                         const void* b_zp, size_t b_zp_len, const int32_t* a_rowsum, const icx_chain* chain,
+                         float* const* ys, int n_seg, void* ws, size_t ws_bytes) {
+    return gemm_common(s, A, a_dtype, B, b_dtype, 1, b_colsum, M, K, N, a_zp, b_zp, b_zp_len, a_rowsum, chain,
+                       nullptr, OUT_F32, ws, ws_bytes, "QLinear", nullptr, nullptr, ys, n_seg);
 }
 
 extern "C" int icx_qlinear_f32(icx_stream_t stream, const void* A, int a_dtype, const void* B,

@@ -97,6 +97,9 @@ __device__ __forceinline__ void block_range_store(float mn, float mx, float2* pa
 // Most partials any producing kernel leaves (the DQL quantize launch folds them).
 constexpr int kMaxRangeParts = 1024;
 
+// Most output segments of one GEMM launch (sibling linears over one input, e.g. Q / K / V).
+constexpr int kMaxSegments = 4;
+
 // int8 / uint8 operand description used by the GEMM entry points.
 inline bool is_int8_kind(int dt) { return dt == ICX_I8 || dt == ICX_U8; }
 

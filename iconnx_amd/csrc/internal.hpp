@@ -23,6 +23,15 @@ int qlinear_f32(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
                 size_t b_zp_len, const int32_t* a_rowsum, const icx_chain* chain, float* Y, void* ws,
                 size_t ws_bytes, float2* part, int* n_part);
 
+// Sibling quantized linears over one input in one launch: B is the packed weight of the
+// column-concatenated [K, N] weight, N = n_seg equal segments of a multiple of 256 columns,
+// segment s (columns [s*N/n_seg, (s+1)*N/n_seg)) stored as the row-major [M, N/n_seg]
+// tensor ys[s].  Column chain operands index the concatenated N.
+int qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,
+                    const int32_t* b_colsum, size_t M, size_t K, size_t N, const void* a_zp, const void* b_zp,
+                    size_t b_zp_len, const int32_t* a_rowsum, const icx_chain* chain, float* const* ys,
+                    int n_seg, void* ws, size_t ws_bytes);
+
 // DynamicQuantizeLinear of x from the n_part partials its producer left: one launch (the
 // quantize pass of icx_dynamic_quantize_linear, which folds them).
 int dql_from_parts(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,

@@ -30,7 +30,9 @@ _NP_DT = {np.dtype(np.int8): ICX_I8, np.dtype(np.uint8): ICX_U8,
 _INIT_DT = {**_NP_DT, np.dtype(np.int64): ICX_I64}
 _DT_NP = {v: k for k, v in _NP_DT.items()}
 
-PlanEntry = namedtuple("PlanEntry", "node op_type kind pattern steps out wzp_folded")
+# group: for a quantized linear run as one launch with its siblings, the lead's node name
+PlanEntry = namedtuple("PlanEntry", "node op_type kind pattern steps out wzp_folded group",
+                       defaults=(None,))
 
 
 def _torch():
@@ -172,7 +174,7 @@ class GpuGraphExecutor:
             extra = dict(p.split("=", 1) for p in parts[4:])
             entries.append(PlanEntry(parts[0], parts[1], parts[2], parts[3],
                                      int(extra.get("steps", 0)), extra.get("out"),
-                                     extra.get("wzp") == "folded"))
+                                     extra.get("wzp") == "folded", extra.get("group")))
         self._range_inputs = ranges
         return entries, rowsums
 

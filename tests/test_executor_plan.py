@@ -169,6 +169,50 @@ def test_shared_dql_for_three_projections():
     assert sum(e.op_type == "DynamicQuantizeLinear" and e.kind == "Regular" for e in entries) == 1
 
 
+def _siblings(n, N=256, w_zps=None, chains=None, w_scales=None, dtypes=None, K=8):
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, K])
+    dql = graphs.add_dynamic_quantize(ex, "x", "s")
+    rng = np.random.default_rng(1)
+    outs = []
+    for i in range(n):
+        dt = dtypes[i] if dtypes else np.int8
+        w = rng.integers(0 if dt == np.uint8 else -127, 128, size=(K, N)).astype(dt)
+        zp = np.asarray(w_zps[i] if w_zps else 0).astype(dt)
+        sc = w_scales[i] if w_scales else np.float32(0.01 * (i + 1))
+        outs.append(graphs.add_quantized_linear(ex, "x", w, zp, sc, rng.standard_normal(N).astype(np.float32),
+                                                chains[i] if chains else (), prefix="h%d" % i, dql=dql))
+    for o in outs:
+        ex.add_output(o)
+    entries, _ = ex.plan()
+    return [next(e.group for e in entries if e.node == "h%d.mmi" % i) for i in range(n)]
+
+
+def test_sibling_linears_group_into_one_gemm():
+    assert _siblings(3) == ["h0.mmi"] * 3
+    assert _siblings(2, N=512) == ["h0.mmi"] * 2
+    # at most four segments per launch; the rest group among themselves
+    assert _siblings(6) == ["h0.mmi"] * 4 + ["h4.mmi"] * 2
+    assert _siblings(5) == ["h0.mmi"] * 4 + [None]
+    # scalar and per-column scales mix (each expands to a column vector)
+    assert _siblings(3, w_scales=[np.float32(0.01), np.full(256, 0.02, np.float32), np.float32(0.03)]) == \
+        ["h0.mmi"] * 3
+    # a lone head, widths that are not a multiple of 256, or unequal widths: no group
+    assert _siblings(1) == [None]
+    assert _siblings(3, N=16) == [None] * 3
+    assert _siblings(3, N=384) == [None] * 3
+    # a non-zero weight zero point keeps the head out; the other two still group
+    assert _siblings(3, w_zps=[0, 3, 0]) == ["h0.mmi", None, "h0.mmi"]
+    # a head whose chain has other steps stays single
+    ch = [(), [("Mul", np.float32(2.0))], ()]
+    assert _siblings(3, chains=ch) == ["h0.mmi", None, "h0.mmi"]
+    # same step kinds with different constants group (constants become columns)
+    ch = [[("Mul", np.float32(2.0))], [("Mul", np.float32(3.0))], [("Mul", np.arange(256, dtype=np.float32))]]
+    assert _siblings(3, chains=ch) == ["h0.mmi"] * 3
+    # weights of different dtypes do not share a launch
+    assert _siblings(2, dtypes=[np.int8, np.uint8], w_zps=[0, 0]) == [None, None]
+
+
 def test_insertion_order_does_not_matter():
     ref = GpuGraphExecutor()
     ref.add_input("x", [None, 8])
@@ -260,6 +304,12 @@ def test_encoder_layer_plan():
     assert rowsums == []  # zero int8 weight zero points are folded
     heads = {e.node: e for e in entries if e.kind == "FusedHead"}
     assert heads["L0.ff1.mmi"].out == "L0.ff1.gelu.gelu"
+    # Q / K / V run as one GEMM led by the first; O and the FFN linears stay single
+    for l in (0, 1):
+        for p in ("q", "k", "v"):
+            assert heads["L%d.%s.mmi" % (l, p)].group == "L%d.q.mmi" % l
+        for p in ("o", "ff1", "ff2"):
+            assert heads["L%d.%s.mmi" % (l, p)].group is None
     assert heads["L1.attn.softmax"].out == "L1.attn.ctx"
     skipped = {e.node for e in entries if e.kind == "Skip"}
     for n in ("L0.attn.reshape_q", "L0.attn.transpose_k", "L0.attn.scale_q", "L0.attn.scores",
