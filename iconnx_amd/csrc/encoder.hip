@@ -285,17 +285,23 @@ matmul_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, int 
 }
 
 // ---- fused self-attention, S <= 128, D == 64 --------------------------------------------
-// One block per (batch, head), 4 waves; wave w owns query rows [32w, 32w + 32).
-//   scores = (Q K^T) (*|/) scale   (or Q scaled first)  — 4 tiles of 32x32, K = 64
-//   P = softmax over the keys, in registers (lanes of a half-wave hold one row's columns)
-//   ctx = P V                                            — 2 tiles of 32x32, K = S
+// One block per (batch, head), 4 waves; wave w owns query rows [32w, 32w + 32).  K and V
+// sit in LDS (66 KB, so two blocks share a CU); each lane keeps its Q fragment in registers.
+//   S^T = K Q^T (*|/) scale (or Q scaled first): 4 key tiles of 32 x 32, contraction 64
+//   P = softmax over the keys, in registers
+//   ctx = P V: 2 tiles of 32 x 32, contraction S
 // v_mfma_f32_32x32x2f32: A lane l = A[l % 32][l / 32], B lane l = B[l / 32][l % 32],
 // D register r of lane l = D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+// Computing S^T rather than S leaves lane l with query l % 32 and, in register r of key tile
+// jt, key 32 jt + 8 (r / 4) + 4 (l / 32) + r % 4 (the other half-wave holds the row's other
+// keys).  That is exactly P's A-operand layout for the product with V when step (jt, r)
+// contracts over those keys, so P never leaves registers.  Each contraction visits its terms
+// in an order fixed for A and B alike (dims 32 (l / 32) + s; the keys above).
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int ATT_S = 128, ATT_D = 64;
-constexpr int QK_STRIDE = ATT_D + 1;   // floats per LDS row of Q, K, V (bank-conflict free)
-constexpr int P_STRIDE = ATT_S + 1;
+constexpr int K_STRIDE = ATT_D + 4;  // floats per LDS row of K: 16-byte fragment reads conflict-free
+constexpr int V_STRIDE = ATT_D;      // V is read one 128-byte row segment per half-wave
 
 struct AttnArgs {
     const float* q;
@@ -314,105 +320,117 @@ __device__ __forceinline__ float apply_scale(float x, const AttnArgs& a) {
     return a.scale_div ? __fdiv_rn(x, a.scale) : __fmul_rn(x, a.scale);
 }
 
-__global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
+__device__ __forceinline__ float f4c(const float4& v, int e) {
+    return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
+
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+attention_kernel(AttnArgs a) {
     extern __shared__ float smem[];
-    float* sq = smem;                        // [128][65]
-    float* sk = sq + ATT_S * QK_STRIDE;      // [128][65]
-    float* sv = sk + ATT_S * QK_STRIDE;      // [128][65]
-    float* sp = smem;                        // [128][129], over Q and K once they are read
+    float* sk = smem;                     // [128][K_STRIDE]
+    float* sv = smem + ATT_S * K_STRIDE;  // [128][V_STRIDE]
     const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
     const int S = a.S;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int lr = lane & 31, lh = lane >> 5;
+    const int qi = 32 * w + lr;  // this lane's query row
 
-    // load Q, K, V of (b, h): rows past S are zero
-    for (int i = t; i < ATT_S * (ATT_D / 4); i += kThreads) {
-        const int r = i / (ATT_D / 4), c4 = (i % (ATT_D / 4)) * 4;
-        float4 qv = make_float4(0, 0, 0, 0), kv = qv, vv = qv;
+    // every load in flight at once: K and V of (b, h) (rows past S are zero), and this
+    // lane's Q fragment, dims [32 lh, 32 lh + 32) of row qi
+    float4 kr[8], vr[8], qr[8];
+    const int c4 = (t & 15) * 4;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int r = u * 16 + (t >> 4);
+        kr[u] = vr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (r < S) {
             const size_t row = (size_t)b * S + r;
-            qv = *reinterpret_cast<const float4*>(a.q + row * a.ldq + h * ATT_D + c4);
-            kv = *reinterpret_cast<const float4*>(a.k + row * a.ldk + h * ATT_D + c4);
-            vv = *reinterpret_cast<const float4*>(a.v + row * a.ldv + h * ATT_D + c4);
-            if (a.scale_q) {
-                qv.x = apply_scale(qv.x, a);
-                qv.y = apply_scale(qv.y, a);
-                qv.z = apply_scale(qv.z, a);
-                qv.w = apply_scale(qv.w, a);
-            }
+            kr[u] = *reinterpret_cast<const float4*>(a.k + row * a.ldk + h * ATT_D + c4);
+            vr[u] = *reinterpret_cast<const float4*>(a.v + row * a.ldv + h * ATT_D + c4);
         }
-        float* dq = sq + r * QK_STRIDE + c4;
-        float* dk = sk + r * QK_STRIDE + c4;
-        float* dv = sv + r * QK_STRIDE + c4;
-        dq[0] = qv.x; dq[1] = qv.y; dq[2] = qv.z; dq[3] = qv.w;
-        dk[0] = kv.x; dk[1] = kv.y; dk[2] = kv.z; dk[3] = kv.w;
-        dv[0] = vv.x; dv[1] = vv.y; dv[2] = vv.z; dv[3] = vv.w;
+    }
+    const float* qp = a.q + ((size_t)b * S + qi) * a.ldq + h * ATT_D + 32 * lh;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+        qr[u] = qi < S ? *reinterpret_cast<const float4*>(qp + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int r = u * 16 + (t >> 4);
+        *reinterpret_cast<float4*>(sk + r * K_STRIDE + c4) = kr[u];
+        *reinterpret_cast<float4*>(sv + r * V_STRIDE + c4) = vr[u];
+    }
+    if (a.scale_q) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            qr[u].x = apply_scale(qr[u].x, a);
+            qr[u].y = apply_scale(qr[u].y, a);
+            qr[u].z = apply_scale(qr[u].z, a);
+            qr[u].w = apply_scale(qr[u].w, a);
+        }
     }
     __syncthreads();
 
-    // scores for rows [32w, 32w+32) x 128 keys
-    v16f acc[4];
+    // S^T: A = K (lane = key), B = Q^T (lane = query)
+    v16f st[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int jt = 0; jt < 4; ++jt) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
-    const int qrow = 32 * w + lr;
-#pragma unroll 4
-    for (int k2 = 0; k2 < ATT_D / 2; ++k2) {
-        const int kk = 2 * k2 + lh;
-        const float av = sq[qrow * QK_STRIDE + kk];
+        for (int r = 0; r < 16; ++r) st[jt][r] = 0.0f;
+        const float* kp = sk + (32 * jt + lr) * K_STRIDE + 32 * lh;
+        float4 kf[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float bv = sk[(32 * j + lr) * QK_STRIDE + kk];
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[j], 0, 0, 0);
-        }
+        for (int u = 0; u < 8; ++u) kf[u] = *reinterpret_cast<const float4*>(kp + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                st[jt] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4c(kf[u], e), f4c(qr[u], e), st[jt], 0, 0, 0);
     }
-    __syncthreads();  // Q and K are no longer read: P may overwrite them
 
-    // softmax of each row; row of register r in this half-wave: 32w + 8(r/4) + 4 lh + r%4
+    // softmax of row qi over its S keys: 64 here, 64 in lane ^ 32
+    float m = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        float s[4];
-        float m = -INFINITY;
+    for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int col = 32 * j + lr;
-            s[j] = a.scale_q ? acc[j][r] : apply_scale(acc[j][r], a);
-            if (col >= S) s[j] = -INFINITY;
-            m = fmaxf(m, s[j]);
+        for (int r = 0; r < 16; ++r) {
+            const int key = 32 * jt + 8 * (r / 4) + 4 * lh + (r % 4);
+            float x = a.scale_q ? st[jt][r] : apply_scale(st[jt][r], a);
+            if (key >= S) x = -INFINITY;
+            st[jt][r] = x;
+            m = fmaxf(m, x);
         }
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    float sum = 0.0f;
 #pragma unroll
-        for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 32));
-        float sum = 0.0f;
+    for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            s[j] = expf(__fsub_rn(s[j], m));
-            sum = __fadd_rn(sum, s[j]);
+        for (int r = 0; r < 16; ++r) {
+            const float e = expf(__fsub_rn(st[jt][r], m));
+            st[jt][r] = e;
+            sum = __fadd_rn(sum, e);
         }
+    sum = __fadd_rn(sum, __shfl_xor(sum, 32, 64));
 #pragma unroll
-        for (int o = 16; o > 0; o >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, o, 32));
-        const int row = 32 * w + 8 * (r / 4) + 4 * lh + (r % 4);
+    for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sp[row * P_STRIDE + 32 * j + lr] = __fdiv_rn(s[j], sum);
-    }
-    __syncthreads();
+        for (int r = 0; r < 16; ++r) st[jt][r] = __fdiv_rn(st[jt][r], sum);
 
-    // ctx = P V for rows [32w, 32w+32) x 64
+    // ctx = P V: A = P straight from the S^T registers, B = V rows from LDS
     v16f o2[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o2[j][r] = 0.0f;
-#pragma unroll 4
-    for (int c2 = 0; c2 < ATT_S / 2; ++c2) {
-        const int cc = 2 * c2 + lh;
-        const float av = sp[qrow * P_STRIDE + cc];
+        for (int r = 0; r < 16; ++r) o2[dt][r] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const float bv = sv[cc * QK_STRIDE + 32 * j + lr];
-            o2[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, o2[j], 0, 0, 0);
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = 32 * jt + 8 * (r / 4) + 4 * lh + (r % 4);
+            const float* vp = sv + key * V_STRIDE + lr;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+                o2[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(st[jt][r], vp[32 * dt], o2[dt], 0, 0, 0);
         }
-    }
     float mn = 0.0f, mx = 0.0f;  // DQL range of out (when a.part is given)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -420,15 +438,15 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
         if (row >= S) continue;
         float* dst = a.out + ((size_t)b * S + row) * a.ldo + h * ATT_D;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            dst[32 * j + lr] = o2[j][r];
-            if (a.part) icx::range_acc(o2[j][r], mn, mx);
+        for (int dt = 0; dt < 2; ++dt) {
+            dst[32 * dt + lr] = o2[dt][r];
+            if (a.part) icx::range_acc(o2[dt][r], mn, mx);
         }
     }
     if (a.part) icx::block_range_store<kThreads>(mn, mx, a.part);
 }
 
-constexpr size_t kAttnSmem = (size_t)3 * ATT_S * QK_STRIDE * sizeof(float);
+constexpr size_t kAttnSmem = (size_t)ATT_S * (K_STRIDE + V_STRIDE) * sizeof(float);
 
 unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
     size_t b = icx::cdiv(work, per_block);
@@ -556,7 +574,7 @@ int icx::attention_f32(hipStream_t s, const float* q, const float* k, const floa
     float2* pp = (part && B * H <= (size_t)icx::kMaxRangeParts) ? part : nullptr;
     AttnArgs a{q, k, v, out, (int)S, (int)H, (int64_t)ldq, (int64_t)ldk, (int64_t)ldv, (int64_t)ldo,
                scale, scale_div ? 1 : 0, scale_q ? 1 : 0, pp};
-    static bool smem_set = false;  // ~98 KB of dynamic LDS is above the default limit
+    static bool smem_set = false;  // 66 KB of dynamic LDS is above the default limit
     if (!smem_set) {
         ICX_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
                                           hipFuncAttributeMaxDynamicSharedMemorySize,
