@@ -18,12 +18,13 @@
 // shape: the kernel is an "NT" GEMM whose 16-byte global loads and 16-byte LDS fragment
 // reads are all contiguous.
 //
-// Tiling: 256 threads = 4 waves (2x2), K step 64, LDS double buffered with rows padded by
-// 16 B.  Two block tiles: 128x128 (wave 64x64 = 2x2 v_mfma_i32_32x32x32_i8, 40 KB LDS) for
-// shapes with few tiles, and 256x256 (wave 128x128 = 4x4 MFMA tiles, accumulators in
-// AGPRs, 80 KB LDS) for large ones, where the bigger wave tile halves the LDS bytes read
-// per MFMA.  Blocks are remapped so each XCD (blockIdx % 8) works on a contiguous,
-// M-grouped range of tiles that shares A/B panels in its own L2.
+// Tiling: v_mfma_i32_32x32x32_i8 tiles.  128x128 block tiles (4 waves of 64x64, three
+// blocks per CU) for shapes with few tiles; 256x256 (8 waves of 128x64) when there are at
+// least 512 of them; a persistent producer/consumer kernel for K-heavy shapes with fewer
+// tiles than CUs.  Operand tiles reach LDS by LDS DMA (main loops B, B2, C) or through
+// registers (main loop A: any K and alignment).  Blocks are remapped so each XCD
+// (blockIdx % 8) works on a contiguous, M-grouped range of tiles that shares A/B panels in
+// its own L2.
 #include "chain.hpp"
 #include "internal.hpp"
 
@@ -520,6 +521,140 @@ gemm_i8_dma_kernel(GemmArgs g) {
     if (OUT == OUT_F32 && g.part) icx::block_range_store<64 * WGM * WGN>(mn, mx, g.part);
 }
 
+// ---- main loop B2: LDS DMA with 128-byte K rows (256x256 tile, K % 128 == 0) ------------
+// The large-shape variant of main loop B.  A stage holds two 64-wide K steps as 128-byte
+// LDS rows, so every lane-octet of a copy reads one whole 128-byte line of a row (the
+// 64-byte rows of main loop B read half a line per copy, and the copies' throughput from L2
+// is what bounds this GEMM).  Two stages of 64 KB (128 KB): the copies of stage kt+2 are
+// issued into stage kt's buffer right after the barrier that ends stage kt, so they have one
+// stage (four 32-wide MFMA K steps per wave) to land.  Chunk c of row r sits at slot
+// c ^ ((r >> 1) & 7): the 16 lanes of a fragment read that share a cycle hit 16 distinct
+// 16-byte bank groups.  8 waves (2 x 4, 128 x 64 each); waves 0-3 issue the copies, eight
+// 8-row copies of A and eight of B per stage each.
+template <int OUT, int CH>
+__global__ void __launch_bounds__(512) gemm_i8_dma128_kernel(GemmArgs g) {
+    constexpr int BM = 256, BN = 256, WGM = 2, WGN = 4;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TI = WM / 32, TJ = WN / 32;
+    constexpr int ROWB = 128;
+    constexpr int STAGE = (BM + BN) * ROWB;
+    constexpr int DW = 4;
+    constexpr int PA = BM / 8 / DW, PB = BN / 8 / DW;
+    static_assert(PA + PB <= 63, "outstanding copies must fit the 6-bit vmcnt");
+    constexpr int TILE_BYTES = 2 * STAGE;
+    constexpr int EPI_BYTES = EpiLayout<BM, BN, WGM, WGN>::BYTES;
+    __shared__ __attribute__((aligned(1024)))
+        int8_t smem[TILE_BYTES > EPI_BYTES ? TILE_BYTES : EPI_BYTES];
+
+    int tm, tn;
+    tile_coords(g, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wid = t >> 6;
+    const int wm = wid / WGN, wn = wid % WGN;
+    const int lr = lane & 31;
+    const bool copier = wid < DW;
+    const int cw = copier ? wid : 0;
+    const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds_addr_of(smem) + cw * PA * 8 * ROWB);
+    const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds_addr_of(smem) + BM * ROWB + cw * PB * 8 * ROWB);
+    // lane l of a copy covers row (l >> 3) of its 8-row group, physical slot l & 7
+    const int8_t* srcA[PA];
+    const int8_t* srcB[PB];
+#pragma unroll
+    for (int i = 0; i < PA; ++i) {
+        const int row = (cw * PA + i) * 8 + (lane >> 3);
+        const int kc = (lane & 7) ^ ((row >> 1) & 7);
+        srcA[i] = g.A + (size_t)min(m0 + row, g.M - 1) * g.K + 16 * kc;
+    }
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+        const int row = (cw * PB + i) * 8 + (lane >> 3);
+        const int kc = (lane & 7) ^ ((row >> 1) & 7);
+        srcB[i] = g.Bp + (size_t)min(n0 + row, g.N - 1) * g.K + 16 * kc;
+    }
+    const int KT = g.K / ROWB;
+    auto issue = [&](int buf, int kt) {
+        if (!copier) return;
+        const int k0 = kt * ROWB;
+#pragma unroll
+        for (int i = 0; i < PA; ++i) dma16(srcA[i] + k0, lds_a + buf * STAGE + i * 8 * ROWB);
+#pragma unroll
+        for (int i = 0; i < PB; ++i) dma16(srcB[i] + k0, lds_b + buf * STAGE + i * 8 * ROWB);
+    };
+
+    v16i acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    const uint32_t axr = g.a_xor;
+    v4i fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+    // fragments of 32-wide K step q (0..3) of a stage
+    auto read_q = [&](int stage, int q, v4i (&fa)[TI], v4i (&fb)[TJ]) {
+        const int8_t* sa = smem + stage * STAGE;
+        const int8_t* sb = sa + BM * ROWB;
+        const int kc = q * 2 + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int row = wm * WM + i * 32 + lr;
+            fa[i] = *reinterpret_cast<const v4i*>(sa + row * ROWB + 16 * (kc ^ ((row >> 1) & 7)));
+        }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int row = wn * WN + j * 32 + lr;
+            fb[j] = *reinterpret_cast<const v4i*>(sb + row * ROWB + 16 * (kc ^ ((row >> 1) & 7)));
+        }
+    };
+    auto mfma_q = [&](const v4i (&fa)[TI], const v4i (&fb)[TJ]) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const v4i a = fa[i] ^ (int)axr;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, fb[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    issue(0, 0);
+    issue(1, min(1, KT - 1));
+    wait_vmcnt<PA + PB>();  // stage 0 has landed
+    __syncthreads();
+    read_q(0, 0, fa0, fb0);
+    // Per stage: the reads of K step q+1 are issued before the MFMAs of step q; between
+    // steps 2 and 3 every wave waits for its copies of stage kt+1 and the barrier frees
+    // stage kt's buffer (its last fragments are in registers) for the copies of stage kt+2.
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        read_q(cur, 1, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_q(fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        read_q(cur, 2, fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_q(fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        read_q(cur, 3, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_q(fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<0>();   // this wave's copies of stage kt+1
+        __syncthreads();   // everyone's; stage kt is fully read
+        issue(cur, min(kt + 2, KT - 1));
+        if (kt + 1 < KT) read_q(cur ^ 1, 0, fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_q(fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();  // all copies landed and all fragment reads done: LDS is free
+    float mn = 0.0f, mx = 0.0f;
+    gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0, mn, mx);
+    if (OUT == OUT_F32 && g.part) icx::block_range_store<64 * WGM * WGN>(mn, mx, g.part);
+}
+
 // ---- main loop C: persistent producer / consumer (K % 64 == 0, column-only epilogue) ----
 // One block per CU slot loops over tiles (virtual tile ids blockIdx.x, +gridDim.x, ...,
 // mapped XCD-contiguous like tile_coords).  The K steps of all of a block's tiles form
@@ -962,10 +1097,18 @@ void launch_dma(int out_kind, int ch, unsigned blocks, hipStream_t s, const Gemm
 }
 
 // The 256x256 tile is only instantiated for int32 output and binary column chains (its
-// register budget has no room for the general or GELU epilogues).
+// register budget has no room for the general or GELU epilogues).  K % 128 == 0 takes the
+// 128-byte-row main loop.
 template <int WGM, int WGN, int NS>
 void launch_dma_big(int out_kind, unsigned blocks, hipStream_t s, const GemmArgs& g) {
     const dim3 grid(blocks), block(64 * WGM * WGN);
+    if (g.K % 128 == 0) {
+        if (out_kind == OUT_I32)
+            hipLaunchKernelGGL((gemm_i8_dma128_kernel<OUT_I32, CH_GENERAL>), grid, dim3(512), 0, s, g);
+        else
+            hipLaunchKernelGGL((gemm_i8_dma128_kernel<OUT_F32, CH_COL>), grid, dim3(512), 0, s, g);
+        return;
+    }
     if (out_kind == OUT_I32)
         hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 256, WGM, WGN, NS, OUT_I32, CH_GENERAL>), grid, block, 0, s, g);
     else

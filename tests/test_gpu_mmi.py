@@ -181,3 +181,20 @@ def test_persistent_kernel_encoder_ffn_down_shape():
     np.testing.assert_array_equal(got.astype(np.int64), _exact_f64(a, b, azp, bzp))
     for r in (0, 2049, 4095):
         assert np.array_equal(got[r:r + 1], oracle.matmul_integer(a[r:r + 1], b, azp, bzp))
+
+
+# At least 512 tiles of 256x256 take the large-tile kernels: K % 128 == 0 the 128-byte-row
+# main loop, K % 128 == 64 the 64-byte-row one.  Ragged M / N exercise the clamped rows.
+@pytest.mark.parametrize("K", [256, 320])
+@pytest.mark.parametrize("adt,bdt", [(np.uint8, np.int8), (np.int8, np.uint8)])
+def test_large_tile_kernels_ragged(K, adt, bdt):
+    rng = np.random.default_rng(31 + K)
+    M, N = 8000, 4100
+    a = rng.integers(np.iinfo(adt).min, np.iinfo(adt).max + 1, (M, K)).astype(adt)
+    b = rng.integers(np.iinfo(bdt).min, np.iinfo(bdt).max + 1, (K, N)).astype(bdt)
+    azp = np.array(rng.integers(np.iinfo(adt).min, np.iinfo(adt).max + 1), adt)
+    bzp = np.array(rng.integers(np.iinfo(bdt).min, np.iinfo(bdt).max + 1), bdt)
+    got = gpu_mmi(a, b, azp, bzp, packed=True)
+    np.testing.assert_array_equal(got.astype(np.int64), _exact_f64(a, b, azp, bzp))
+    for r in (0, 255, 256, 4001, M - 1):
+        assert np.array_equal(got[r:r + 1], oracle.matmul_integer(a[r:r + 1], b, azp, bzp)), r
