@@ -31,6 +31,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxBlocks = 1024;
+constexpr int kU = 8;  // float4 loads per lane in flight in the streaming loops
 
 struct alignas(16) DqlParams {
     double s;     // f64 scale (0 for the constant-input sentinel)
@@ -203,16 +204,17 @@ dql_minmax_kernel(const float* __restrict__ x, size_t units, size_t unit, size_t
     if (vec) {
         const float4* x4 = reinterpret_cast<const float4*>(x);
         const size_t b4 = sl.e0 / 4, end4 = b4 + (sl.e1 - sl.e0) / 4;
-        size_t i = b4 + t;
-        for (; i + 3 * kThreads < end4; i += 4 * kThreads) {
-            const float4 a = x4[i], b = x4[i + kThreads], c = x4[i + 2 * kThreads],
-                         d = x4[i + 3 * kThreads];
-            acc4(a, mn, mx);
-            acc4(b, mn, mx);
-            acc4(c, mn, mx);
-            acc4(d, mn, mx);
+        // kU float4 per lane requested before any is reduced (128 B per lane in flight); the
+        // last batch is guarded per load rather than walked one load at a time.  A skipped
+        // load reads as 0.0, which never moves a range that starts at (0, 0).
+        for (size_t i = b4 + t; i < end4; i += kU * kThreads) {
+            float4 v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                v[u] = i + u * kThreads < end4 ? x4[i + u * kThreads] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) acc4(v[u], mn, mx);
         }
-        for (; i < end4; i += kThreads) acc4(x4[i], mn, mx);
         scalar_from = end4 * 4;
     }
     for (size_t j = scalar_from + t; j < sl.e1; j += kThreads) acc_minmax(x[j], mn, mx);
@@ -234,31 +236,28 @@ dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size
         uint32_t* y4 = reinterpret_cast<uint32_t*>(y);
         const size_t b4 = sl.e0 / 4, end4 = b4 + (sl.e1 - sl.e0) / 4;
         size_t i = b4 + t;
-        // the lane's first four float4 are requested before the partials are folded, so
-        // the fold's loads and barriers overlap them
-        float4 v0[4];
+        // the lane's first kU float4 are requested before the partials are folded, so the
+        // fold's loads and barriers overlap them; every batch is guarded per element, so a
+        // short last batch still has all its loads in flight at once
+        float4 v[kU];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (i + j * kThreads < end4) v0[j] = x4[i + j * kThreads];
+        for (int j = 0; j < kU; ++j)
+            if (i + j * kThreads < end4) v[j] = x4[i + j * kThreads];
         const DqlParams p = fold_partials(part, G);
         if (blockIdx.x == 0 && threadIdx.x == 0) {
             *y_scale = (float)p.s;
             *y_zp = (uint8_t)p.zp;
         }
-        if (i + 3 * kThreads < end4) {
+        while (true) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) y4[i + j * kThreads] = quant4(v0[j], p);
-            i += 4 * kThreads;
+            for (int j = 0; j < kU; ++j)
+                if (i + j * kThreads < end4) y4[i + j * kThreads] = quant4(v[j], p);
+            i += kU * kThreads;
+            if (i >= end4) break;
+#pragma unroll
+            for (int j = 0; j < kU; ++j)
+                if (i + j * kThreads < end4) v[j] = x4[i + j * kThreads];
         }
-        for (; i + 3 * kThreads < end4; i += 4 * kThreads) {
-            const float4 a = x4[i], b = x4[i + kThreads], c = x4[i + 2 * kThreads],
-                         d = x4[i + 3 * kThreads];
-            y4[i] = quant4(a, p);
-            y4[i + kThreads] = quant4(b, p);
-            y4[i + 2 * kThreads] = quant4(c, p);
-            y4[i + 3 * kThreads] = quant4(d, p);
-        }
-        for (; i < end4; i += kThreads) y4[i] = quant4(x4[i], p);
         for (size_t j = end4 * 4 + t; j < sl.e1; j += kThreads) y[j] = (uint8_t)quant1(x[j], p);
         return;
     }

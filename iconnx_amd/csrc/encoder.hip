@@ -13,6 +13,7 @@
 //       activations, with fp32 MFMA (v_mfma_f32_32x32x2f32) and the softmax in registers.
 #include "icx_common.hpp"
 #include "internal.hpp"
+#include <cmath>
 
 #include <algorithm>
 
@@ -314,10 +315,13 @@ struct AttnArgs {
     int scale_div;  // 1: x / scale, 0: x * scale
     int scale_q;    // 1: applied to Q before the product, 0: to the scores
     float2* part;   // DQL range partials of out, one per block, or null
+    float recip;      // 1 / scale when that is exact (a power of two), so x / scale == x * recip
+    int recip_exact;  // bit for bit, and the division becomes a multiplication
 };
 
 __device__ __forceinline__ float apply_scale(float x, const AttnArgs& a) {
-    return a.scale_div ? __fdiv_rn(x, a.scale) : __fmul_rn(x, a.scale);
+    if (!a.scale_div) return __fmul_rn(x, a.scale);
+    return a.recip_exact ? __fmul_rn(x, a.recip) : __fdiv_rn(x, a.scale);
 }
 
 __device__ __forceinline__ float f4c(const float4& v, int e) {
@@ -400,20 +404,24 @@ attention_kernel(AttnArgs a) {
             m = fmaxf(m, x);
         }
     m = fmaxf(m, __shfl_xor(m, 32, 64));
+    // hardware exp2 and one reciprocal per row: within a few ulp of expf and of e / sum,
+    // far inside the attention's tolerance, at a fraction of the VALU work (the softmax
+    // otherwise costs about half as many cycles as this wave's MFMAs)
     float sum = 0.0f;
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float e = expf(__fsub_rn(st[jt][r], m));
+            const float e = __expf(__fsub_rn(st[jt][r], m));
             st[jt][r] = e;
             sum = __fadd_rn(sum, e);
         }
     sum = __fadd_rn(sum, __shfl_xor(sum, 32, 64));
+    const float inv = __fdiv_rn(1.0f, sum);
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) st[jt][r] = __fdiv_rn(st[jt][r], sum);
+        for (int r = 0; r < 16; ++r) st[jt][r] = __fmul_rn(st[jt][r], inv);
 
     // ctx = P V: A = P straight from the S^T registers, B = V rows from LDS
     v16f o2[2];
@@ -573,7 +581,17 @@ int icx::attention_f32(hipStream_t s, const float* q, const float* k, const floa
     if (B * H > 0x7fffffff) ICX_FAIL(ICX_ERR_SHAPE, "Attention: too many (batch, head) pairs");
     float2* pp = (part && B * H <= (size_t)icx::kMaxRangeParts) ? part : nullptr;
     AttnArgs a{q, k, v, out, (int)S, (int)H, (int64_t)ldq, (int64_t)ldk, (int64_t)ldv, (int64_t)ldo,
-               scale, scale_div ? 1 : 0, scale_q ? 1 : 0, pp};
+               scale, scale_div ? 1 : 0, scale_q ? 1 : 0, pp, 0.0f, 0};
+    {
+        // a power-of-two scale whose reciprocal is a normal float: x / scale == x * (1 / scale)
+        int e = 0;
+        const float m = std::frexp(scale, &e);
+        const float r = 1.0f / scale;
+        if (m == 0.5f && std::isnormal(scale) && std::isnormal(r)) {
+            a.recip = r;
+            a.recip_exact = 1;
+        }
+    }
     static bool smem_set = false;  // 66 KB of dynamic LDS is above the default limit
     if (!smem_set) {
         ICX_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
