@@ -97,7 +97,8 @@ class Runner:
             self.keep += k
             self.a_dtype, self.b_dtype = ICX_U8, ICX_I8
             self.ops_count = 2.0 * self.M * self.N * self.K
-            self.dominant = "gemm_i8_dma_kernel"
+            # >= 512 tiles of 256x256 with K % 128 == 0 (cfg4) take the 128-byte-row kernel
+            self.dominant = "gemm_i8_dma128_kernel" if cfg == "cfg4" else "gemm_i8_dma_kernel"
         elif cfg == "cfg5a":
             self.M, self.K = d["a"].shape
             self.N = d["b"].shape[1]
@@ -114,7 +115,7 @@ class Runner:
             self.keep += k
             self.a_dtype, self.b_dtype = ICX_U8, ICX_I8
             self.ops_count = 2.0 * self.M * self.N * self.K
-            self.dominant = "gemm_i8_dma_kernel"
+            self.dominant = "gemm_i8_dma128_kernel"
         else:  # cfg5b, copy
             self.x = dev(d["x"])
             self.M, self.N = d["x"].shape

@@ -284,36 +284,60 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
     }
     const Slice sl = slice_of(rows, 1, 0);  // a range of rows
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    for (size_t r = sl.e0 + wid; r < sl.e1; r += kThreads / 64) {
+    constexpr size_t kWaves = kThreads / 64;
+    if (vec) {
+        // Two rows per wave at a time (r and r + kWaves), four float4 of each per lane in
+        // flight, so a wave never waits on a single row's loads.
+        const size_t n4 = row_len / 4;
+        for (size_t r = sl.e0 + wid; r < sl.e1; r += 2 * kWaves) {
+            const size_t r2 = r + kWaves;
+            const bool two = r2 < sl.e1;
+            const float4* xa = reinterpret_cast<const float4*>(x + r * row_len);
+            const float4* xb = reinterpret_cast<const float4*>(x + (two ? r2 : r) * row_len);
+            uint32_t* ya = reinterpret_cast<uint32_t*>(y + r * row_len);
+            uint32_t* yb = reinterpret_cast<uint32_t*>(y + (two ? r2 : r) * row_len);
+            uint32_t sa = 0, sb = 0;
+            for (size_t i = lane; i < n4; i += 4 * 64) {
+                float4 va[4], vb[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (i + 64 * j < n4) va[j] = xa[i + 64 * j];
+                    if (two && i + 64 * j < n4) vb[j] = xb[i + 64 * j];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (i + 64 * j < n4) {
+                        const uint32_t q = quant4(va[j], p);
+                        ya[i + 64 * j] = q;
+                        sa += bytesum4(q);
+                    }
+                    if (two && i + 64 * j < n4) {
+                        const uint32_t q = quant4(vb[j], p);
+                        yb[i + 64 * j] = q;
+                        sb += bytesum4(q);
+                    }
+                }
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                sa += __shfl_xor(sa, off, 64);
+                sb += __shfl_xor(sb, off, 64);
+            }
+            if (lane == 0) {
+                rowsum[r] = (int32_t)sa;
+                if (two) rowsum[r2] = (int32_t)sb;
+            }
+        }
+        return;
+    }
+    for (size_t r = sl.e0 + wid; r < sl.e1; r += kWaves) {
         const float* xr = x + r * row_len;
         uint8_t* yr = y + r * row_len;
         uint32_t s = 0;
-        if (vec) {
-            const float4* x4 = reinterpret_cast<const float4*>(xr);
-            uint32_t* y4 = reinterpret_cast<uint32_t*>(yr);
-            const size_t n4 = row_len / 4;
-            size_t i = lane;
-            for (; i + 3 * 64 < n4; i += 4 * 64) {
-                const float4 a = x4[i], b = x4[i + 64], c = x4[i + 128], d = x4[i + 192];
-                const uint32_t qa = quant4(a, p), qb = quant4(b, p), qc = quant4(c, p),
-                               qd = quant4(d, p);
-                y4[i] = qa;
-                y4[i + 64] = qb;
-                y4[i + 128] = qc;
-                y4[i + 192] = qd;
-                s += bytesum4(qa) + bytesum4(qb) + bytesum4(qc) + bytesum4(qd);
-            }
-            for (; i < n4; i += 64) {
-                const uint32_t q = quant4(x4[i], p);
-                y4[i] = q;
-                s += bytesum4(q);
-            }
-        } else {
-            for (size_t i = lane; i < row_len; i += 64) {
-                const uint32_t q = quant1(xr[i], p);
-                yr[i] = (uint8_t)q;
-                s += q;
-            }
+        for (size_t i = lane; i < row_len; i += 64) {
+            const uint32_t q = quant1(xr[i], p);
+            yr[i] = (uint8_t)q;
+            s += q;
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
