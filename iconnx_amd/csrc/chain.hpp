@@ -5,11 +5,9 @@
 //
 // Two evaluation forms:
 //  * apply_chain      — general: every operand fetched per element (any broadcast kind);
-//  * load_col_operands + apply_loaded — when every factor is a scalar or a [cols] vector
-//    (the dequant-scale / bias / per-channel chain case): the operands of one column are
-//    fetched once, as independent loads issued together, and the per-element work is pure
-//    arithmetic.  Loops run over the fixed ICX_MAX_CHAIN bound with predication so the
-//    operand array stays in registers.
+//  * load_col_operands + run_chain4 (op-major, over chain_codes) — when every factor is a
+//    scalar or a [cols] vector (the dequant-scale / bias / per-channel chain case): the
+//    operands of one column are fetched once and the per-element work is pure arithmetic.
 #pragma once
 
 #include "icx_common.hpp"
@@ -39,9 +37,10 @@ __device__ __forceinline__ bool op_takes_operand(int op) { return op <= ICX_OP_D
 // division and a library expf (the GELU epilogue of the FFN-up projection runs this for
 // every output element).
 __device__ __forceinline__ float erf_ref(float x) {
-    const float sign = (x != x) ? x : (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : copysignf(1.0f, x)));
+    // x.signum() for every non-NaN x (+-1, also for +-0); NaN is returned as is below
+    const float sign = copysignf(1.0f, x);
     // |x| >= 10 gives exactly +-1 either way (e^-100 is 0 in f32); the clamp keeps the
-    // Newton step finite for |x| = inf (NaN still propagates through `sign`).
+    // Newton step finite for |x| = inf.
     const float a = fminf(fabsf(x), 16.0f);
     const float d = __fadd_rn(1.0f, __fmul_rn(0.3275911f, a));
     const float r0 = __builtin_amdgcn_rcpf(d);
@@ -52,7 +51,7 @@ __device__ __forceinline__ float erf_ref(float x) {
     p = __fadd_rn(__fmul_rn(p, t), 0.2548296f);
     const float e = __expf(__fmul_rn(-a, a));
     const float y = __fsub_rn(1.0f, __fmul_rn(__fmul_rn(p, t), e));
-    return __fmul_rn(sign, y);
+    return (x != x) ? x : __fmul_rn(sign, y);
 }
 
 __device__ __forceinline__ float chain_operand(const icx_chain_op& op, size_t r, size_t c,
@@ -100,39 +99,47 @@ __device__ __forceinline__ float col_factor(const float* p, int kind, size_t c) 
     return kind == ICX_BCAST_SCALAR ? p[0] : p[c];
 }
 
+// x / d whose only reader is the next step's Erf (the erf-GELU's x / sqrt(2)).  The op-major
+// evaluators (run_chain4 over chain_codes) run it as x * RN(1/d): the quotient then differs
+// from the IEEE one by at most one ulp, which moves erf by at most max|erf'(t) t| * 2^-23
+// < 4e-8 — inside erf's own tolerance — and saves a correctly rounded division per element.
+// The per-element evaluator (apply_chain) keeps the division.
+__host__ __device__ inline bool div_feeds_erf(const icx_chain& ch, int k) {
+    return k + 1 < ch.n_ops && ch.ops[k].op == ICX_OP_DIV && !ch.ops[k].operand_is_lhs &&
+           ch.ops[k + 1].op == ICX_OP_ERF;
+}
+
+// Operand of step k at column c as the op-major evaluators consume it: the factor product,
+// or its correctly rounded reciprocal for a division that feeds an Erf (see above).
+__device__ __forceinline__ float col_operand(const icx_chain& ch, int k, size_t c) {
+    const icx_chain_op& op = ch.ops[k];
+    float a = col_factor(op.p0, op.kind0, c);
+    if (op.p1) a = __fmul_rn(a, col_factor(op.p1, op.kind1, c));
+    return div_feeds_erf(ch, k) ? __fdiv_rn(1.0f, a) : a;
+}
+
+// The operands of column c for the op-major evaluators (run_chain4 with chain_codes).
 __device__ __forceinline__ void load_col_operands(const icx_chain& ch, size_t c,
                                                   float (&o)[ICX_MAX_CHAIN]) {
 #pragma unroll
-    for (int i = 0; i < ICX_MAX_CHAIN; ++i) {
-        if (i < ch.n_ops && op_takes_operand(ch.ops[i].op)) {
-            const icx_chain_op& op = ch.ops[i];
-            float a = col_factor(op.p0, op.kind0, c);
-            if (op.p1) a = __fmul_rn(a, col_factor(op.p1, op.kind1, c));
-            o[i] = a;
-        } else {
-            o[i] = 0.0f;
-        }
-    }
+    for (int i = 0; i < ICX_MAX_CHAIN; ++i)
+        o[i] = (i < ch.n_ops && op_takes_operand(ch.ops[i].op)) ? col_operand(ch, i, c) : 0.0f;
 }
 
-__device__ __forceinline__ float apply_loaded(const icx_chain& ch, float v,
-                                              const float (&o)[ICX_MAX_CHAIN]) {
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < ICX_MAX_CHAIN; ++i)
-        if (i < ch.n_ops) v = step_one(ch.ops[i], v, o[i], s);
-    return v;
-}
 
 // ---- op-major evaluation over a register block of float4 values ------------------------
 // The op codes of a chain packed 4 bits per op: bits [2:0] = ICX_OP_*, bit 3 = operand on
 // the left.  One uniform switch per op, then straight-line IEEE ops over every value the
 // lane holds — no per-element branching.  `opnd(k)` returns the float4 operand of op k for
 // the lane's 4 columns (unused by the operand-free ops).
+// A division that feeds an Erf is coded as a multiplication: its staged operand is the
+// reciprocal (col_operand).
 __host__ __device__ inline uint32_t chain_codes(const icx_chain& ch) {
     uint32_t c = 0;
-    for (int i = 0; i < ch.n_ops; ++i)
-        c |= (uint32_t)((ch.ops[i].op & 7) | (ch.ops[i].operand_is_lhs ? 8 : 0)) << (4 * i);
+    for (int i = 0; i < ch.n_ops; ++i) {
+        const int op = div_feeds_erf(ch, i) ? ICX_OP_MUL : ch.ops[i].op;
+        c |= (uint32_t)((op & 7) | (ch.ops[i].operand_is_lhs ? 8 : 0)) << (4 * i);
+    }
     return c;
 }
 

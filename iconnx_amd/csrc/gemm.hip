@@ -187,13 +187,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
 #pragma unroll
         for (int k = 0; k < ICX_MAX_CHAIN; ++k) {
             if (k < g.chain.n_ops && icx::op_takes_operand(g.chain.ops[k].op)) {
-                const icx_chain_op& op = g.chain.ops[k];
-                for (int c = t; c < BN; c += NT) {
-                    const int col = min(n0 + c, g.N - 1);
-                    float a = icx::col_factor(op.p0, op.kind0, col);
-                    if (op.p1) a = __fmul_rn(a, icx::col_factor(op.p1, op.kind1, col));
-                    sop[k * BN + c] = a;
-                }
+                for (int c = t; c < BN; c += NT) sop[k * BN + c] = icx::col_operand(g.chain, k, min(n0 + c, g.N - 1));
             }
         }
     }
@@ -225,47 +219,53 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
         }
         __syncthreads();
         constexpr int NQ = 32 / RPI;  // float4 values per lane in this slab
-        float4 v[NQ];
+        // the erf-GELU chain also keeps a saved copy of every value: run it on half the slab
+        // at a time so the values stay in registers at three blocks per CU
+        constexpr int QC = (CH == CH_COL_EXT && NQ > 4) ? NQ / 2 : NQ;
 #pragma unroll
-        for (int q = 0; q < NQ; ++q)
-            v[q] = *reinterpret_cast<const float4*>(&stage[(q * RPI + rsub) * SROW + cc]);
-        if (OUT == OUT_F32) {
-            if constexpr (CH != CH_GENERAL) {
-                icx::run_chain4<CH == CH_COL_EXT ? 2 : 0>(g.codes, g.chain.n_ops, v, [&](int k) {
-                    return *reinterpret_cast<const float4*>(&sop[k * BN + wn * WN + cc]);
-                });
-            } else {
+        for (int h = 0; h < NQ; h += QC) {
+            float4 v[QC];
 #pragma unroll
-                for (int q = 0; q < NQ; ++q) {
-                    const int grow = min(rbase + q * RPI + rsub, g.M - 1);
-                    float* w = reinterpret_cast<float*>(&v[q]);
+            for (int q = 0; q < QC; ++q)
+                v[q] = *reinterpret_cast<const float4*>(&stage[((h + q) * RPI + rsub) * SROW + cc]);
+            if (OUT == OUT_F32) {
+                if constexpr (CH != CH_GENERAL) {
+                    icx::run_chain4<CH == CH_COL_EXT ? 2 : 0>(g.codes, g.chain.n_ops, v, [&](int k) {
+                        return *reinterpret_cast<const float4*>(&sop[k * BN + wn * WN + cc]);
+                    });
+                } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        w[e] = icx::apply_chain(g.chain, w[e], grow, min(gcol + e, g.N - 1), g.N);
+                    for (int q = 0; q < QC; ++q) {
+                        const int grow = min(rbase + (h + q) * RPI + rsub, g.M - 1);
+                        float* w = reinterpret_cast<float*>(&v[q]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            w[e] = icx::apply_chain(g.chain, w[e], grow, min(gcol + e, g.N - 1), g.N);
+                    }
                 }
             }
-        }
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-            const int grow = rbase + q * RPI + rsub;
-            if (grow >= g.M || gcol >= g.N) continue;
-            const size_t off = (size_t)grow * ov.ld + (gcol - ov.c0);
-            if (vec_out && gcol + 3 < g.N) {
-                icx::store_nt(reinterpret_cast<float4*>(ov.base + off), v[q]);
-                if (rng) {
-                    icx::range_acc(v[q].x, mn, mx);
-                    icx::range_acc(v[q].y, mn, mx);
-                    icx::range_acc(v[q].z, mn, mx);
-                    icx::range_acc(v[q].w, mn, mx);
-                }
-            } else {
-                const float* w = reinterpret_cast<const float*>(&v[q]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (gcol + e < g.N) {
-                        ov.base[off + e] = w[e];
-                        if (rng) icx::range_acc(w[e], mn, mx);
+            for (int q = 0; q < QC; ++q) {
+                const int grow = rbase + (h + q) * RPI + rsub;
+                if (grow >= g.M || gcol >= g.N) continue;
+                const size_t off = (size_t)grow * ov.ld + (gcol - ov.c0);
+                if (vec_out && gcol + 3 < g.N) {
+                    icx::store_nt(reinterpret_cast<float4*>(ov.base + off), v[q]);
+                    if (rng) {
+                        icx::range_acc(v[q].x, mn, mx);
+                        icx::range_acc(v[q].y, mn, mx);
+                        icx::range_acc(v[q].z, mn, mx);
+                        icx::range_acc(v[q].w, mn, mx);
                     }
+                } else {
+                    const float* w = reinterpret_cast<const float*>(&v[q]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (gcol + e < g.N) {
+                            ov.base[off + e] = w[e];
+                            if (rng) icx::range_acc(w[e], mn, mx);
+                        }
+                }
             }
         }
     }
@@ -838,13 +838,8 @@ gemm_i8_stream_kernel(GemmArgs g) {
             if (OUT == OUT_F32) {
 #pragma unroll
                 for (int k = 0; k < ICX_MAX_CHAIN; ++k) {
-                    float a = 0.0f;
-                    if (k < g.chain.n_ops && icx::op_takes_operand(g.chain.ops[k].op)) {
-                        const icx_chain_op& op = g.chain.ops[k];
-                        a = icx::col_factor(op.p0, op.kind0, col);
-                        if (op.p1) a = __fmul_rn(a, icx::col_factor(op.p1, op.kind1, col));
-                    }
-                    ov[j][k] = a;
+                    ov[j][k] = (k < g.chain.n_ops && icx::op_takes_operand(g.chain.ops[k].op))
+                                   ? icx::col_operand(g.chain, k, col) : 0.0f;
                 }
             }
         }
