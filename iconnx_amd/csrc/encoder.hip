@@ -287,7 +287,7 @@ matmul_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, int 
 
 // ---- fused self-attention, S <= 128, D == 64 --------------------------------------------
 // One block per (batch, head), 4 waves; wave w owns query rows [32w, 32w + 32).  K and V
-// sit in LDS (66 KB, so two blocks share a CU); each lane keeps its Q fragment in registers.
+// sit in LDS (67 KB, V transposed; two blocks share a CU); each lane keeps its Q fragment in registers.
 //   S^T = K Q^T (*|/) scale (or Q scaled first): 4 key tiles of 32 x 32, contraction 64
 //   P = softmax over the keys, in registers
 //   ctx = P V: 2 tiles of 32 x 32, contraction S
@@ -301,8 +301,9 @@ matmul_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, int 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int ATT_S = 128, ATT_D = 64;
-constexpr int K_STRIDE = ATT_D + 4;  // floats per LDS row of K: 16-byte fragment reads conflict-free
-constexpr int V_STRIDE = ATT_D;      // V is read one 128-byte row segment per half-wave
+constexpr int K_STRIDE = ATT_D + 4;   // floats per LDS row of K: 16-byte fragment reads conflict-free
+constexpr int VT_STRIDE = ATT_S + 4;  // V is stored transposed, [dim][key]: the B operands of four
+                                      // consecutive P V steps are one 16-byte read, conflict-free
 
 struct AttnArgs {
     const float* q;
@@ -331,8 +332,8 @@ __device__ __forceinline__ float f4c(const float4& v, int e) {
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 attention_kernel(AttnArgs a) {
     extern __shared__ float smem[];
-    float* sk = smem;                     // [128][K_STRIDE]
-    float* sv = smem + ATT_S * K_STRIDE;  // [128][V_STRIDE]
+    float* sk = smem;                      // [128][K_STRIDE]
+    float* svt = smem + ATT_S * K_STRIDE;  // [64][VT_STRIDE], V transposed
     const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
     const int S = a.S;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -361,7 +362,10 @@ attention_kernel(AttnArgs a) {
     for (int u = 0; u < 8; ++u) {
         const int r = u * 16 + (t >> 4);
         *reinterpret_cast<float4*>(sk + r * K_STRIDE + c4) = kr[u];
-        *reinterpret_cast<float4*>(sv + r * V_STRIDE + c4) = vr[u];
+        svt[(c4 + 0) * VT_STRIDE + r] = vr[u].x;
+        svt[(c4 + 1) * VT_STRIDE + r] = vr[u].y;
+        svt[(c4 + 2) * VT_STRIDE + r] = vr[u].z;
+        svt[(c4 + 3) * VT_STRIDE + r] = vr[u].w;
     }
     if (a.scale_q) {
 #pragma unroll
@@ -374,21 +378,26 @@ attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // S^T: A = K (lane = key), B = Q^T (lane = query)
+    // S^T: A = K (lane = key), B = Q^T (lane = query).  The K fragments of key tile jt+1
+    // are read from LDS while the MFMAs of tile jt run.
     v16f st[4];
+    float4 kf[2][8];
+    auto read_k = [&](int jt, float4 (&f)[8]) {
+        const float* kp = sk + (32 * jt + lr) * K_STRIDE + 32 * lh;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) f[u] = *reinterpret_cast<const float4*>(kp + 4 * u);
+    };
+    read_k(0, kf[0]);
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
+        if (jt + 1 < 4) read_k(jt + 1, kf[(jt + 1) & 1]);
 #pragma unroll
         for (int r = 0; r < 16; ++r) st[jt][r] = 0.0f;
-        const float* kp = sk + (32 * jt + lr) * K_STRIDE + 32 * lh;
-        float4 kf[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) kf[u] = *reinterpret_cast<const float4*>(kp + 4 * u);
 #pragma unroll
         for (int u = 0; u < 8; ++u)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                st[jt] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4c(kf[u], e), f4c(qr[u], e), st[jt], 0, 0, 0);
+                st[jt] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4c(kf[jt & 1][u], e), f4c(qr[u], e), st[jt], 0, 0, 0);
     }
 
     // softmax of row qi over its S keys: 64 here, 64 in lane ^ 32
@@ -423,7 +432,9 @@ attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) st[jt][r] = __fmul_rn(st[jt][r], inv);
 
-    // ctx = P V: A = P straight from the S^T registers, B = V rows from LDS
+    // ctx = P V: A = P straight from the S^T registers, B = V from LDS.  Step (jt, r)
+    // contracts over key 32 jt + 8 (r / 4) + 4 lh + r % 4 (this half-wave's key), so the B
+    // operands of r = 4 rq .. 4 rq + 3 are four consecutive keys of V^T row 32 dt + lr.
     v16f o2[2];
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
@@ -432,12 +443,17 @@ attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = 32 * jt + 8 * (r / 4) + 4 * lh + (r % 4);
-            const float* vp = sv + key * V_STRIDE + lr;
+        for (int rq = 0; rq < 4; ++rq) {
+            float4 vq[2];
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt)
-                o2[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(st[jt][r], vp[32 * dt], o2[dt], 0, 0, 0);
+                vq[dt] = *reinterpret_cast<const float4*>(svt + (32 * dt + lr) * VT_STRIDE + 32 * jt +
+                                                          8 * rq + 4 * lh);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt)
+                    o2[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(st[jt][4 * rq + e], f4c(vq[dt], e), o2[dt], 0, 0, 0);
         }
     float mn = 0.0f, mx = 0.0f;  // DQL range of out (when a.part is given)
 #pragma unroll
@@ -454,7 +470,7 @@ attention_kernel(AttnArgs a) {
     if (a.part) icx::block_range_store<kThreads>(mn, mx, a.part);
 }
 
-constexpr size_t kAttnSmem = (size_t)ATT_S * (K_STRIDE + V_STRIDE) * sizeof(float);
+constexpr size_t kAttnSmem = ((size_t)ATT_S * K_STRIDE + (size_t)ATT_D * VT_STRIDE) * sizeof(float);
 
 unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
     size_t b = icx::cdiv(work, per_block);
@@ -592,7 +608,7 @@ int icx::attention_f32(hipStream_t s, const float* q, const float* k, const floa
             a.recip_exact = 1;
         }
     }
-    static bool smem_set = false;  // 66 KB of dynamic LDS is above the default limit
+    static bool smem_set = false;  // 67 KB of dynamic LDS is above the default limit
     if (!smem_set) {
         ICX_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
                                           hipFuncAttributeMaxDynamicSharedMemorySize,
