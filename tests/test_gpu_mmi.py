@@ -198,3 +198,18 @@ def test_large_tile_kernels_ragged(K, adt, bdt):
     np.testing.assert_array_equal(got.astype(np.int64), _exact_f64(a, b, azp, bzp))
     for r in (0, 255, 256, 4001, M - 1):
         assert np.array_equal(got[r:r + 1], oracle.matmul_integer(a[r:r + 1], b, azp, bzp)), r
+
+
+# 256x192 tiles (12 waves) when they give every CU at least one: N % 192 == 0, K % 128 == 0,
+# cdiv(M, 256) * N / 192 >= CUs; ragged M exercises the clamped rows.
+@pytest.mark.parametrize("M", [4000, 4100])
+def test_mid_tile_kernel_ragged(M):
+    rng = np.random.default_rng(37 + M)
+    K, N = 256, 3072
+    a = rng.integers(0, 256, (M, K)).astype(np.uint8)
+    b = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    azp, bzp = np.array(131, np.uint8), np.array(-3, np.int8)
+    got = gpu_mmi(a, b, azp, bzp, packed=True)
+    np.testing.assert_array_equal(got.astype(np.int64), _exact_f64(a, b, azp, bzp))
+    for r in (0, 255, 256, 3999, M - 1):
+        assert np.array_equal(got[r:r + 1], oracle.matmul_integer(a[r:r + 1], b, azp, bzp)), r
