@@ -206,17 +206,24 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
             rterm[r] = g.rowsum_raw ? (uint32_t)g.rowsum_raw[row] - aK : 0u;
         }
         __syncthreads();  // previous slab read back; column operands written
+        // without row sums (the weight zero point folded away) the row term is 0: a uniform
+        // branch drops its 32-bit multiply (a quarter-rate instruction) from every element
+        auto stage_slab = [&](bool with_rows) {
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
+            for (int j = 0; j < TJ; ++j) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int lrow = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const uint32_t v = (uint32_t)acc[i][j][r] + colterm[j] + colfac[j] * rterm[r];
-                float* dst = &stage[lrow * SROW + j * 32 + lr];
-                if (OUT == OUT_I32) *reinterpret_cast<int32_t*>(dst) = (int32_t)v;
-                else *dst = (float)(int32_t)v;  // Cast INT32 -> FLOAT, round to nearest even
+                for (int r = 0; r < 16; ++r) {
+                    const int lrow = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    uint32_t v = (uint32_t)acc[i][j][r] + colterm[j];
+                    if (with_rows) v += colfac[j] * rterm[r];
+                    float* dst = &stage[lrow * SROW + j * 32 + lr];
+                    if (OUT == OUT_I32) *reinterpret_cast<int32_t*>(dst) = (int32_t)v;
+                    else *dst = (float)(int32_t)v;  // Cast INT32 -> FLOAT, round to nearest even
+                }
             }
-        }
+        };
+        if (g.rowsum_raw) stage_slab(true);
+        else stage_slab(false);
         __syncthreads();
         constexpr int NQ = 32 / RPI;  // float4 values per lane in this slab
         // the erf-GELU chain also keeps a saved copy of every value: run it on half the slab
