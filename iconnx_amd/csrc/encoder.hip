@@ -286,24 +286,26 @@ matmul_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, int 
 }
 
 // ---- fused self-attention, S <= 128, D == 64 --------------------------------------------
-// One block per (batch, head), 4 waves; wave w owns query rows [32w, 32w + 32).  K and V
-// sit in LDS (67 KB, V transposed; two blocks share a CU); each lane keeps its Q fragment in registers.
-//   S^T = K Q^T (*|/) scale (or Q scaled first): 4 key tiles of 32 x 32, contraction 64
+// One block per (batch, head, half of the queries): 4 waves of 16 queries each, so the
+// 2 * B * H blocks give every CU three blocks (12 waves, three per SIMD) at the DistilBERT
+// shape.  K and then V pass through one 35 KB LDS region: K for S^T, V (transposed) for P V,
+// both held in registers from the start so the V load overlaps S^T.
+//   S^T = K Q^T (*|/) scale (or Q scaled first): 8 key tiles of 16 x 16, contraction 64
 //   P = softmax over the keys, in registers
-//   ctx = P V: 2 tiles of 32 x 32, contraction S
-// v_mfma_f32_32x32x2f32: A lane l = A[l % 32][l / 32], B lane l = B[l / 32][l % 32],
-// D register r of lane l = D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
-// Computing S^T rather than S leaves lane l with query l % 32 and, in register r of key tile
-// jt, key 32 jt + 8 (r / 4) + 4 (l / 32) + r % 4 (the other half-wave holds the row's other
-// keys).  That is exactly P's A-operand layout for the product with V when step (jt, r)
-// contracts over those keys, so P never leaves registers.  Each contraction visits its terms
-// in an order fixed for A and B alike (dims 32 (l / 32) + s; the keys above).
-typedef float v16f __attribute__((ext_vector_type(16)));
+//   ctx = P V: 4 tiles of 16 x 16, contraction S
+// v_mfma_f32_16x16x4f32: A lane l = A[l % 16][l / 16], B lane l = B[l / 16][l % 16],
+// D register r of lane l = D[4 (l / 16) + r][l % 16].
+// Step s of the S^T contraction gives lane-group g = l / 16 dimension 16 g + s, so each lane
+// reads its K row and Q row as 16 contiguous floats.  S^T leaves lane l with query l % 16
+// and, in register r of key tile t, key 16 t + 4 (l / 16) + r — exactly P's A-operand layout
+// for the P V step (t, r), whose 4-key contraction takes key 16 t + 4 g + r from group g, so P
+// never leaves registers; the B operands of steps r = 0..3 are four consecutive keys of V^T.
+typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int ATT_S = 128, ATT_D = 64;
-constexpr int K_STRIDE = ATT_D + 4;   // floats per LDS row of K: 16-byte fragment reads conflict-free
-constexpr int VT_STRIDE = ATT_S + 4;  // V is stored transposed, [dim][key]: the B operands of four
-                                      // consecutive P V steps are one 16-byte read, conflict-free
+constexpr int ATT_S = 128, ATT_D = 64, ATT_QB = 64;  // keys, head size, queries per block
+constexpr int K_STRIDE = ATT_D + 4;   // floats per LDS row of K: 16-byte reads conflict-free
+constexpr int VT_STRIDE = ATT_S + 4;  // V^T rows [dim][key]
+constexpr int ATT_LDS_FLOATS = ATT_S * K_STRIDE > ATT_D * VT_STRIDE ? ATT_S * K_STRIDE : ATT_D * VT_STRIDE;
 
 struct AttnArgs {
     const float* q;
@@ -318,6 +320,7 @@ struct AttnArgs {
     float2* part;   // DQL range partials of out, one per block, or null
     float recip;      // 1 / scale when that is exact (a power of two), so x / scale == x * recip
     int recip_exact;  // bit for bit, and the division becomes a multiplication
+    int qsplit;       // blocks per (batch, head): 2 when S > 64 (64 queries each), else 1
 };
 
 __device__ __forceinline__ float apply_scale(float x, const AttnArgs& a) {
@@ -329,20 +332,18 @@ __device__ __forceinline__ float f4c(const float4& v, int e) {
     return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
 }
 
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-attention_kernel(AttnArgs a) {
-    extern __shared__ float smem[];
-    float* sk = smem;                      // [128][K_STRIDE]
-    float* svt = smem + ATT_S * K_STRIDE;  // [64][VT_STRIDE], V transposed
-    const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
+__global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) float lds[ATT_LDS_FLOATS];
+    const int pair = blockIdx.x / a.qsplit, half = blockIdx.x % a.qsplit;
+    const int b = pair / a.H, h = pair % a.H;
     const int S = a.S;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int lr = lane & 31, lh = lane >> 5;
-    const int qi = 32 * w + lr;  // this lane's query row
+    const int lq = lane & 15, lg = lane >> 4;
+    const int qi = half * ATT_QB + 16 * w + lq;  // this lane's query row
 
-    // every load in flight at once: K and V of (b, h) (rows past S are zero), and this
-    // lane's Q fragment, dims [32 lh, 32 lh + 32) of row qi
-    float4 kr[8], vr[8], qr[8];
+    // every load in flight at once: K and V of (b, h) (rows past S are zero), and this lane's
+    // Q row segment, dims [16 lg, 16 lg + 16)
+    float4 kr[8], vr[8], qr[4];
     const int c4 = (t & 15) * 4;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -354,22 +355,16 @@ attention_kernel(AttnArgs a) {
             vr[u] = *reinterpret_cast<const float4*>(a.v + row * a.ldv + h * ATT_D + c4);
         }
     }
-    const float* qp = a.q + ((size_t)b * S + qi) * a.ldq + h * ATT_D + 32 * lh;
+    const float* qp = a.q + ((size_t)b * S + qi) * a.ldq + h * ATT_D + 16 * lg;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 4; ++u)
         qr[u] = qi < S ? *reinterpret_cast<const float4*>(qp + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int r = u * 16 + (t >> 4);
-        *reinterpret_cast<float4*>(sk + r * K_STRIDE + c4) = kr[u];
-        svt[(c4 + 0) * VT_STRIDE + r] = vr[u].x;
-        svt[(c4 + 1) * VT_STRIDE + r] = vr[u].y;
-        svt[(c4 + 2) * VT_STRIDE + r] = vr[u].z;
-        svt[(c4 + 3) * VT_STRIDE + r] = vr[u].w;
-    }
+    for (int u = 0; u < 8; ++u)
+        *reinterpret_cast<float4*>(lds + (u * 16 + (t >> 4)) * K_STRIDE + c4) = kr[u];
     if (a.scale_q) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 4; ++u) {
             qr[u].x = apply_scale(qr[u].x, a);
             qr[u].y = apply_scale(qr[u].y, a);
             qr[u].z = apply_scale(qr[u].z, a);
@@ -378,99 +373,102 @@ attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // S^T: A = K (lane = key), B = Q^T (lane = query).  The K fragments of key tile jt+1
-    // are read from LDS while the MFMAs of tile jt run.
-    v16f st[4];
-    float4 kf[2][8];
-    auto read_k = [&](int jt, float4 (&f)[8]) {
-        const float* kp = sk + (32 * jt + lr) * K_STRIDE + 32 * lh;
+    // S^T: A = K (lane = key), B = Q^T (lane = query); K fragments of tile kt+1 are read
+    // during the MFMAs of tile kt
+    v4f st[8];
+    float4 kf[2][4];
+    auto read_k = [&](int kt, float4 (&f)[4]) {
+        const float* kp = lds + (16 * kt + lq) * K_STRIDE + 16 * lg;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) f[u] = *reinterpret_cast<const float4*>(kp + 4 * u);
+        for (int u = 0; u < 4; ++u) f[u] = *reinterpret_cast<const float4*>(kp + 4 * u);
     };
     read_k(0, kf[0]);
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        if (jt + 1 < 4) read_k(jt + 1, kf[(jt + 1) & 1]);
+    for (int kt = 0; kt < 8; ++kt) {
+        if (kt + 1 < 8) read_k(kt + 1, kf[(kt + 1) & 1]);
+        st[kt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) st[jt][r] = 0.0f;
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                st[jt] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4c(kf[jt & 1][u], e), f4c(qr[u], e), st[jt], 0, 0, 0);
+                st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4c(kf[kt & 1][u], e), f4c(qr[u], e), st[kt], 0, 0, 0);
+    }
+    __syncthreads();  // every wave is done with K: the region takes V^T
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int r = u * 16 + (t >> 4);
+        lds[(c4 + 0) * VT_STRIDE + r] = vr[u].x;
+        lds[(c4 + 1) * VT_STRIDE + r] = vr[u].y;
+        lds[(c4 + 2) * VT_STRIDE + r] = vr[u].z;
+        lds[(c4 + 3) * VT_STRIDE + r] = vr[u].w;
     }
 
-    // softmax of row qi over its S keys: 64 here, 64 in lane ^ 32
+    // softmax of row qi over its S keys: 32 in this lane, the rest in lanes l ^ 16, l ^ 32
     float m = -INFINITY;
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
+    for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = 32 * jt + 8 * (r / 4) + 4 * lh + (r % 4);
-            float x = a.scale_q ? st[jt][r] : apply_scale(st[jt][r], a);
+        for (int r = 0; r < 4; ++r) {
+            const int key = 16 * kt + 4 * lg + r;
+            float x = a.scale_q ? st[kt][r] : apply_scale(st[kt][r], a);
             if (key >= S) x = -INFINITY;
-            st[jt][r] = x;
+            st[kt][r] = x;
             m = fmaxf(m, x);
         }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
     m = fmaxf(m, __shfl_xor(m, 32, 64));
     // hardware exp2 and one reciprocal per row: within a few ulp of expf and of e / sum,
-    // far inside the attention's tolerance, at a fraction of the VALU work (the softmax
-    // otherwise costs about half as many cycles as this wave's MFMAs)
+    // far inside the attention's tolerance, at a fraction of the VALU work
     float sum = 0.0f;
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
+    for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float e = __expf(__fsub_rn(st[jt][r], m));
-            st[jt][r] = e;
+        for (int r = 0; r < 4; ++r) {
+            const float e = __expf(__fsub_rn(st[kt][r], m));
+            st[kt][r] = e;
             sum = __fadd_rn(sum, e);
         }
+    sum = __fadd_rn(sum, __shfl_xor(sum, 16, 64));
     sum = __fadd_rn(sum, __shfl_xor(sum, 32, 64));
     const float inv = __fdiv_rn(1.0f, sum);
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
+    for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) st[jt][r] = __fmul_rn(st[jt][r], inv);
+        for (int r = 0; r < 4; ++r) st[kt][r] = __fmul_rn(st[kt][r], inv);
+    __syncthreads();  // V^T written
 
-    // ctx = P V: A = P straight from the S^T registers, B = V from LDS.  Step (jt, r)
-    // contracts over key 32 jt + 8 (r / 4) + 4 lh + r % 4 (this half-wave's key), so the B
-    // operands of r = 4 rq .. 4 rq + 3 are four consecutive keys of V^T row 32 dt + lr.
-    v16f o2[2];
+    // ctx = P V: A = P from the S^T registers, B = V^T rows of dims 16 dt + lq
+    v4f o[4];
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+    for (int dt = 0; dt < 4; ++dt) o[dt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o2[dt][r] = 0.0f;
+    for (int kt = 0; kt < 8; ++kt) {
+        float4 vq[4];
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
+        for (int dt = 0; dt < 4; ++dt)
+            vq[dt] = *reinterpret_cast<const float4*>(lds + (16 * dt + lq) * VT_STRIDE + 16 * kt + 4 * lg);
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-            float4 vq[2];
+        for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
-                vq[dt] = *reinterpret_cast<const float4*>(svt + (32 * dt + lr) * VT_STRIDE + 32 * jt +
-                                                          8 * rq + 4 * lh);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int dt = 0; dt < 2; ++dt)
-                    o2[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(st[jt][4 * rq + e], f4c(vq[dt], e), o2[dt], 0, 0, 0);
-        }
+            for (int dt = 0; dt < 4; ++dt)
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[kt][r], f4c(vq[dt], r), o[dt], 0, 0, 0);
+    }
+    // lane l holds ctx rows (queries) 16 w + 4 lg + r, dims 16 dt + lq
     float mn = 0.0f, mx = 0.0f;  // DQL range of out (when a.part is given)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = 32 * w + 8 * (r / 4) + 4 * lh + (r % 4);
+    for (int r = 0; r < 4; ++r) {
+        const int row = half * ATT_QB + 16 * w + 4 * lg + r;
         if (row >= S) continue;
-        float* dst = a.out + ((size_t)b * S + row) * a.ldo + h * ATT_D;
+        float* dst = a.out + ((size_t)b * S + row) * a.ldo + h * ATT_D + lq;
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-            dst[32 * dt + lr] = o2[dt][r];
-            if (a.part) icx::range_acc(o2[dt][r], mn, mx);
+        for (int dt = 0; dt < 4; ++dt) {
+            dst[16 * dt] = o[dt][r];
+            if (a.part) icx::range_acc(o[dt][r], mn, mx);
         }
     }
     if (a.part) icx::block_range_store<kThreads>(mn, mx, a.part);
 }
 
-constexpr size_t kAttnSmem = ((size_t)ATT_S * K_STRIDE + (size_t)ATT_D * VT_STRIDE) * sizeof(float);
 
 unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
     size_t b = icx::cdiv(work, per_block);
@@ -594,10 +592,13 @@ int icx::attention_f32(hipStream_t s, const float* q, const float* k, const floa
         !icx::aligned16(q) || !icx::aligned16(k) || !icx::aligned16(v))
         ICX_FAIL(ICX_ERR_SHAPE, "Attention: row strides must cover H*D and keep 16-byte alignment");
     if (B * H == 0) return ICX_OK;
-    if (B * H > 0x7fffffff) ICX_FAIL(ICX_ERR_SHAPE, "Attention: too many (batch, head) pairs");
-    float2* pp = (part && B * H <= (size_t)icx::kMaxRangeParts) ? part : nullptr;
+    if (B * H > 0x3fffffff) ICX_FAIL(ICX_ERR_SHAPE, "Attention: too many (batch, head) pairs");
+    // two blocks per (batch, head) when S > 64 (each takes 64 queries), one otherwise
+    const size_t per = S > (size_t)ATT_QB ? 2 : 1;
+    const size_t blocks = B * H * per;
+    float2* pp = (part && blocks <= (size_t)icx::kMaxRangeParts) ? part : nullptr;
     AttnArgs a{q, k, v, out, (int)S, (int)H, (int64_t)ldq, (int64_t)ldk, (int64_t)ldv, (int64_t)ldo,
-               scale, scale_div ? 1 : 0, scale_q ? 1 : 0, pp, 0.0f, 0};
+               scale, scale_div ? 1 : 0, scale_q ? 1 : 0, pp, 0.0f, 0, (int)per};
     {
         // a power-of-two scale whose reciprocal is a normal float: x / scale == x * (1 / scale)
         int e = 0;
@@ -608,16 +609,9 @@ int icx::attention_f32(hipStream_t s, const float* q, const float* k, const floa
             a.recip_exact = 1;
         }
     }
-    static bool smem_set = false;  // 67 KB of dynamic LDS is above the default limit
-    if (!smem_set) {
-        ICX_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          (int)kAttnSmem));
-        smem_set = true;
-    }
-    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)(B * H)), dim3(kThreads), kAttnSmem, s, a);
+    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
     ICX_LAUNCH_CHECK("attention_kernel");
-    if (pp && n_part) *n_part = (int)(B * H);
+    if (pp && n_part) *n_part = (int)blocks;
     return ICX_OK;
 }
 

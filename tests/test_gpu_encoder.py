@@ -1,10 +1,12 @@
 """GPU parity of the DistilBERT-shaped encoder run through GpuGraphExecutor.
 
 Two kinds of evidence:
-  * end to end on a small encoder (2 layers, batch 2, seq 16) against the oracle composition
-    of the same graph: the fp32 attention and exp differ from the reference's summation
-    order by f32 rounding, which can move a downstream quantized value by one step, so the
-    final output is compared within 1e-3 of its magnitude;
+  * end to end on a small encoder (2 layers, batch 2, seq 16, three seeds) against the oracle
+    composition of the same graph: the fp32 attention and exp differ from the reference's
+    summation order by f32 rounding.  When that moves the extreme element of a tensor a
+    DynamicQuantizeLinear reads, the scale changes and every element of that tensor is
+    requantized, so the final output is compared within 2e-2 of its magnitude (a few
+    quantization steps); when no range endpoint moves the outputs agree to ~1e-7;
   * node by node at the full BASELINE size (6 layers, batch 32, seq 128): each node's GPU
     output is checked against the oracle applied to that node's GPU inputs — bit-exact for
     every DynamicQuantizeLinear (x_q, scale, zero point), every quantized linear (integer
@@ -40,10 +42,11 @@ def assert_bits(got, want, what):
         what, bad, want.size, rel_err(got, want) if got.dtype == np.float32 else -1)
 
 
-def test_small_encoder_end_to_end():
+@pytest.mark.parametrize("seed", [4000, 4100, 4200])
+def test_small_encoder_end_to_end(seed):
     ex = GpuGraphExecutor()
-    out, names, params = graphs.encoder_graph(ex, layers=2, seed=4000)
-    x = graphs.encoder_input(2, 16, seed=4999)
+    out, names, params = graphs.encoder_graph(ex, layers=2, seed=seed)
+    x = graphs.encoder_input(2, 16, seed=seed + 999)
     got = ex.run({"x": x}, [out])[out]
     entries, _ = ex.plan()
     pats = [e.pattern for e in entries if e.kind == "FusedHead"]
@@ -51,7 +54,7 @@ def test_small_encoder_end_to_end():
     want = x
     for l in range(2):
         want = ref.layer_ref(want, params[l], 12, 1e-12)["out"]
-    assert rel_err(got, want) < 1e-3
+    assert rel_err(got, want) < 2e-2
 
 
 def test_attention_outside_the_fused_kernel_runs_node_by_node():
