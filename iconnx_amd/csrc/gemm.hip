@@ -19,7 +19,8 @@
 // reads are all contiguous.
 //
 // Tiling: v_mfma_i32_32x32x32_i8 tiles.  128x128 block tiles (4 waves of 64x64, three
-// blocks per CU) for shapes with few tiles; 256x256 (8 waves of 128x64) when there are at
+// blocks per CU) by default; 64x64 when 128x128 tiles would leave CUs idle; 256x192 (12
+// waves) when that gives every CU a tile; 256x256 (8 waves of 128x64) when there are at
 // least 512 of them; a persistent producer/consumer kernel for K-heavy shapes with fewer
 // tiles than CUs.  Operand tiles reach LDS by LDS DMA (main loops B, B2, C) or through
 // registers (main loop A: any K and alignment).  Blocks are remapped so each XCD
@@ -1298,18 +1299,25 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     const bool mid = !big && dma && K % 128 == 0 && N % 192 == 0 && (out_kind == OUT_I32 || ch != CH_GENERAL) &&
                      icx::cdiv(M, 256) * (N / 192) >= (size_t)num_cus() &&
                      (n_seg == 0 || (N / n_seg) % 192 == 0);
+    // 64x64 tiles when 128x128 ones would leave CUs idle (the encoder's output projection,
+    // 4096x768: 768 tiles instead of 192, up to six blocks per CU to hide each K step's latency)
+    const bool small = dma && !big && !mid && icx::cdiv(M, 128) * icx::cdiv(N, 128) < (size_t)num_cus();
     if (big) {
         g.tiles_m = (int)icx::cdiv(M, 256);
         g.tiles_n = (int)icx::cdiv(N, 256);
     } else if (mid) {
         g.tiles_m = (int)icx::cdiv(M, 256);
         g.tiles_n = (int)(N / 192);
+    } else if (small) {
+        g.tiles_m = (int)icx::cdiv(M, 64);
+        g.tiles_n = (int)icx::cdiv(N, 64);
     }
     const unsigned blocks = (unsigned)(g.tiles_m * g.tiles_n);
     if (out_kind == OUT_F32 && part && blocks <= (unsigned)icx::kMaxRangeParts) g.part = part;
     if (dma) {
         if (big) launch_dma_big<2, 4, 4>(out_kind, blocks, s, g);
         else if (mid) launch_dma_mid(out_kind, ch, blocks, s, g);
+        else if (small) launch_dma<64, 64, 2, 2, 3>(out_kind, ch, blocks, s, g);
         else launch_dma<128, 128, 2, 2, 3>(out_kind, ch, blocks, s, g);
     } else {
         if (big) launch_reg<256, 256>(vec, out_kind, ch, blocks, s, g);
