@@ -190,10 +190,10 @@ def test_dequantize_i32_large_values_follow_cpu_semantics():
     np.testing.assert_array_equal(bits(got), bits(oracle.dequantize_linear(x, s, zp)))
 
 
-def test_persistent_kernel_fused_epilogue():
-    """FFN-down shape (K = 3072, 192 tiles < CUs: the persistent kernel) with the dequant
-    scale, bias and a Sub/Div/Mul chain with an operand on the left, bit-exact vs the oracle's
-    op-by-op graph; per-channel scale and zero point included."""
+def test_ffn_down_shape_fused_epilogue():
+    """FFN-down shape (K = 3072; 768 tiles of 64x64) with the dequant scale, bias and a
+    Sub/Div/Mul chain with an operand on the left, bit-exact vs the oracle's op-by-op graph;
+    per-channel scale and zero point included."""
     rng = np.random.default_rng(31)
     M, K, N = 4096, 3072, 768
     x = rng.standard_normal((M, K)).astype(np.float32)

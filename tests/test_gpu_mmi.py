@@ -150,7 +150,7 @@ def test_baseline_gemm_shapes(cfg):
     np.testing.assert_array_equal(lhs, rhs)
 
 
-# Shapes with K >= 2048 and fewer 128x128 tiles than CUs take the persistent producer /
+# Shapes with K >= 2048 and fewer 64x64 tiles than CUs take the persistent producer /
 # consumer kernel; the rest of this file covers the multi-block kernels.
 @pytest.mark.parametrize("adt,bdt", [(np.uint8, np.int8), (np.int8, np.uint8)])
 def test_persistent_kernel_shapes(adt, bdt):
@@ -170,9 +170,9 @@ def test_persistent_kernel_shapes(adt, bdt):
         assert np.array_equal(gpu_mmi(a, b, azp, bzp_col, True, rowsum=rs), want)
 
 
-def test_persistent_kernel_encoder_ffn_down_shape():
-    """The DistilBERT FFN-down GEMM (4096 x 3072 x 768) at full size: every element against
-    the exact float64 product, rows against the oracle."""
+def test_encoder_ffn_down_shape():
+    """The DistilBERT FFN-down GEMM (4096 x 3072 x 768, 64x64 tiles) at full size: every
+    element against the exact float64 product, rows against the oracle."""
     rng = np.random.default_rng(29)
     a = rng.integers(0, 256, (4096, 3072)).astype(np.uint8)
     b = rng.integers(-127, 128, (3072, 768)).astype(np.int8)

@@ -108,7 +108,7 @@ def test_big_tile_path_sampled_rows():
 
 
 def test_stream_kernel_path():
-    # K = 2048, 4 x 6 128-wide tiles < CUs -> the persistent producer / consumer kernel
+    # K = 2048, 8 x 12 64-wide tiles < CUs -> the persistent producer / consumer kernel
     ex, x, params, outs = build(512, 2048, 256, 3, seed=71)
     got = ex.run({"x": torch.from_numpy(x).cuda()}, outs)
     assert set(groups_of(ex).values()) == {"h0.mmi"}
