@@ -97,8 +97,9 @@ class Runner:
             self.keep += k
             self.a_dtype, self.b_dtype = ICX_U8, ICX_I8
             self.ops_count = 2.0 * self.M * self.N * self.K
-            # >= 512 tiles of 256x256 with K % 128 == 0 (cfg4) take the 128-byte-row kernel
-            self.dominant = "gemm_i8_dma128_kernel" if cfg == "cfg4" else "gemm_i8_dma_kernel"
+            # cfg2 (256x192 tiles) and cfg4 (256x256) take the 128-byte-row kernel, cfg1 the
+            # 64x64-tile one
+            self.dominant = "gemm_i8_dma128_kernel" if cfg in ("cfg2", "cfg4") else "gemm_i8_dma_kernel"
         elif cfg == "cfg5a":
             self.M, self.K = d["a"].shape
             self.N = d["b"].shape[1]

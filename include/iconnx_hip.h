@@ -100,9 +100,15 @@ int icx_matmul_integer(icx_stream_t stream, const void* A, int a_dtype, const vo
 enum { ICX_OP_ADD = 0, ICX_OP_SUB = 1, ICX_OP_MUL = 2, ICX_OP_DIV = 3 };
 /* Operand-free steps (p0 may be NULL; kinds ignored), for the erf-GELU subgraph
  * Mul(x, Add(Erf(Div(x, c0)), c1)) [* c2] (src/operators/erf.rs:21-31):
- *   ICX_OP_ERF        v = erf(v) — the reference's Abramowitz-Stegun 7.1.26 evaluated in f32;
+ *   ICX_OP_ERF        v = erf(v) — the reference's Abramowitz-Stegun 7.1.26 in f32, with a
+ *                     Newton-refined hardware reciprocal and the hardware exp2 (within 2e-7
+ *                     of the formula evaluated with correctly rounded ops);
  *   ICX_OP_SAVE       s = v (v unchanged);
- *   ICX_OP_MUL_SAVED  v = s * v (one rounding; operand_is_lhs ignored, products commute). */
+ *   ICX_OP_MUL_SAVED  v = s * v (one rounding; operand_is_lhs ignored, products commute).
+ * A Div (operand on the right) whose next step is ICX_OP_ERF is, in chains whose operands
+ * are all scalars or [cols] vectors, evaluated as v * RN(1 / operand): at most one ulp from
+ * the quotient, which moves the erf result by < 4e-8 (its only reader; Erf is compared
+ * within tolerance anyway).  Every other step rounds exactly as the reference's node. */
 enum { ICX_OP_ERF = 4, ICX_OP_SAVE = 5, ICX_OP_MUL_SAVED = 6 };
 enum { ICX_BCAST_SCALAR = 0, ICX_BCAST_COL = 1, ICX_BCAST_ROW = 2, ICX_BCAST_FULL = 3 };
 #define ICX_MAX_CHAIN 8
