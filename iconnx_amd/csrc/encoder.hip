@@ -334,7 +334,19 @@ __device__ __forceinline__ float f4c(const float4& v, int e) {
 
 __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float lds[ATT_LDS_FLOATS];
-    const int pair = blockIdx.x / a.qsplit, half = blockIdx.x % a.qsplit;
+    // The two halves of a (batch, head) are blocks g and g + 8 of a group of 16, which the
+    // hardware places on the same XCD (block i runs on XCD i % 8), so the second half's K and
+    // V loads hit that XCD's L2.
+    int pair = blockIdx.x, half = 0;
+    if (a.qsplit == 2) {
+        const int grp = blockIdx.x >> 4, in = blockIdx.x & 15;
+        pair = grp * 8 + (in & 7);
+        half = in >> 3;
+        if ((int)gridDim.x & 15) {  // a partial last group: plain pairing
+            pair = blockIdx.x >> 1;
+            half = blockIdx.x & 1;
+        }
+    }
     const int b = pair / a.H, h = pair % a.H;
     const int S = a.S;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
