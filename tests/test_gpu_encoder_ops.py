@@ -152,6 +152,17 @@ def test_fused_attention_close(B, S, H, scale_q):
     assert rel_err(out, attention_oracle(q, k, v, H, 8.0, scale_q)) < 1e-5
 
 
+@pytest.mark.parametrize("B,S,H,scale,scale_q", [(3, 97, 5, 3.0, False), (1, 128, 8, 0.7, True)])
+def test_fused_attention_other_scales_and_grids(B, S, H, scale, scale_q):
+    """A scale that is not a power of two (the correctly rounded division path), a query
+    split whose block count is not a multiple of 16 (plain pairing of the two halves), and
+    one that is (the XCD-local pairing) with an odd sequence length."""
+    rng = np.random.default_rng(B * 1000 + S)
+    q, k, v = (rng.standard_normal((B, S, H * 64)).astype(np.float32) for _ in range(3))
+    out = host(ops.gpu_attention(dev(q), dev(k), dev(v), H, scale, scale_div=True, scale_q=scale_q))
+    assert rel_err(out, attention_oracle(q, k, v, H, scale, scale_q)) < 1e-5
+
+
 def test_attention_rejects_unsupported_shapes():
     q = torch.zeros((1, 129, 64), device="cuda")
     with pytest.raises(IconnxError, match="unsupported"):
