@@ -181,13 +181,26 @@ __device__ __forceinline__ Slice slice_of(size_t units, size_t unit, size_t tail
     return s;
 }
 
-// Reduce the partials of launch 1 (every block of launch 2 does this redundantly).
+// Reduce the partials of launch 1 (every block of launch 2 does this redundantly).  The
+// first 4 * kThreads partials (all of them for the grids used here) are requested at once;
+// a missing one reads as (0, 0), which never moves a range that starts at (0, 0).
 __device__ __forceinline__ DqlParams fold_partials(const float2* __restrict__ part, int G) {
     float mn = 0.0f, mx = 0.0f;
-    for (int i = threadIdx.x; i < G; i += kThreads) {
-        float2 v = part[i];
-        acc_minmax(v.x, mn, mx);
-        acc_minmax(v.y, mn, mx);
+    float2 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = threadIdx.x + u * kThreads;
+        v[u] = i < G ? part[i] : make_float2(0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        acc_minmax(v[u].x, mn, mx);
+        acc_minmax(v[u].y, mn, mx);
+    }
+    for (int i = threadIdx.x + 4 * kThreads; i < G; i += kThreads) {
+        const float2 w = part[i];
+        acc_minmax(w.x, mn, mx);
+        acc_minmax(w.y, mn, mx);
     }
     block_minmax(mn, mx);
     return make_params(mn, mx);
