@@ -1,0 +1,154 @@
+// DynamicQuantizeLinear's arithmetic (src/operators/dynamic_quantize_linear.rs:32-112),
+// shared by the DQL launches and the GEMM that quantizes its own output:
+//   * min/max start at 0.0 and skip NaN (:56-69) — `v < mn ? v : mn` keeps that exactly,
+//     including +0.0 winning over -0.0;
+//   * scale = (max-min)/255 and zp = clamp(rne(0 - min/scale)) in f64 (:89-91);
+//   * y = clamp(rne(x / scale) + zp) with the division in f64 (:97-103), NaN -> 0.
+// Per-element rounding.  |x / scale| <= 255 because min <= 0 <= max.  The fast path forms
+// q = x * fl32(1/scale) in f32: two roundings of relative size <= 2^-24 each give
+// |q - x/scale| <= 255 * 2^-23 < 3.1e-5.  When q is farther than 1e-4 from a half-integer,
+// rne(q) equals rne of the exact quotient and of its f64 rounding (which is within
+// 255 * 2^-53 of it).  Otherwise — and for NaN, subnormal x, or a scale outside
+// [1e-30, 1e30] — the f64 division is performed as the reference does.  The f64 path itself
+// uses x * (1/scale) and falls back to the correctly rounded division within 1e-9 of a tie.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace icx {
+namespace dql {
+
+struct alignas(16) DqlParams {
+    double s;     // f64 scale (0 for the constant-input sentinel)
+    double inv;   // 1/s
+    float inv32;  // fl32(1/s), used when `fast`
+    int zp;
+    int zero;     // min == max
+    int fast;     // scale in [1e-30, 1e30]
+};
+
+__device__ __forceinline__ void acc_minmax(float v, float& mn, float& mx) {
+    mn = (v < mn) ? v : mn;  // NaN compares false: skipped
+    mx = (v > mx) ? v : mx;
+}
+
+__device__ __forceinline__ void acc4(float4 v, float& mn, float& mx) {
+    acc_minmax(v.x, mn, mx);
+    acc_minmax(v.y, mn, mx);
+    acc_minmax(v.z, mn, mx);
+    acc_minmax(v.w, mn, mx);
+}
+
+__device__ __forceinline__ void wave_minmax(float& mn, float& mx) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        float omn = __shfl_xor(mn, off, 64);
+        float omx = __shfl_xor(mx, off, 64);
+        acc_minmax(omn, mn, mx);
+        acc_minmax(omx, mn, mx);
+    }
+}
+
+// Block-wide (min, max) over NT threads; result valid in every thread.
+template <int NT>
+__device__ __forceinline__ void block_minmax(float& mn, float& mx) {
+    __shared__ float smn[NT / 64], smx[NT / 64];
+    wave_minmax(mn, mx);
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        smn[wid] = mn;
+        smx[wid] = mx;
+    }
+    __syncthreads();
+    mn = smn[0];
+    mx = smx[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) {
+        acc_minmax(smn[w], mn, mx);
+        acc_minmax(smx[w], mn, mx);
+    }
+}
+
+__device__ __forceinline__ int clamp_u8(double q) {
+    if (q != q) return 0;  // NaN -> 0 (Rust saturating `as u8`)
+    q = q < 0.0 ? 0.0 : q;
+    q = q > 255.0 ? 255.0 : q;
+    return (int)q;
+}
+
+__device__ __forceinline__ DqlParams make_params(float mn, float mx) {
+    DqlParams p;
+    const double mnd = (double)mn, mxd = (double)mx;
+    if (mnd == mxd) {
+        p.s = 0.0;
+        p.inv = 0.0;
+        p.inv32 = 0.0f;
+        p.zp = 0;
+        p.zero = 1;
+        p.fast = 0;
+        return p;
+    }
+    p.s = (mxd - mnd) / 255.0;
+    p.zp = clamp_u8(rint(0.0 - mnd / p.s));
+    p.inv = 1.0 / p.s;
+    p.inv32 = (float)p.inv;
+    p.zero = 0;
+    p.fast = (p.s >= 1e-30 && p.s <= 1e30) ? 1 : 0;
+    return p;
+}
+
+// Reference-exact f64 path.
+__device__ __forceinline__ uint32_t quant1_f64(float x, const DqlParams& p) {
+    const double xd = (double)x;
+    const double q = xd * p.inv;
+    const double fr = q - floor(q);
+    double r;
+    if (fabs(fr - 0.5) < 1e-9)
+        r = rint(xd / p.s);  // near a tie: the correctly rounded quotient decides
+    else
+        r = rint(q);
+    return (uint32_t)clamp_u8(r + (double)p.zp);
+}
+
+__device__ __forceinline__ uint32_t quant1(float x, const DqlParams& p) {
+    if (p.zero) return 0u;
+    const float q = x * p.inv32;
+    const float r = rintf(q);
+    const float tie_dist = fabsf(fabsf(q - r) - 0.5f);  // q - r is exact (Sterbenz)
+    // NaN fails every comparison and so takes the exact path, as do subnormal inputs.
+    const bool ok = p.fast && tie_dist > 1e-4f && (fabsf(x) >= 1.17549435e-38f || x == 0.0f);
+    if (!ok) return quant1_f64(x, p);
+    int v = (int)r + p.zp;
+    v = v < 0 ? 0 : v;
+    v = v > 255 ? 255 : v;
+    return (uint32_t)v;
+}
+
+// Four elements at once.  With `fast` (a scale in [1e-30, 1e30]) the f32 quotient q and
+// r = rne(q) decide every element with |q - r| < 0.4999 (the condition of quant1 written
+// without its tie-distance arithmetic: |q - r| <= 0.5 always).  Subnormal x need no
+// separate test here: |q| < 2e-8 then, so r = 0 = rne of the exact quotient.  NaN and inf
+// make q - r NaN, which fails the test and goes to quant1.
+__device__ __forceinline__ uint32_t quant4(float4 v, const DqlParams& p) {
+    if (p.fast) {
+        const float q0 = v.x * p.inv32, q1 = v.y * p.inv32, q2 = v.z * p.inv32, q3 = v.w * p.inv32;
+        const float r0 = rintf(q0), r1 = rintf(q1), r2 = rintf(q2), r3 = rintf(q3);
+        const bool ok = fabsf(q0 - r0) < 0.4999f && fabsf(q1 - r1) < 0.4999f &&
+                        fabsf(q2 - r2) < 0.4999f && fabsf(q3 - r3) < 0.4999f;
+        if (ok) {
+            const uint32_t a = (uint32_t)__builtin_amdgcn_fmed3f(r0 + (float)p.zp, 0.0f, 255.0f);
+            const uint32_t b = (uint32_t)__builtin_amdgcn_fmed3f(r1 + (float)p.zp, 0.0f, 255.0f);
+            const uint32_t c = (uint32_t)__builtin_amdgcn_fmed3f(r2 + (float)p.zp, 0.0f, 255.0f);
+            const uint32_t d = (uint32_t)__builtin_amdgcn_fmed3f(r3 + (float)p.zp, 0.0f, 255.0f);
+            return a | (b << 8) | (c << 16) | (d << 24);
+        }
+    }
+    return quant1(v.x, p) | (quant1(v.y, p) << 8) | (quant1(v.z, p) << 16) |
+           (quant1(v.w, p) << 24);
+}
+
+
+}  // namespace dql
+}  // namespace icx

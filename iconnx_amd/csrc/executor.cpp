@@ -249,6 +249,9 @@ struct icx_graph {
     std::map<std::string, size_t> last_use;    // tensor -> plan index of its last reader
     std::set<std::string> rowsum_wanted;       // DQL outputs whose row sums a GEMM reads
     std::set<std::string> range_wanted;        // DQL inputs whose producer leaves their range
+    // quantized-linear head output -> the DynamicQuantizeLinear that is its only reader: the
+    // head's GEMM writes the DQL's outputs itself when the shape allows (icx::qlinear_dql)
+    std::map<std::string, Node> quant_out;
 
     // device state
     std::map<std::string, DevTensor> weights;      // uploaded initializers
@@ -257,6 +260,9 @@ struct icx_graph {
     std::map<std::string, DevTensor> values;       // tensors of the current / last run
     std::map<std::string, std::string> rowsum_of;  // DQL y -> its row-sum tensor
     std::map<std::string, std::pair<std::string, int>> range_of;  // DQL x -> (partials tensor, count)
+    std::set<std::string> dql_done;  // DQL outputs already written by their producer's GEMM
+    int64_t quant_fused = 0;         // GEMM launches that quantized their own output
+    unsigned* qsync = nullptr;       // exchange buffer of those launches (zeroed once)
     hipStream_t last_stream = nullptr;
     bool ran = false;
     Pool pool;
@@ -292,6 +298,8 @@ struct icx_graph {
         if (ws) (void)hipFree(ws);
         ws = nullptr;
         ws_bytes = 0;
+        if (qsync) (void)hipFree(qsync);
+        qsync = nullptr;
     }
     void clear_run() {
         for (auto& kv : values)
@@ -299,6 +307,7 @@ struct icx_graph {
         values.clear();
         rowsum_of.clear();
         range_of.clear();
+        dql_done.clear();
     }
     void invalidate() {
         planned = compiled = false;
@@ -449,6 +458,21 @@ class Planner {
         for (auto& o : g_.live_outputs) {
             g_.keep.insert(o);
             g_.keep.insert(root_of(o));
+        }
+        // a quantized-linear head (Int8 weight without zero point, no sibling group) whose
+        // output only a DynamicQuantizeLinear reads, and whose quantized output no GEMM reads
+        // row sums of: the head's GEMM may write the DQL's outputs itself
+        g_.quant_out.clear();
+        for (auto& op : g_.plan) {
+            if (op.kind != Kind::FusedHead || op.pattern != Pattern::QuantizedLinear || !op.group.empty()) continue;
+            if (g_.inits[op.w].dtype != ICX_I8 || !(op.w_zp.empty() || op.w_zp_folded)) continue;
+            if (g_.keep.count(op.out) || !g_.range_wanted.count(op.out)) continue;
+            auto cs = gi_.consumers.find(op.out);
+            if (cs == gi_.consumers.end() || cs->second.size() != 1) continue;
+            const Node& d = nodes_[cs->second[0]];
+            if (d.op != "DynamicQuantizeLinear" || d.in.size() != 1 || d.out.size() != 3) continue;
+            if (g_.rowsum_wanted.count(d.out[0])) continue;
+            g_.quant_out[op.out] = d;
         }
         g_.planned = true;
         return ICX_OK;
@@ -1305,6 +1329,25 @@ class Runner {
         if (rc) return rc;
         const void* a_ptr = A->ptr;
         const int a_dt = A->dtype;
+        auto qo = g_.quant_out.find(op.out);
+        if (qo != g_.quant_out.end() && g_.qsync && bzp == nullptr) {
+            const Node& d = qo->second;
+            DevTensor *QY, *QS, *QZ;
+            rc = alloc(d.out[0], ICX_U8, oshape, &QY);
+            if (!rc) rc = alloc(d.out[1], ICX_F32, {}, &QS);
+            if (!rc) rc = alloc(d.out[2], ICX_U8, {}, &QZ);
+            if (rc) return rc;
+            rc = icx::qlinear_dql(s_, a_ptr, a_dt, pw.packed, pw.dtype, pw.colsum, M, pw.K, pw.N, azp, &ch,
+                                  static_cast<uint8_t*>(QY->ptr), static_cast<float*>(QS->ptr),
+                                  static_cast<uint8_t*>(QZ->ptr), g_.qsync);
+            if (rc == ICX_OK) {
+                g_.dql_done.insert(d.out[0]);
+                ++g_.quant_fused;
+                return ICX_OK;
+            }
+            if (rc != ICX_ERR_UNSUPPORTED) return rc;
+            icx::clear_error();  // shape outside the fused kernel: f32 output, then the DQL
+        }
         DevTensor* Y;
         rc = alloc(op.out, ICX_F32, oshape, &Y);
         if (rc) return rc;
@@ -1609,6 +1652,7 @@ class Runner {
                       n.out.size());
             return ICX_ERR_INVALID_ARG;
         }
+        if (g_.dql_done.count(n.out[0])) return ICX_OK;  // its producer's GEMM wrote y, scale, zp
         const DevTensor* X;
         int rc = need(n.in[0], &X, "DynamicQuantizeLinear");
         if (rc) return rc;
@@ -1904,6 +1948,8 @@ static int icx_graph_plan_impl(icx_graph* g, char* buf, size_t buf_len) {
         }
         for (auto& r : g->rowsum_wanted) o << "rowsum " << r << "\n";
         for (auto& r : g->range_wanted) o << "range " << r << "\n";
+        for (auto& q : g->quant_out) o << "quantout " << q.first << " " << q.second.name << "\n";
+        if (g->quant_fused) o << "quantout-launches " << g->quant_fused << "\n";
         const std::string s = o.str();
         if (s.size() + 1 > buf_len)
             ICX_FAIL(ICX_ERR_INVALID_ARG, "plan: summary needs %zu bytes, buffer has %zu", s.size() + 1, buf_len);
@@ -1921,6 +1967,11 @@ static int icx_graph_compile_impl(icx_graph* g, icx_stream_t stream) {
     if (g->ran && g->last_stream) ICX_HIP_CHECK(hipStreamSynchronize(g->last_stream));
     g->clear_run();
     g->free_weights();
+    if (!g->quant_out.empty()) {  // zeroed once; every launch leaves it valid for the next
+        ICX_HIP_CHECK(hipMalloc(&g->qsync, icx::kQoutSyncBytes));
+        ICX_HIP_CHECK(hipMemsetAsync(g->qsync, 0, icx::kQoutSyncBytes, s));
+        ICX_HIP_CHECK(hipStreamSynchronize(s));
+    }
     // initializers read as a MatMulInteger weight are packed once: B'^T [N,K] + colsum
     std::set<std::string> gemm_w;
     for (auto& op : g->plan) {

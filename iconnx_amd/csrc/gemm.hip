@@ -27,6 +27,7 @@
 // (blockIdx % 8) works on a contiguous, M-grouped range of tiles that shares A/B panels in
 // its own L2.
 #include "chain.hpp"
+#include "dql_core.hpp"
 #include "internal.hpp"
 
 namespace {
@@ -65,6 +66,14 @@ struct GemmArgs {
     // so a tile lies in one segment.
     void* seg[icx::kMaxSegments];
     int seg_n;
+    // Quantized output (the GEMM is the producer of a DynamicQuantizeLinear): y as u8, its
+    // scale and zero point, the exchange buffer (see qout_epilogue) and the bound of every
+    // wait, in polls.
+    uint8_t* qy;
+    float* q_scale;
+    uint8_t* q_zp;
+    unsigned* q_sync;
+    int q_spin;
 };
 
 // Output of the tile whose first column is n0: base pointer, row stride and the global
@@ -529,6 +538,155 @@ gemm_i8_dma_kernel(GemmArgs g) {
     if (OUT == OUT_F32 && g.part) icx::block_range_store<64 * WGM * WGN>(mn, mx, g.part);
 }
 
+// ---- quantized output -------------------------------------------------------------------
+// For a GEMM whose f32 output is read only by a DynamicQuantizeLinear: the chain runs on the
+// accumulators in their MFMA layout (lane = column), every block publishes the (min, max) of
+// its tile, waits for all the others' (every block is resident — the host launches no more
+// than fit — and each wait is bounded by q_spin polls), folds them into the DQL's scale and
+// zero point exactly as the DQL launch would (dql_core.hpp) and writes its tile as u8
+// through an LDS byte tile with 16-byte row stores.  The f32 output is never written.  No
+// row term: the host requires an int8 weight whose zero point was folded away.
+//
+// q_sync: word 0 the launch number E, word 1 the finish count (bits 0-15) and the number of
+// blocks whose wait ran out (bits 16-31); from byte 256, two 64-bit slots per block: min
+// and max, each tagged with E + 1 in its high half, so that a reader takes a slot as this
+// launch's as soon as it sees the tag (zeroed memory never matches).  Every block reads E
+// before it counts its finish, and the last block to finish increments E, so all blocks of
+// a launch agree on it.  All accesses to q_sync are device-scope atomics (they bypass the
+// per-XCD L2s): no release / acquire fences, whose per-block L2 write-back and invalidate
+// would cost more than the exchange.  If a wait runs out (blocks not co-resident) that
+// block's tile is written as 0 and the last block to finish writes the scale as NaN, so
+// that every consumer shows the failure.
+template <int BM, int BN, int WGM, int WGN, int CH>
+__device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
+                                              int8_t* smem, int m0, int n0, unsigned tag) {
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TI = WM / 32, TJ = WN / 32;
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int MODE = CH == CH_COL_EXT ? 2 : 0;
+    constexpr int QS = BN + 16;                          // bytes per staged u8 row
+    constexpr int SOP_BYTES = ICX_MAX_CHAIN * BN * 4;
+    static_assert(SOP_BYTES + BM * QS <= (BM + BN) * 256, "LDS regions fit the tile buffer");
+    const int t = threadIdx.x;
+    const int lane = t & 63, wid = t >> 6;
+    const int wm = wid / WGN, wn = wid % WGN;
+    const int lr = lane & 31;
+    float* sop = reinterpret_cast<float*>(smem);
+    uint8_t* qs = reinterpret_cast<uint8_t*>(smem) + SOP_BYTES;
+    if (t < BN) {
+#pragma unroll
+        for (int k = 0; k < ICX_MAX_CHAIN; ++k)
+            if (k < g.chain.n_ops && icx::op_takes_operand(g.chain.ops[k].op))
+                sop[k * BN + t] = icx::col_operand(g.chain, k, min(n0 + t, g.N - 1));
+    }
+    const int azp = load_zp(g.a_zp, g.a_zp_u8, 0);
+    const uint32_t amz = (uint32_t)(g.alpha - azp);
+    __syncthreads();
+
+    float mn = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int c = wn * WN + j * 32 + lr;  // column within the tile
+        const int col = min(n0 + c, g.N - 1);
+        const uint32_t colterm = amz * (uint32_t)g.colsum[col] + (uint32_t)g.K * amz * (uint32_t)g.beta;
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            float4 v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[q].x = (float)(int32_t)((uint32_t)acc[i][j][4 * q + 0] + colterm);
+                v[q].y = (float)(int32_t)((uint32_t)acc[i][j][4 * q + 1] + colterm);
+                v[q].z = (float)(int32_t)((uint32_t)acc[i][j][4 * q + 2] + colterm);
+                v[q].w = (float)(int32_t)((uint32_t)acc[i][j][4 * q + 3] + colterm);
+            }
+            icx::run_chain4<MODE>(g.codes, g.chain.n_ops, v, [&](int k) {
+                const float o = sop[k * BN + c];
+                return make_float4(o, o, o, o);
+            });
+            // register 4 q + e holds row 8 q + 4 (lane >> 5) + e of this 32-row slab
+            const int rbase = m0 + wm * WM + i * 32 + 4 * (lane >> 5);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float* w = reinterpret_cast<const float*>(&v[q]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (rbase + 8 * q + e < g.M) icx::range_acc(w[e], mn, mx);
+                    acc[i][j][4 * q + e] = __float_as_int(w[e]);
+                }
+            }
+        }
+    }
+    icx::dql::block_minmax<NT>(mn, mx);
+    unsigned long long* slot = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(g.q_sync) + 256);
+    const unsigned long long hi_tag = (unsigned long long)tag << 32;
+    if (t == 0) {
+        __hip_atomic_store(slot + 2 * blockIdx.x, hi_tag | __float_as_uint(mn), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(slot + 2 * blockIdx.x + 1, hi_tag | __float_as_uint(mx), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // thread b waits for block b's pair (G <= NT, checked by the host)
+    float gmn = 0.0f, gmx = 0.0f;
+    int late = 0;
+    if (t < (int)gridDim.x) {
+        unsigned long long lo, hi;
+        for (int it = 0;; ++it) {
+            lo = __hip_atomic_load(slot + 2 * t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            hi = __hip_atomic_load(slot + 2 * t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((unsigned)(lo >> 32) == tag && (unsigned)(hi >> 32) == tag) break;
+            if (it >= g.q_spin) {
+                late = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(8);
+        }
+        icx::dql::acc_minmax(__uint_as_float((uint32_t)lo), gmn, gmx);
+        icx::dql::acc_minmax(__uint_as_float((uint32_t)hi), gmn, gmx);
+    }
+    const bool ok = __syncthreads_or(late) == 0;
+    icx::dql::block_minmax<NT>(gmn, gmx);
+    const icx::dql::DqlParams p = icx::dql::make_params(gmn, gmx);
+    // quantize into the LDS byte tile [BM][QS]
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int c = wn * WN + j * 32 + lr;
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int r0 = wm * WM + i * 32 + 4 * (lane >> 5);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 w = make_float4(__int_as_float(acc[i][j][4 * q + 0]), __int_as_float(acc[i][j][4 * q + 1]),
+                                             __int_as_float(acc[i][j][4 * q + 2]), __int_as_float(acc[i][j][4 * q + 3]));
+                const uint32_t b4 = ok ? icx::dql::quant4(w, p) : 0u;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qs[(r0 + 8 * q + e) * QS + c] = (uint8_t)(b4 >> (8 * e));
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int C16 = BN / 16;
+    for (int idx = t; idx < BM * C16; idx += NT) {
+        const int r = idx / C16, c16 = idx - r * C16;
+        const int grow = m0 + r;
+        if (grow < g.M)
+            *reinterpret_cast<uint4*>(g.qy + (size_t)grow * g.N + n0 + 16 * c16) =
+                *reinterpret_cast<const uint4*>(qs + r * QS + 16 * c16);
+    }
+    // the last block to finish writes the scale and zero point (NaN and 0 if any block's
+    // wait ran out) and starts the next launch number
+    if (t == 0) {
+        unsigned* fin = g.q_sync + 1;
+        const unsigned old = __hip_atomic_fetch_add(fin, ok ? 1u : 0x10001u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((old & 0xffffu) == gridDim.x - 1) {
+            const bool err = !ok || (old >> 16) != 0;
+            *g.q_scale = err ? __builtin_nanf("") : (float)p.s;
+            *g.q_zp = err ? (uint8_t)0 : (uint8_t)p.zp;
+            __hip_atomic_store(fin, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(g.q_sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 // ---- main loop B2: LDS DMA with 128-byte K rows (256x256 tile, K % 128 == 0) ------------
 // The large-shape variant of main loop B.  A stage holds two 64-wide K steps as 128-byte
 // LDS rows, so every lane-octet of a copy reads one whole 128-byte line of a row (the
@@ -542,7 +700,7 @@ gemm_i8_dma_kernel(GemmArgs g) {
 // tiles), and 256x192 with 12 waves of 64x64 — three per SIMD — for shapes that give every CU
 // one such tile (the DistilBERT FFN-up: 256 tiles), where it moves 42% fewer bytes from L2
 // into LDS than three 128x128 tiles per CU.
-template <int BM, int BN, int WGM, int WGN, int OUT, int CH>
+template <int BM, int BN, int WGM, int WGN, int OUT, int CH, int QOUT = 0>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs g) {
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
@@ -584,6 +742,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
         srcB[i] = g.Bp + (size_t)min(n0 + row, g.N - 1) * g.K + 16 * kc;
     }
     const int KT = g.K / ROWB;
+    // the launch number of a quantized-output launch, read before the main loop hides its latency
+    unsigned q_tag = 0;
+    if constexpr (QOUT != 0) q_tag = __hip_atomic_load(g.q_sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     auto issue = [&](int buf, int kt) {
         if (!copier) return;
         const int k0 = kt * ROWB;
@@ -662,6 +823,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
     wait_vmcnt<0>();
     __syncthreads();  // all copies landed and all fragment reads done: LDS is free
     float mn = 0.0f, mx = 0.0f;
+    if constexpr (QOUT != 0) {
+        qout_epilogue<BM, BN, WGM, WGN, CH>(g, acc, smem, m0, n0, q_tag);
+        return;
+    }
     gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0, mn, mx);
     if (OUT == OUT_F32 && g.part) icx::block_range_store<64 * WGM * WGN>(mn, mx, g.part);
 }
@@ -1180,6 +1345,29 @@ int launch_stream(int out_kind, int ch, unsigned tiles, hipStream_t s, const Gem
         return launch_stream_one<BM, BN, WGM, WGN, NP, NS, OUT_F32, CH_COL>(tiles, s, g);
 }
 
+// 256x192 tiles quantizing their own output: every block must be resident at once, so the
+// launch is refused (ICX_ERR_UNSUPPORTED, nothing launched) when the occupancy calculator
+// says the grid does not fit.
+template <int CH>
+int launch_qout(unsigned blocks, hipStream_t s, const GemmArgs& g) {
+    auto kern = gemm_i8_dma128_kernel<256, 192, 4, 3, OUT_F32, CH, 1>;
+    static int per_cu[64] = {0};
+    int d = 0;
+    ICX_HIP_CHECK(hipGetDevice(&d));
+    if (d < 0 || d >= 64) ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: device index %d", d);
+    if (!per_cu[d]) {
+        int n = 0;
+        ICX_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 768, 0));
+        per_cu[d] = n > 0 ? n : -1;
+    }
+    if (per_cu[d] < 0 || blocks > (unsigned)(per_cu[d] * num_cus()))
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: %u blocks exceed the %d resident ones", blocks,
+                 per_cu[d] * num_cus());
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(768), 0, s, g);
+    ICX_LAUNCH_CHECK("gemm_i8_dma128_kernel (quantized output)");
+    return ICX_OK;
+}
+
 int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,
                 int b_packed, const int32_t* b_colsum, size_t M, size_t K, size_t N,
                 const void* a_zp, const void* b_zp, size_t b_zp_len, const int32_t* a_rowsum,
@@ -1364,6 +1552,54 @@ int icx::qlinear_f32(hipStream_t s, const void* A, int a_dtype, const void* B, i
                      size_t ws_bytes, float2* part, int* n_part) {
     return gemm_common(s, A, a_dtype, B, b_dtype, b_packed, b_colsum, M, K, N, a_zp, b_zp, b_zp_len, a_rowsum,
                        chain, Y, OUT_F32, ws, ws_bytes, "QLinear", part, n_part);
+}
+
+int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int b_dtype,
+                     const int32_t* b_colsum, size_t M, size_t K, size_t N, const void* a_zp,
+                     const icx_chain* chain, uint8_t* y, float* y_scale, uint8_t* y_zp, unsigned* sync) {
+    if (!A || !Bp || !b_colsum || !y || !y_scale || !y_zp || !sync)
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "QLinear+DQL: null pointer");
+    if (!icx::is_int8_kind(a_dtype) || b_dtype != ICX_I8)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: needs an Int8 weight (dtypes %d, %d)", a_dtype, b_dtype);
+    if (M == 0 || M > 0x7fffffff || K > 0x7fffffff || N > 0x7fffffff || K < 128 || K % 128 != 0 ||
+        N % 192 != 0 || !icx::aligned16(A) || !icx::aligned16(Bp) || !icx::aligned16(y))
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: shape %zux%zux%zu or alignment outside the 256x192 kernel",
+                 M, K, N);
+    GemmArgs g{};
+    if (chain) {
+        int rc = icx::validate_chain(chain, "QLinear+DQL");
+        if (rc) return rc;
+        g.chain = *chain;
+    } else {
+        g.chain.n_ops = 0;
+    }
+    if (!icx::chain_is_col_only(g.chain))
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: the epilogue has row or full-tensor operands");
+    const unsigned blocks = (unsigned)(icx::cdiv(M, 256) * (N / 192));
+    if (blocks > (unsigned)icx::kQoutMaxBlocks)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: %u tiles exceed %d", blocks, icx::kQoutMaxBlocks);
+    g.A = reinterpret_cast<const int8_t*>(A);
+    g.Bp = Bp;
+    g.colsum = b_colsum;
+    g.a_zp = a_zp;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.tiles_m = (int)icx::cdiv(M, 256);
+    g.tiles_n = (int)(N / 192);
+    g.a_xor = a_dtype == ICX_U8 ? 0x80808080u : 0u;
+    g.alpha = a_dtype == ICX_U8 ? 128 : 0;
+    g.beta = 0;
+    g.a_zp_u8 = a_dtype == ICX_U8;
+    g.b_zp_len = 1;
+    g.codes = icx::chain_codes(g.chain);
+    g.qy = y;
+    g.q_scale = y_scale;
+    g.q_zp = y_zp;
+    g.q_sync = sync;
+    g.q_spin = 1 << 20;
+    if (icx::chain_mode(g.chain) == 2) return launch_qout<CH_COL_EXT>(blocks, s, g);
+    return launch_qout<CH_COL>(blocks, s, g);
 }
 
 int icx::qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,

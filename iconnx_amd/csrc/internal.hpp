@@ -32,6 +32,20 @@ int qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, in
                     size_t b_zp_len, const int32_t* a_rowsum, const icx_chain* chain, float* const* ys,
                     int n_seg, void* ws, size_t ws_bytes);
 
+// A quantized linear whose f32 output is read only by a DynamicQuantizeLinear, as one launch:
+// y, y_scale, y_zp are what the DQL of icx_qlinear_f32's Y would give, bit for bit, and Y
+// itself is never written.  Int8 packed weight without zero point (no row term), column-only
+// chain, K % 128 == 0, N % 192 == 0, 16-byte aligned A, B and y, at most kQoutMaxBlocks
+// 256x192 tiles.  `sync`: kQoutSyncBytes of device memory, zero before its first use and
+// left valid by every call; calls that share it must not overlap.  Returns
+// ICX_ERR_UNSUPPORTED, having launched nothing, for a shape outside the kernel or a grid
+// that would not be resident at once.
+constexpr int kQoutMaxBlocks = 768;  // one waiting thread per block in a 768-thread block
+constexpr size_t kQoutSyncBytes = 256 + 16 * (size_t)kQoutMaxBlocks;
+int qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int b_dtype, const int32_t* b_colsum,
+                size_t M, size_t K, size_t N, const void* a_zp, const icx_chain* chain, uint8_t* y,
+                float* y_scale, uint8_t* y_zp, unsigned* sync);
+
 // DynamicQuantizeLinear of x from the n_part partials its producer left: one launch (the
 // quantize pass of icx_dynamic_quantize_linear, which folds them).
 int dql_from_parts(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,

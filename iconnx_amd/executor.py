@@ -162,7 +162,8 @@ class GpuGraphExecutor:
             if "buffer has" not in msg or size > (1 << 26):
                 check(rc)
             size *= 4
-        entries, rowsums, ranges = [], [], []
+        entries, rowsums, ranges, quant_out = [], [], [], {}
+        self._quant_launches = 0
         for line in buf.value.decode().splitlines():
             parts = line.split()
             if parts[0] == "rowsum":
@@ -171,12 +172,26 @@ class GpuGraphExecutor:
             if parts[0] == "range":
                 ranges.append(parts[1])
                 continue
+            if parts[0] == "quantout":
+                quant_out[parts[1]] = parts[2]
+                continue
+            if parts[0] == "quantout-launches":
+                self._quant_launches = int(parts[1])
+                continue
             extra = dict(p.split("=", 1) for p in parts[4:])
             entries.append(PlanEntry(parts[0], parts[1], parts[2], parts[3],
                                      int(extra.get("steps", 0)), extra.get("out"),
                                      extra.get("wzp") == "folded", extra.get("group")))
         self._range_inputs = ranges
+        self._quant_out = quant_out
         return entries, rowsums
+
+    def quantized_outputs(self):
+        """Quantized-linear outputs read only by a DynamicQuantizeLinear, mapped to that
+        node: the GEMM writes the DQL's outputs itself when the shape allows, and the f32
+        tensor is never formed.  Second value: how many GEMM launches so far did that."""
+        self.plan()
+        return dict(self._quant_out), self._quant_launches
 
     def range_inputs(self):
         """DynamicQuantizeLinear inputs whose producing kernel (LayerNorm, attention, a
