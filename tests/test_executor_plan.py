@@ -382,3 +382,47 @@ def test_encoder_dql_ranges_come_from_producers():
         want |= {t["ctx"], t["x1"], t["h"]}
     assert got == want
     assert names[0]["x"] not in got  # the graph input has no producing kernel
+
+
+def _two_linears(w2_dtype=np.int8, w2_zp=0, w1_dtype=np.int8, w1_zp=0, extra_reader=False):
+    ex = GpuGraphExecutor()
+    ex.add_input("x", [None, 8])
+    y1 = linear(ex, w_zp=w1_zp, prefix="l1", w_dtype=w1_dtype, N=8)
+    y2 = linear(ex, w_zp=w2_zp, prefix="l2", x=y1, w_dtype=w2_dtype)
+    ex.add_output(y2)
+    if extra_reader:
+        ex.add_initializer("one", np.ones(8, np.float32))
+        ex.add_node("tap", "Mul", [y1, "one"], ["tapped"])
+        ex.add_output("tapped")
+    return ex, y1
+
+
+def test_quantized_output_selection():
+    """A quantized-linear head whose output only a DynamicQuantizeLinear reads may write that
+    DQL's outputs itself: Int8 weight without zero point, no other reader, the f32 tensor not
+    requested, and no GEMM reading row sums of the quantized tensor."""
+    ex, y1 = _two_linears()
+    assert ex.quantized_outputs() == ({y1: "l2.dql"}, 0)
+    # the consumer's weight is uint8: it reads the DQL's row sums, which only the DQL writes
+    assert _two_linears(w2_dtype=np.uint8)[0].quantized_outputs()[0] == {}
+    assert _two_linears(w2_zp=np.arange(16) - 8)[0].quantized_outputs()[0] == {}
+    # the producer's weight keeps a row term (uint8 or a nonzero zero point)
+    assert _two_linears(w1_dtype=np.uint8)[0].quantized_outputs()[0] == {}
+    assert _two_linears(w1_zp=np.arange(8) - 4)[0].quantized_outputs()[0] == {}
+    # another reader of the f32 output (the fused head then stops before it)
+    assert _two_linears(extra_reader=True)[0].quantized_outputs()[0] == {}
+    # the f32 output requested
+    ex, y1 = _two_linears()
+    ex.add_output(y1)
+    assert ex.quantized_outputs()[0] == {}
+
+
+def test_encoder_ffn_up_quantizes_its_own_output():
+    ex = GpuGraphExecutor()
+    out, names, _ = graphs.encoder_graph(ex, layers=2)
+    ex.add_output(out)
+    planned, _ = ex.quantized_outputs()
+    assert set(planned) == {t["h"] for t in names}  # the erf-GELU outputs, one per layer
+    entries, _ = ex.plan()
+    dql_of = {e.node: e for e in entries if e.op_type == "DynamicQuantizeLinear"}
+    assert all(d in dql_of for d in planned.values())
