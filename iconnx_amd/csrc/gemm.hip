@@ -29,6 +29,7 @@
 #include "chain.hpp"
 #include "dql_core.hpp"
 #include "internal.hpp"
+#include "qexchange.hpp"
 
 namespace {
 
@@ -547,16 +548,7 @@ gemm_i8_dma_kernel(GemmArgs g) {
 // through an LDS byte tile with 16-byte row stores.  The f32 output is never written.  No
 // row term: the host requires an int8 weight whose zero point was folded away.
 //
-// q_sync: word 0 the launch number E, word 1 the finish count (bits 0-15) and the number of
-// blocks whose wait ran out (bits 16-31); from byte 256, two 64-bit slots per block: min
-// and max, each tagged with E + 1 in its high half, so that a reader takes a slot as this
-// launch's as soon as it sees the tag (zeroed memory never matches).  Every block reads E
-// before it counts its finish, and the last block to finish increments E, so all blocks of
-// a launch agree on it.  All accesses to q_sync are device-scope atomics (they bypass the
-// per-XCD L2s): no release / acquire fences, whose per-block L2 write-back and invalidate
-// would cost more than the exchange.  If a wait runs out (blocks not co-resident) that
-// block's tile is written as 0 and the last block to finish writes the scale as NaN, so
-// that every consumer shows the failure.
+// The exchange (q_sync, bounded waits, NaN scale on failure) is qexchange.hpp's.
 template <int BM, int BN, int WGM, int WGN, int CH>
 __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
                                               int8_t* smem, int m0, int n0, unsigned tag) {
@@ -617,35 +609,9 @@ __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM 
         }
     }
     icx::dql::block_minmax<NT>(mn, mx);
-    unsigned long long* slot = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(g.q_sync) + 256);
-    const unsigned long long hi_tag = (unsigned long long)tag << 32;
-    if (t == 0) {
-        __hip_atomic_store(slot + 2 * blockIdx.x, hi_tag | __float_as_uint(mn), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(slot + 2 * blockIdx.x + 1, hi_tag | __float_as_uint(mx), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // thread b waits for block b's pair (G <= NT, checked by the host)
-    float gmn = 0.0f, gmx = 0.0f;
-    int late = 0;
-    if (t < (int)gridDim.x) {
-        unsigned long long lo, hi;
-        for (int it = 0;; ++it) {
-            lo = __hip_atomic_load(slot + 2 * t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            hi = __hip_atomic_load(slot + 2 * t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if ((unsigned)(lo >> 32) == tag && (unsigned)(hi >> 32) == tag) break;
-            if (it >= g.q_spin) {
-                late = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(8);
-        }
-        icx::dql::acc_minmax(__uint_as_float((uint32_t)lo), gmn, gmx);
-        icx::dql::acc_minmax(__uint_as_float((uint32_t)hi), gmn, gmx);
-    }
-    const bool ok = __syncthreads_or(late) == 0;
-    icx::dql::block_minmax<NT>(gmn, gmx);
-    const icx::dql::DqlParams p = icx::dql::make_params(gmn, gmx);
+    if (t == 0) icx::qx::publish(g.q_sync, tag, mn, mx);
+    bool ok;
+    const icx::dql::DqlParams p = icx::qx::gather<NT>(g.q_sync, tag, g.q_spin, ok);
     // quantize into the LDS byte tile [BM][QS]
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
@@ -672,19 +638,7 @@ __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM 
             *reinterpret_cast<uint4*>(g.qy + (size_t)grow * g.N + n0 + 16 * c16) =
                 *reinterpret_cast<const uint4*>(qs + r * QS + 16 * c16);
     }
-    // the last block to finish writes the scale and zero point (NaN and 0 if any block's
-    // wait ran out) and starts the next launch number
-    if (t == 0) {
-        unsigned* fin = g.q_sync + 1;
-        const unsigned old = __hip_atomic_fetch_add(fin, ok ? 1u : 0x10001u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((old & 0xffffu) == gridDim.x - 1) {
-            const bool err = !ok || (old >> 16) != 0;
-            *g.q_scale = err ? __builtin_nanf("") : (float)p.s;
-            *g.q_zp = err ? (uint8_t)0 : (uint8_t)p.zp;
-            __hip_atomic_store(fin, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(g.q_sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
+    if (t == 0) icx::qx::finish(g.q_sync, ok, p, g.q_scale, g.q_zp);
 }
 
 // ---- main loop B2: LDS DMA with 128-byte K rows (256x256 tile, K % 128 == 0) ------------
@@ -744,7 +698,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
     const int KT = g.K / ROWB;
     // the launch number of a quantized-output launch, read before the main loop hides its latency
     unsigned q_tag = 0;
-    if constexpr (QOUT != 0) q_tag = __hip_atomic_load(g.q_sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    if constexpr (QOUT != 0) q_tag = icx::qx::read_tag(g.q_sync);
     auto issue = [&](int buf, int kt) {
         if (!copier) return;
         const int k0 = kt * ROWB;

@@ -40,8 +40,8 @@ int qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, in
 // left valid by every call; calls that share it must not overlap.  Returns
 // ICX_ERR_UNSUPPORTED, having launched nothing, for a shape outside the kernel or a grid
 // that would not be resident at once.
-constexpr int kQoutMaxBlocks = 768;  // one waiting thread per block in a 768-thread block
-constexpr size_t kQoutSyncBytes = 256 + 16 * (size_t)kQoutMaxBlocks;
+constexpr int kQoutMaxBlocks = 1024;  // blocks of one quantized-output launch
+constexpr size_t kQoutSyncBytes = 256 + 16 * (size_t)kQoutMaxBlocks;  // qexchange.hpp's layout
 int qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int b_dtype, const int32_t* b_colsum,
                 size_t M, size_t K, size_t N, const void* a_zp, const icx_chain* chain, uint8_t* y,
                 float* y_scale, uint8_t* y_zp, unsigned* sync);

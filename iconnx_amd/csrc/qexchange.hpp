@@ -1,0 +1,91 @@
+// The range exchange of a kernel that quantizes its own output: a producer of a
+// DynamicQuantizeLinear's input whose blocks are all resident at once (one wave of blocks)
+// can compute the per-tensor scale and zero point itself, once every block knows every
+// other block's (min, max), and write the DQL's u8 output directly.
+//
+// Exchange buffer (kQoutSyncBytes, zeroed before its first use, left valid by every launch):
+//   word 0    launch number E
+//   word 1    blocks past the exchange (bits 0-15) and those whose wait ran out (bits 16-31)
+//   byte 256+ two 64-bit slots per block, min and max, each tagged with E + 1 in its high
+//             half, so a reader takes a slot as this launch's as soon as it sees the tag
+//             (zeroed memory never matches).
+// Every block reads E before it publishes, and the last block past the exchange increments
+// E, so all blocks of a launch agree on it.  Every access is a device-scope atomic (they
+// bypass the per-XCD L2s); no release / acquire fences, whose per-block L2 write-back and
+// invalidate cost more than the exchange.  Waits are bounded: a block whose wait runs out
+// must write its part of y as 0, and the last block past the exchange then writes the scale
+// as NaN, so that every consumer shows the failure.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "dql_core.hpp"
+
+namespace icx {
+namespace qx {
+
+__device__ __forceinline__ unsigned long long* slots(unsigned* sync) {
+    return reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(sync) + 256);
+}
+
+// E + 1 for this launch; read it early (before the main work) to hide the latency.
+__device__ __forceinline__ unsigned read_tag(unsigned* sync) {
+    return __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+}
+
+// Thread 0 of a block: publish the block's (min, max).
+__device__ __forceinline__ void publish(unsigned* sync, unsigned tag, float mn, float mx) {
+    const unsigned long long hi = (unsigned long long)tag << 32;
+    unsigned long long* s = slots(sync) + 2 * blockIdx.x;
+    __hip_atomic_store(s, hi | __float_as_uint(mn), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(s + 1, hi | __float_as_uint(mx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every thread of a block of NT threads: wait for all gridDim.x blocks' pairs (thread t polls
+// blocks t, t + NT, ...), fold them as the DQL launch does and return its parameters.
+// `ok` is false in every thread if any wait of this block ran out.
+template <int NT>
+__device__ __forceinline__ dql::DqlParams gather(unsigned* sync, unsigned tag, int spin, bool& ok) {
+    const unsigned long long* s = slots(sync);
+    float mn = 0.0f, mx = 0.0f;
+    int late = 0;
+    for (int b = threadIdx.x; b < (int)gridDim.x; b += NT) {
+        unsigned long long lo, hi;
+        for (int it = 0;; ++it) {
+            lo = __hip_atomic_load(s + 2 * b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            hi = __hip_atomic_load(s + 2 * b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((unsigned)(lo >> 32) == tag && (unsigned)(hi >> 32) == tag) break;
+            if (it >= spin) {
+                late = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(8);
+        }
+        dql::acc_minmax(__uint_as_float((uint32_t)lo), mn, mx);
+        dql::acc_minmax(__uint_as_float((uint32_t)hi), mn, mx);
+    }
+    ok = __syncthreads_or(late) == 0;
+    dql::block_minmax<NT>(mn, mx);
+    return dql::make_params(mn, mx);
+}
+
+// Thread 0 of a block, after its part of y is written: count the block out; the last one
+// writes the scale and zero point (NaN and 0 if any wait ran out) and starts the next
+// launch number.
+__device__ __forceinline__ void finish(unsigned* sync, bool ok, const dql::DqlParams& p, float* y_scale,
+                                       uint8_t* y_zp) {
+    const unsigned old = __hip_atomic_fetch_add(sync + 1, ok ? 1u : 0x10001u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if ((old & 0xffffu) == gridDim.x - 1) {
+        const bool err = !ok || (old >> 16) != 0;
+        *y_scale = err ? __builtin_nanf("") : (float)p.s;
+        *y_zp = err ? (uint8_t)0 : (uint8_t)p.zp;
+        __hip_atomic_store(sync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+}  // namespace qx
+}  // namespace icx
