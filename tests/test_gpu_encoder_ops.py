@@ -107,6 +107,25 @@ def test_qlinear_with_gelu_epilogue():
     assert rel_err(y, want) < 1e-6
 
 
+def test_qlinear_with_gelu_epilogue_narrow_tile():
+    """The erf-GELU epilogue on the 128x96 tile (4096 x 768 x 768: 256 tiles)."""
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((4096, 768)).astype(np.float32)
+    w = rng.integers(-127, 128, (768, 768)).astype(np.int8)
+    w_scale, bias = np.float32(0.01), (0.02 * rng.standard_normal(768)).astype(np.float32)
+    xq, xs, xzp, rs = ops.gpu_dynamic_quantize_linear(dev(x), rowsum_row_len=768)
+    pw = ops.PackedWeight(dev(w))
+    c0, c1, c2 = (dev(np.array(v, np.float32)) for v in (1.4142135, 1.0, 0.5))
+    epi = [("Mul", (xs, dev(np.array(w_scale))), False), ("Add", dev(bias), False),
+           ("Save", None, False), ("Div", c0, False), ("Erf", None, False), ("Add", c1, False),
+           ("MulSaved", None, False), ("Mul", c2, False)]
+    y = host(ops.gpu_qlinear(xq, pw, xzp, None, epilogue=epi, a_rowsum=rs))
+    t = oracle.qlinear_graph(x, w, np.array(0, np.int8), np.array(w_scale), bias)["linear"]
+    want = oracle.mul(oracle.mul(t, oracle.add(oracle.erf(oracle.div(t, np.float32(1.4142135))),
+                                               np.float32(1.0))), np.float32(0.5))
+    assert rel_err(y, want) < 1e-6
+
+
 def test_transpose_exact():
     rng = np.random.default_rng(3)
     x = rng.standard_normal((2, 3, 4, 5)).astype(np.float32)

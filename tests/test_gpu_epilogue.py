@@ -191,7 +191,7 @@ def test_dequantize_i32_large_values_follow_cpu_semantics():
 
 
 def test_ffn_down_shape_fused_epilogue():
-    """FFN-down shape (K = 3072; 768 tiles of 64x64) with the dequant scale, bias and a
+    """FFN-down shape (K = 3072; 256 tiles of 128x96) with the dequant scale, bias and a
     Sub/Div/Mul chain with an operand on the left, bit-exact vs the oracle's op-by-op graph;
     per-channel scale and zero point included."""
     rng = np.random.default_rng(31)

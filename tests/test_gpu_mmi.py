@@ -171,7 +171,7 @@ def test_persistent_kernel_shapes(adt, bdt):
 
 
 def test_encoder_ffn_down_shape():
-    """The DistilBERT FFN-down GEMM (4096 x 3072 x 768, 64x64 tiles) at full size: every
+    """The DistilBERT FFN-down GEMM (4096 x 3072 x 768, 128x96 tiles) at full size: every
     element against the exact float64 product, rows against the oracle."""
     rng = np.random.default_rng(29)
     a = rng.integers(0, 256, (4096, 3072)).astype(np.uint8)
@@ -212,4 +212,20 @@ def test_mid_tile_kernel_ragged(M):
     got = gpu_mmi(a, b, azp, bzp, packed=True)
     np.testing.assert_array_equal(got.astype(np.int64), _exact_f64(a, b, azp, bzp))
     for r in (0, 255, 256, 3999, M - 1):
+        assert np.array_equal(got[r:r + 1], oracle.matmul_integer(a[r:r + 1], b, azp, bzp)), r
+
+
+# 128x96 tiles (12 waves of 32x32) when they give every CU at least one: N % 96 == 0,
+# K % 128 == 0, cdiv(M, 128) * N / 96 >= CUs, not taken by a larger tile; ragged M exercises
+# the clamped rows.
+@pytest.mark.parametrize("M,K", [(4000, 256), (4100, 768)])
+def test_narrow_tile_kernel_ragged(M, K):
+    rng = np.random.default_rng(41 + M)
+    N = 768
+    a = rng.integers(0, 256, (M, K)).astype(np.uint8)
+    b = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    azp, bzp = np.array(7, np.uint8), np.array(5, np.int8)
+    got = gpu_mmi(a, b, azp, bzp, packed=True)
+    np.testing.assert_array_equal(got.astype(np.int64), _exact_f64(a, b, azp, bzp))
+    for r in (0, 127, 128, 3999, M - 1):
         assert np.array_equal(got[r:r + 1], oracle.matmul_integer(a[r:r + 1], b, azp, bzp)), r
