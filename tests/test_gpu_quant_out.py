@@ -136,3 +136,43 @@ def test_quantized_output_capture_and_replay():
         check_same(got, want[i], "replay %d" % rep)
         _ = (xs[i] * 2.0).sum().item()
         torch.cuda.synchronize()
+
+
+def build_int8_act(ex, K, N, seed):
+    """MatMulInteger over an Int8 graph input with an Int8 zero point, then the dequant, a
+    bias and a column-vector Div / Mul chain, then a DQL."""
+    rng = np.random.default_rng(seed)
+    inits = {
+        "w": rng.integers(-127, 128, (K, N)).astype(np.int8),
+        "a_zp": np.array(-3, np.int8),
+        "s": np.array(0.0037, np.float32),
+        "bias": (0.05 * rng.standard_normal(N)).astype(np.float32),
+        "d": rng.uniform(0.5, 2.5, N).astype(np.float32),
+        "m": rng.uniform(0.5, 1.5, N).astype(np.float32),
+    }
+    ex.add_input("a", [None, K])
+    for name, arr in inits.items():
+        ex.add_initializer(name, arr)
+    ex.add_node("mm", "MatMulInteger", ["a", "w", "a_zp"], ["acc"])
+    ex.add_node("cast", "Cast", ["acc"], ["accf"], {"to": 1})
+    ex.add_node("deq", "Mul", ["accf", "s"], ["l0"])
+    ex.add_node("bias_add", "Add", ["l0", "bias"], ["l1"])
+    ex.add_node("div", "Div", ["l1", "d"], ["l2"])
+    ex.add_node("mul", "Mul", ["l2", "m"], ["h"])
+    ex.add_node("dql_h", "DynamicQuantizeLinear", ["h"], ["hq", "hs", "hzp"])
+    return "h"
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 768, 3072), (257, 384, 576)])
+def test_quantized_output_int8_activations_and_column_division(M, K, N):
+    a = np.random.default_rng(M).integers(-128, 128, (M, K)).astype(np.int8)
+    ref_ex, fused_ex = GpuGraphExecutor(), GpuGraphExecutor()
+    h = build_int8_act(ref_ex, K, N, seed=N)
+    build_int8_act(fused_ex, K, N, seed=N)
+    ref = ref_ex.run({"a": a}, [h, "hq", "hs", "hzp"])
+    yq, ys, yzp = oracle.dynamic_quantize_linear(ref[h])
+    check_same(ref, {"hq": yq, "hs": ys, "hzp": yzp}, "separate DQL vs oracle")
+    fused = fused_ex.run({"a": a}, ["hq", "hs", "hzp"])
+    planned, launches = fused_ex.quantized_outputs()
+    assert planned == {h: "dql_h"} and launches == 1
+    check_same(fused, ref, "fused vs separate (int8 activations)")
