@@ -102,9 +102,13 @@ def test_quantized_output_repeated_runs_and_smaller_input():
     assert fused_ex.quantized_outputs()[1] == 3
 
 
-def test_quantized_output_falls_back_outside_the_kernel():
-    """N not a multiple of 192: the GEMM writes f32 and the DQL runs as its own launch."""
-    K, N, M = 256, 200, 64
+@pytest.mark.parametrize("M,K,N", [
+    (64, 256, 200),     # N not a multiple of 192
+    (8192, 768, 3072),  # 512 tiles of 256x192: more than can be resident at once
+])
+def test_quantized_output_falls_back_outside_the_kernel(M, K, N):
+    """Outside the fused kernel (shape, or a grid that would not be resident at once) the GEMM
+    writes f32 and the DQL runs as its own launch; the results are the same."""
     x = np.random.default_rng(3).standard_normal((M, K)).astype(np.float32)
     fused_ex, ref_ex = GpuGraphExecutor(), GpuGraphExecutor()
     h = build(fused_ex, K, N, True, seed=5)
