@@ -595,16 +595,22 @@ __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM 
                 const float o = sop[k * BN + c];
                 return make_float4(o, o, o, o);
             });
-            // register 4 q + e holds row 8 q + 4 (lane >> 5) + e of this 32-row slab
+            // register 4 q + e holds row 8 q + 4 (lane >> 5) + e of this 32-row slab; only the
+            // last row of tiles can reach past M (a uniform test per tile)
             const int rbase = m0 + wm * WM + i * 32 + 4 * (lane >> 5);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float* w = reinterpret_cast<const float*>(&v[q]);
+                if (m0 + BM <= g.M) {
+                    mn = fminf(mn, fminf(fminf(w[0], w[1]), fminf(w[2], w[3])));
+                    mx = fmaxf(mx, fmaxf(fmaxf(w[0], w[1]), fmaxf(w[2], w[3])));
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (rbase + 8 * q + e < g.M) icx::range_acc(w[e], mn, mx);
-                    acc[i][j][4 * q + e] = __float_as_int(w[e]);
+                    for (int e = 0; e < 4; ++e)
+                        if (rbase + 8 * q + e < g.M) icx::range_acc(w[e], mn, mx);
                 }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] = __float_as_int(w[e]);
             }
         }
     }
