@@ -512,6 +512,7 @@ def main():
         # the metric's second part, encoder seq/s, measured in the same run
         enc = EncoderRunner()
         ms_e, _ = time_replays(enc.step, 50, 5, torch)
+        enc.ex.check_status()  # a quantized-output launch that failed on the device raises
         out["encoder"] = {"metric": "encoder seq/s", "value": round(enc.B / (ms_e * 1e-3), 1),
                           "unit": "seq/s", "ms_per_forward": round(ms_e, 4),
                           "int8_TOPS": round(enc.int8_ops / (ms_e * 1e-3) / 1e12, 2),
@@ -531,6 +532,7 @@ ENCODER_WORKLOAD = ("cfg3: 6-layer DistilBERT-int8-shaped encoder, hidden 768, 1
 def main_encoder(args, torch):
     enc = EncoderRunner()
     ms_step, wall = time_replays(enc.step, args.steps, args.warmup, torch)
+    enc.ex.check_status()
     seq_s = enc.B / (ms_step * 1e-3)
     # dominant kernel: the FFN-up GEMM with its erf-GELU epilogue, R launches in one graph
     ffn = FfnUpGeluRunner(enc.params[0])

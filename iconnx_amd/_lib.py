@@ -76,6 +76,8 @@ SIGNATURES = {
     "icx_graph_pool_stats": ([P, P, P, P], I),
     "icx_graph_capture": ([P, P], I),
     "icx_graph_replay": ([P, P], I),
+    "icx_graph_status": ([P, P], I),
+    "icx_debug_qout_fault": ([I], None),
 }
 
 

@@ -128,6 +128,7 @@ extern "C" const char* icx_status_str(int status) {
         case ICX_ERR_WORKSPACE: return "workspace too small";
         case ICX_ERR_HIP: return "HIP runtime error";
         case ICX_ERR_UNSUPPORTED: return "unsupported";
+        case ICX_ERR_KERNEL: return "kernel reported a failure on the device";
         default: return "unknown status";
     }
 }

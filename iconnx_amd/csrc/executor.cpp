@@ -2217,6 +2217,31 @@ extern "C" int icx_graph_replay(icx_graph* g, icx_stream_t stream) {
     return ICX_OK;
 }
 
+extern "C" int icx_graph_status(icx_graph* g, icx_stream_t stream) {
+    icx::clear_error();
+    if (!g) ICX_FAIL(ICX_ERR_INVALID_ARG, "status: null graph");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (!g->qsync) {
+        ICX_HIP_CHECK(hipStreamSynchronize(s));
+        return ICX_OK;
+    }
+    // the exchange buffer's sticky word: launches whose range exchange gave up
+    unsigned* word = g->qsync + icx::kQoutErrWord;
+    unsigned failed = 0;
+    ICX_HIP_CHECK(hipMemcpyAsync(&failed, word, sizeof failed, hipMemcpyDeviceToHost, s));
+    ICX_HIP_CHECK(hipStreamSynchronize(s));
+    if (failed) {
+        ICX_HIP_CHECK(hipMemsetAsync(word, 0, sizeof failed, s));
+        ICX_HIP_CHECK(hipStreamSynchronize(s));
+        ICX_FAIL(ICX_ERR_KERNEL,
+                 "QuantizedLinear+DynamicQuantizeLinear: %u launch(es) since the last status check had a block "
+                 "whose wait for the other blocks' ranges ran out (they were not all resident, e.g. other work "
+                 "held CUs); their quantized outputs are invalid (y = 0, scale = NaN)",
+                 failed);
+    }
+    return ICX_OK;
+}
+
 extern "C" int icx_graph_get_output(icx_graph* g, const char* name, int* dtype, int* rank,
                                     int64_t* dims, const void** device_ptr) {
     icx::clear_error();

@@ -26,6 +26,8 @@
 // registers (main loop A: any K and alignment).  Blocks are remapped so each XCD
 // (blockIdx % 8) works on a contiguous, M-grouped range of tiles that shares A/B panels in
 // its own L2.
+#include <atomic>
+
 #include "chain.hpp"
 #include "dql_core.hpp"
 #include "internal.hpp"
@@ -75,6 +77,7 @@ struct GemmArgs {
     uint8_t* q_zp;
     unsigned* q_sync;
     int q_spin;
+    unsigned q_poison;  // 0; the fault test hook makes every wait expect tag ^ q_poison
 };
 
 // Output of the tile whose first column is n0: base pointer, row stride and the global
@@ -617,7 +620,7 @@ __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM 
     icx::dql::block_minmax<NT>(mn, mx);
     if (t == 0) icx::qx::publish(g.q_sync, tag, mn, mx);
     bool ok;
-    const icx::dql::DqlParams p = icx::qx::gather<NT>(g.q_sync, tag, g.q_spin, ok);
+    const icx::dql::DqlParams p = icx::qx::gather<NT>(g.q_sync, tag ^ g.q_poison, g.q_spin, ok);
     // quantize into the LDS byte tile [BM][QS]
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
@@ -1536,6 +1539,13 @@ int icx::qlinear_f32(hipStream_t s, const void* A, int a_dtype, const void* B, i
                        chain, Y, OUT_F32, ws, ws_bytes, "QLinear", part, n_part);
 }
 
+// icx_debug_qout_fault: > 0 makes every quantized-output launch wait for a tag that no block
+// publishes, giving up after that many polls (every block then exits through the failure
+// path); 0 is normal operation.
+static std::atomic<int> g_qout_fault_spin{0};
+
+extern "C" void icx_debug_qout_fault(int spin) { g_qout_fault_spin.store(spin > 0 ? spin : 0); }
+
 int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int b_dtype,
                      const int32_t* b_colsum, size_t M, size_t K, size_t N, const void* a_zp,
                      const icx_chain* chain, uint8_t* y, float* y_scale, uint8_t* y_zp, unsigned* sync) {
@@ -1580,6 +1590,11 @@ int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp
     g.q_zp = y_zp;
     g.q_sync = sync;
     g.q_spin = 1 << 20;
+    g.q_poison = 0;
+    if (const int f = g_qout_fault_spin.load(std::memory_order_relaxed)) {  // test hook
+        g.q_spin = f;
+        g.q_poison = 0x80000000u;
+    }
     if (icx::chain_mode(g.chain) == 2) return launch_qout<CH_COL_EXT>(blocks, s, g);
     return launch_qout<CH_COL>(blocks, s, g);
 }

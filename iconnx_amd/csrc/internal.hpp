@@ -42,6 +42,7 @@ int qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, in
 // that would not be resident at once.
 constexpr int kQoutMaxBlocks = 1024;  // blocks of one quantized-output launch
 constexpr size_t kQoutSyncBytes = 256 + 16 * (size_t)kQoutMaxBlocks;  // qexchange.hpp's layout
+constexpr int kQoutErrWord = 2;  // word of that buffer counting launches whose exchange failed
 int qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int b_dtype, const int32_t* b_colsum,
                 size_t M, size_t K, size_t N, const void* a_zp, const icx_chain* chain, uint8_t* y,
                 float* y_scale, uint8_t* y_zp, unsigned* sync);

@@ -6,6 +6,8 @@
 // Exchange buffer (kQoutSyncBytes, zeroed before its first use, left valid by every launch):
 //   word 0    launch number E
 //   word 1    blocks past the exchange (bits 0-15) and those whose wait ran out (bits 16-31)
+//   word 2    launches that ended with a wait run out (sticky: only the host clears it, after
+//             reading it, so a failure of any launch reaches the caller as an error status)
 //   byte 256+ two 64-bit slots per block, min and max, each tagged with E + 1 in its high
 //             half, so a reader takes a slot as this launch's as soon as it sees the tag
 //             (zeroed memory never matches).
@@ -14,7 +16,12 @@
 // bypass the per-XCD L2s); no release / acquire fences, whose per-block L2 write-back and
 // invalidate cost more than the exchange.  Waits are bounded: a block whose wait runs out
 // must write its part of y as 0, and the last block past the exchange then writes the scale
-// as NaN, so that every consumer shows the failure.
+// as NaN, so that every consumer shows the failure, and counts the launch in word 2.
+//
+// All blocks of a launch must be resident together for the waits to end in time.  The host
+// sizes the launch from the occupancy calculator, which knows nothing of other kernels that
+// may occupy CUs at the same time (another stream, another process): that is the case the
+// bounded waits and word 2 exist for.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,6 +29,7 @@
 #include <cstdint>
 
 #include "dql_core.hpp"
+#include "internal.hpp"
 
 namespace icx {
 namespace qx {
@@ -45,7 +53,8 @@ __device__ __forceinline__ void publish(unsigned* sync, unsigned tag, float mn, 
 
 // Every thread of a block of NT threads: wait for all gridDim.x blocks' pairs (thread t polls
 // blocks t, t + NT, ...), fold them as the DQL launch does and return its parameters.
-// `ok` is false in every thread if any wait of this block ran out.
+// `ok` is false in every thread if any wait of this block ran out.  `tag` is the value
+// published (read_tag); a test hook passes a tag that no block publishes instead.
 template <int NT>
 __device__ __forceinline__ dql::DqlParams gather(unsigned* sync, unsigned tag, int spin, bool& ok) {
     const unsigned long long* s = slots(sync);
@@ -82,6 +91,7 @@ __device__ __forceinline__ void finish(unsigned* sync, bool ok, const dql::DqlPa
         const bool err = !ok || (old >> 16) != 0;
         *y_scale = err ? __builtin_nanf("") : (float)p.s;
         *y_zp = err ? (uint8_t)0 : (uint8_t)p.zp;
+        if (err) __hip_atomic_fetch_add(sync + kQoutErrWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(sync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

@@ -254,7 +254,18 @@ class GpuGraphExecutor:
         """As the reference's ``run``: host arrays in (device tensors also accepted), host
         arrays (numpy) out."""
         dev = self.run_device(inputs, output_names)
-        return {k: v.cpu().numpy() for k, v in dev.items()}
+        out = {k: v.cpu().numpy() for k, v in dev.items()}
+        self.check_status()
+        return out
+
+    def check_status(self):
+        """Synchronise the current stream, then raise IconnxError (ICX_ERR_KERNEL) if a
+        kernel of an earlier run or replay recorded a failure on the device — the reference
+        surfaces failed launches as CudaError::Kernel (src/cuda/executor/mod.rs:169-186).
+        ``run`` calls this; after ``run_device`` or ``replay`` a caller calls it before
+        trusting the outputs."""
+        torch = _torch()
+        check(self._L.icx_graph_status(self._g, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
 
     def capture(self, inputs, output_names):
         """Record one run into a HIP graph on ``torch.cuda.current_stream()``.  ``inputs``

@@ -32,6 +32,7 @@ typedef enum {
     ICX_ERR_WORKSPACE = 4,   /* workspace missing or smaller than the *_workspace_size */
     ICX_ERR_HIP = 5,         /* a HIP runtime call failed */
     ICX_ERR_UNSUPPORTED = 6, /* outside what this build implements */
+    ICX_ERR_KERNEL = 7,      /* a kernel reported a failure on the device (icx_graph_status) */
 } icx_status;
 
 /* ICX_I64 is accepted for graph initializers only (Reshape shapes, read on the host). */
@@ -258,6 +259,24 @@ int icx_graph_pool_stats(icx_graph* g, int64_t* hipmallocs, int64_t* hits, int64
 int icx_graph_capture(icx_graph* g, icx_stream_t stream);
 /* Launch the recorded run on `stream`; outputs as after icx_graph_run. */
 int icx_graph_replay(icx_graph* g, icx_stream_t stream);
+/* Synchronise `stream`, then report failures that kernels of earlier runs / replays of this
+ * graph recorded on the device; the reference surfaces a failed launch as
+ * CudaError::Kernel (src/cuda/executor/mod.rs:169-186).  icx_graph_run and icx_graph_replay
+ * only enqueue work, so a failure that happens on the device can only be seen here.  The one
+ * such failure today: a quantized linear that quantizes its own output (the 'quantout'
+ * pairs of icx_graph_plan) needs every block of its launch resident at once; the launch is
+ * sized from the occupancy calculator, so other work on the GPU at the same time can keep
+ * blocks from being scheduled, and a block whose bounded wait for the others runs out
+ * writes its part of the u8 output as 0 and the scale as NaN.  Returns ICX_ERR_KERNEL (and
+ * clears the record) if that happened in any launch since the last call, else ICX_OK. */
+int icx_graph_status(icx_graph* g, icx_stream_t stream);
+
+/* ---- test hooks ------------------------------------------------------------------------
+ * No counterpart in the reference.  icx_debug_qout_fault(spin): with spin > 0, every later
+ * quantized-output launch of this process waits for a tag that no block publishes and gives
+ * up after `spin` polls, so every block takes the failure path and exits normally (for
+ * testing icx_graph_status); 0 restores normal launches. */
+void icx_debug_qout_fault(int spin);
 
 #ifdef __cplusplus
 }

@@ -180,3 +180,42 @@ def test_quantized_output_int8_activations_and_column_division(M, K, N):
     planned, launches = fused_ex.quantized_outputs()
     assert planned == {h: "dql_h"} and launches == 1
     check_same(fused, ref, "fused vs separate (int8 activations)")
+
+
+def test_exchange_that_gives_up_is_an_error_status():
+    """A launch in which a block's bounded wait for the others' ranges runs out is reported
+    as ICX_ERR_KERNEL by the status check (the reference's CudaError::Kernel,
+    src/cuda/executor/mod.rs:169-186), not only as a NaN scale.  The host-side test hook makes
+    every wait expect a tag no block publishes, with a short bound, so every block takes the
+    failure path and exits normally.  The record is cleared by the check: a normal run after
+    it is correct and reports no error."""
+    from iconnx_amd._lib import IconnxError, lib
+
+    K, N, M = 768, 3072, 1024
+    x = np.random.default_rng(21).standard_normal((M, K)).astype(np.float32)
+    ex, ref_ex = GpuGraphExecutor(), GpuGraphExecutor()
+    h = build(ex, K, N, True, seed=13)
+    build(ref_ex, K, N, True, seed=13)
+    want = ref_ex.run({"x": x}, [h, "hq", "hs", "hzp"])
+    L = lib()
+    L.icx_debug_qout_fault(64)
+    try:
+        got = ex.run_device({"x": x}, ["hq", "hs", "hzp"])
+        with pytest.raises(IconnxError) as e:
+            ex.check_status()
+    finally:
+        L.icx_debug_qout_fault(0)
+    assert e.value.status == 7 and "1 launch" in str(e.value)
+    assert ex.quantized_outputs()[1] == 1
+    assert np.isnan(got["hs"].cpu().numpy()) and not got["hq"].cpu().numpy().any()
+    ex.check_status()  # cleared
+    check_same(ex.run({"x": x}, ["hq", "hs", "hzp"]), want, "normal run after the failure")
+    # run() itself raises when the failure happens in it
+    L.icx_debug_qout_fault(64)
+    try:
+        with pytest.raises(IconnxError) as e:
+            ex.run({"x": x}, ["hq", "hs", "hzp"])
+    finally:
+        L.icx_debug_qout_fault(0)
+    assert e.value.status == 7
+    check_same(ex.run({"x": x}, ["hq", "hs", "hzp"]), want, "normal run after the second failure")
