@@ -51,6 +51,8 @@ SIGNATURES = {
     "icx_pack_weight": ([P, P, I, S, S, P, P], I),
     "icx_matmul_integer_workspace_size": ([S, S, S, I], S),
     "icx_matmul_integer": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, P, P, S], I),
+    "icx_matmul_integer_noalloc_max_bytes": ([], S),
+    "icx_matmul_integer_noalloc": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, P], I),
     "icx_fused_chain_f32": ([P, P, S, S, ctypes.POINTER(Chain), P], I),
     "icx_qlinear_f32": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, ctypes.POINTER(Chain), P, P, S], I),
     "icx_cast_i32_f32": ([P, P, S, P], I),

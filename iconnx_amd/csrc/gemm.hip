@@ -27,6 +27,7 @@
 // (blockIdx % 8) works on a contiguous, M-grouped range of tiles that shares A/B panels in
 // its own L2.
 #include <atomic>
+#include <mutex>
 
 #include "chain.hpp"
 #include "dql_core.hpp"
@@ -1529,6 +1530,64 @@ extern "C" int icx_matmul_integer(icx_stream_t stream, const void* A, int a_dtyp
     return gemm_common(reinterpret_cast<hipStream_t>(stream), A, a_dtype, B, b_dtype, b_packed,
                        b_colsum, M, K, N, a_zp, b_zp, b_zp_len, a_rowsum, nullptr, C, OUT_I32,
                        ws, ws_bytes, "MatMulInteger");
+}
+
+// ---- icx_matmul_integer_noalloc: the workspace in a file-scope device array ---------------
+// For callers that cannot allocate (code under HIP graph capture, serving loops, harnesses
+// that forbid hipMalloc).  The workspace of icx_matmul_integer (the packed weight and its
+// column sums when B is not packed, row sums of A when a zero point needs them) lives in
+// `scratch`, one copy per GPU, held until the process ends.  Every byte of it that a call
+// reads is written earlier in the same call, so nothing needs clearing between calls; calls
+// that overlap on one GPU (two streams, two host threads) share the array and race.
+static __device__ __align__(256) char scratch[icx::kNoAllocScratchBytes];
+
+namespace {
+// Device address of `scratch` on each device (the array's name in host code is a host-side
+// stand-in, never a device address).  Looked up once per device, with that device current.
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+int scratch_ptr(void** out) {
+    int dev = 0;
+    ICX_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) ICX_FAIL(ICX_ERR_UNSUPPORTED, "MatMulInteger (no-alloc): device index %d", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            ICX_FAIL(ICX_ERR_HIP, "MatMulInteger (no-alloc): hipGetSymbolAddress(scratch) failed: %s",
+                     hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return ICX_OK;
+}
+}  // namespace
+
+extern "C" size_t icx_matmul_integer_noalloc_max_bytes(void) { return icx::kNoAllocScratchBytes; }
+
+extern "C" int icx_matmul_integer_noalloc(icx_stream_t stream, const void* A, int a_dtype,
+                                          const void* B, int b_dtype, int b_packed,
+                                          const int32_t* b_colsum, size_t M, size_t K, size_t N,
+                                          const void* a_zp, const void* b_zp, size_t b_zp_len,
+                                          const int32_t* a_rowsum, int32_t* C) {
+    icx::clear_error();
+    // the same workspace icx_matmul_integer would need, checked before any HIP call
+    const size_t need = ws_layout(M, K, N, b_packed).total;
+    if (need > icx::kNoAllocScratchBytes)
+        ICX_FAIL(ICX_ERR_WORKSPACE,
+                 "MatMulInteger (no-alloc): M=%zu K=%zu N=%zu (b_packed=%d) needs %zu bytes of workspace; the "
+                 "static scratch holds %zu (pack the weight once with icx_pack_weight, or call icx_matmul_integer)",
+                 M, K, N, b_packed, need, icx::kNoAllocScratchBytes);
+    void* ws = nullptr;
+    if (M && N) {
+        const int rc = scratch_ptr(&ws);
+        if (rc) return rc;
+    }
+    return gemm_common(reinterpret_cast<hipStream_t>(stream), A, a_dtype, B, b_dtype, b_packed, b_colsum, M, K, N,
+                       a_zp, b_zp, b_zp_len, a_rowsum, nullptr, C, OUT_I32, ws, icx::kNoAllocScratchBytes,
+                       "MatMulInteger (no-alloc)");
 }
 
 int icx::qlinear_f32(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype, int b_packed,

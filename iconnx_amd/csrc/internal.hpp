@@ -43,6 +43,8 @@ int qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, in
 constexpr int kQoutMaxBlocks = 1024;  // blocks of one quantized-output launch
 constexpr size_t kQoutSyncBytes = 256 + 16 * (size_t)kQoutMaxBlocks;  // qexchange.hpp's layout
 constexpr int kQoutErrWord = 2;  // word of that buffer counting launches whose exchange failed
+// icx_matmul_integer_noalloc's file-scope device scratch (one per GPU, for the process's life)
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 int qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int b_dtype, const int32_t* b_colsum,
                 size_t M, size_t K, size_t N, const void* a_zp, const icx_chain* chain, uint8_t* y,
                 float* y_scale, uint8_t* y_zp, unsigned* sync);

@@ -87,6 +87,20 @@ int icx_matmul_integer(icx_stream_t stream, const void* A, int a_dtype, const vo
                        size_t b_zp_len, const int32_t* a_rowsum, int32_t* C, void* ws,
                        size_t ws_bytes);
 
+/* No counterpart in the reference: icx_matmul_integer for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * calls no allocator: the workspace icx_matmul_integer would take lives in a static device
+ * array of icx_matmul_integer_noalloc_max_bytes() bytes (32 MiB) per GPU, held until the
+ * process ends.  Arguments and results as icx_matmul_integer; a shape whose workspace
+ * (icx_matmul_integer_workspace_size) exceeds that size is ICX_ERR_WORKSPACE, before any
+ * GPU work.  Calls that overlap on one GPU (two streams or host threads) share the array
+ * and race: order them. */
+size_t icx_matmul_integer_noalloc_max_bytes(void);
+int icx_matmul_integer_noalloc(icx_stream_t stream, const void* A, int a_dtype, const void* B,
+                               int b_dtype, int b_packed, const int32_t* b_colsum, size_t M,
+                               size_t K, size_t N, const void* a_zp, const void* b_zp,
+                               size_t b_zp_len, const int32_t* a_rowsum, int32_t* C);
+
 /* ---- elementwise epilogue / fused chain -----------------------------------------------
  * An ordered list of f32 binary ops applied to a running value v, each rounding once,
  * exactly like separate ONNX Mul/Add/Sub/Div nodes (src/operators/{mul,add,div}.rs):

@@ -54,3 +54,15 @@ def test_library_is_gfx950_only():
     assert b"gfx950" in blob
     for other in (b"gfx942", b"gfx90a", b"gfx1100"):
         assert other not in blob
+
+
+def test_noalloc_matmul_rejects_an_oversized_workspace_before_any_gpu_work(L):
+    """icx_matmul_integer_noalloc checks the shape's workspace against its static array
+    (32 MiB) first: an unpacked 8192 x 8192 weight is refused with ICX_ERR_WORKSPACE and a
+    message, without touching the (here fake) pointers or the GPU."""
+    assert L.icx_matmul_integer_noalloc_max_bytes() == 32 << 20
+    fake = ctypes.c_void_p(0x1000)
+    rc = L.icx_matmul_integer_noalloc(None, fake, 0, fake, 0, 0, None, 16, 8192, 8192,
+                                      None, None, 1, None, fake)
+    assert rc == 4
+    assert b"static scratch" in L.icx_last_error()
