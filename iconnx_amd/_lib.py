@@ -45,6 +45,18 @@ SIGNATURES = {
     "icx_status_str": ([I], ctypes.c_char_p),
     "icx_last_error": ([], ctypes.c_char_p),
     "icx_version": ([], ctypes.c_char_p),
+    "icx_stream_create": ([ctypes.POINTER(P)], I),
+    "icx_stream_destroy": ([P], I),
+    "icx_stream_synchronize": ([P], I),
+    "icx_pool_create": ([], P),
+    "icx_pool_destroy": ([P], None),
+    "icx_pool_alloc": ([P, S, ctypes.POINTER(P)], I),
+    "icx_pool_free": ([P, P], I),
+    "icx_pool_stats": ([P, P, P, P], I),
+    "icx_host_alloc": ([S, ctypes.POINTER(P)], I),
+    "icx_host_free": ([P], I),
+    "icx_memcpy_h2d_async": ([P, P, P, S], I),
+    "icx_memcpy_d2h_async": ([P, P, P, S], I),
     "icx_dql_workspace_size": ([S], S),
     "icx_dynamic_quantize_linear": ([P, P, S, P, P, P, P, S, P, S], I),
     "icx_packed_weight_bytes": ([S, S], S),
@@ -57,6 +69,7 @@ SIGNATURES = {
     "icx_qlinear_f32": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, ctypes.POINTER(Chain), P, P, S], I),
     "icx_cast_i32_f32": ([P, P, S, P], I),
     "icx_dequantize_linear_f32": ([P, P, I, P, P, S, S, S, P], I),
+    "icx_gather": ([P, P, S, S, S, S, P, I, S, P], I),
     "icx_layer_norm_f32": ([P, P, P, S, S, P, P, ctypes.c_float, P], I),
     "icx_softmax_f32": ([P, P, S, S, P], I),
     "icx_transpose": ([P, P, S, I, P, P, P], I),

@@ -2,6 +2,7 @@
 // DequantizeLinear, plus the library's error / version plumbing.
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 
 #include "chain.hpp"
 
@@ -111,6 +112,33 @@ dequantize_kernel(const T* __restrict__ x, const float* __restrict__ scale,
     }
 }
 
+// Gather of whole rows: data viewed as [outer, axis_len, row] (row = the bytes of the inner
+// dimensions), out as [outer, n_idx, row]; one wave per output row, VEC-byte chunks (16 when
+// rows and pointers allow it).  An index is taken from the end when negative and clamped into
+// [0, axis_len) when still outside, as the reference's gather kernels do.
+template <int VEC>
+__global__ void __launch_bounds__(kThreads)
+gather_rows_kernel(const uint8_t* __restrict__ data, const void* __restrict__ indices, int idx64,
+                   size_t n_idx, size_t axis_len, size_t row_bytes, size_t rows,
+                   uint8_t* __restrict__ out) {
+    typedef typename std::conditional<VEC == 16, uint4, typename std::conditional<VEC == 4, uint32_t,
+                                                                                   uint8_t>::type>::type T;
+    const int lane = threadIdx.x & 63;
+    const size_t waves = (size_t)gridDim.x * (kThreads / 64);
+    for (size_t r = (size_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6); r < rows; r += waves) {
+        const size_t o = r / n_idx, i = r - o * n_idx;
+        long long k = idx64 ? reinterpret_cast<const long long*>(indices)[i]
+                            : (long long)reinterpret_cast<const int*>(indices)[i];
+        if (k < 0) k += (long long)axis_len;
+        if (k < 0) k = 0;
+        if (k >= (long long)axis_len) k = (long long)axis_len - 1;
+        const T* src = reinterpret_cast<const T*>(data + (o * axis_len + (size_t)k) * row_bytes);
+        T* dst = reinterpret_cast<T*>(out + r * row_bytes);
+        const size_t n = row_bytes / VEC;
+        for (size_t c = lane; c < n; c += 64) dst[c] = src[c];
+    }
+}
+
 unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
     size_t b = icx::cdiv(work, per_block);
     if (b < 1) b = 1;
@@ -213,5 +241,35 @@ extern "C" int icx_dequantize_linear_f32(icx_stream_t stream, const void* x, int
             ICX_FAIL(ICX_ERR_DTYPE, "DequantizeLinear: input dtype %d unsupported (must be Int8, UInt8, or Int32)", x_dtype);
     }
     ICX_LAUNCH_CHECK("dequantize_kernel");
+    return ICX_OK;
+}
+
+extern "C" int icx_gather(icx_stream_t stream, const void* data, size_t elem_bytes, size_t outer,
+                          size_t axis_len, size_t inner, const void* indices, int idx_dtype,
+                          size_t n_idx, void* out) {
+    icx::clear_error();
+    if (idx_dtype != ICX_I64 && idx_dtype != ICX_I32)
+        ICX_FAIL(ICX_ERR_DTYPE, "Gather: indices dtype %d unsupported (must be Int64 or Int32)", idx_dtype);
+    if (elem_bytes == 0) ICX_FAIL(ICX_ERR_INVALID_ARG, "Gather: zero element size");
+    const size_t rows = outer * n_idx, row_bytes = inner * elem_bytes;
+    if (rows == 0 || row_bytes == 0) return ICX_OK;
+    if (axis_len == 0) ICX_FAIL(ICX_ERR_SHAPE, "Gather: %zu indices into an empty axis", n_idx);
+    if (!data || !indices || !out) ICX_FAIL(ICX_ERR_INVALID_ARG, "Gather: null pointer argument");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid(grid_for(rows, kThreads / 64, 8192)), block(kThreads);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(data) | reinterpret_cast<uintptr_t>(out) | row_bytes;
+    const auto* d = reinterpret_cast<const uint8_t*>(data);
+    auto* o = reinterpret_cast<uint8_t*>(out);
+    const int i64 = idx_dtype == ICX_I64;
+    if (align % 16 == 0)
+        hipLaunchKernelGGL(gather_rows_kernel<16>, grid, block, 0, s, d, indices, i64, n_idx, axis_len, row_bytes,
+                           rows, o);
+    else if (align % 4 == 0)
+        hipLaunchKernelGGL(gather_rows_kernel<4>, grid, block, 0, s, d, indices, i64, n_idx, axis_len, row_bytes,
+                           rows, o);
+    else
+        hipLaunchKernelGGL(gather_rows_kernel<1>, grid, block, 0, s, d, indices, i64, n_idx, axis_len, row_bytes,
+                           rows, o);
+    ICX_LAUNCH_CHECK("gather_rows_kernel");
     return ICX_OK;
 }

@@ -739,6 +739,7 @@ class Planner {
         const std::string w_zp = m.in.size() > 3 ? m.in[3] : "";
         if (!w_zp.empty() && !is_init(w_zp)) return false;
         const int ci = sole_consumer(m.out[0]);
+        if (is_op(ci, "DequantizeLinear")) return match_dequant_head(mi, ci, head, mem);
         if (!is_op(ci, "Cast") || nodes_[ci].attr_or("to", -1) != 1 || nodes_[ci].out.size() != 1) return false;
         const std::string cast_out = nodes_[ci].out[0];
         const int si = sole_consumer(cast_out);
@@ -773,6 +774,103 @@ class Planner {
         // zero-point folding: an all-zero weight zero point contributes nothing
         head.w_zp_folded = !w_zp.empty() && g_.inits[w_zp].all_zero();
         return true;
+    }
+
+    // MatMulInteger(A, W) -> DequantizeLinear(acc, scale, [zp]) [-> chain]: the int32
+    // DequantizeLinear of the CPU forward, (acc as f32 - zp as f32) * scale
+    // (src/operators/dequantize_linear.rs:158-174), as the chain steps Sub(zp as f32),
+    // Mul(scale) after the GEMM's Cast — each one rounding, as there.  The reference GPU runs it
+    // as its own kernel (dequantize_linear_i32_kernel, src/cuda/ops/quantize_kernels.rs:72-81).
+    // Needs a static f32 scale and an optional static Int32 zero point, per tensor or per
+    // output column (a [N] scale whose axis is the output's last).
+    bool match_dequant_head(int mi, int di, PlannedOp& head, std::vector<int>& mem) {
+        const Node& m = nodes_[mi];
+        const Node& dq = nodes_[di];
+        if (dq.in.size() < 2 || dq.in.size() > 3 || dq.out.size() != 1 || dq.in[0] != m.out[0]) return false;
+        const int64_t N = g_.inits[m.in[1]].shape[1];
+        auto sc = g_.inits.find(dq.in[1]);
+        if (sc == g_.inits.end() || sc->second.dtype != ICX_F32) return false;
+        const int64_t ns = numel(sc->second.shape);
+        if (ns != 1 && !(ns == N && sc->second.shape.size() == 1)) return false;
+        if (ns != 1 && N != 1) {  // per axis: the axis must be the output's last
+            const int64_t ax = dq.attr_or("axis", 1);
+            const int r = rank_of(m.in[0]);
+            if (!(ax == -1 || (r > 0 && (ax == r - 1 || ax == -1)))) return false;
+            if (ax < -1) return false;
+        }
+        std::string zpf;
+        if (dq.in.size() == 3 && !dq.in[2].empty()) {
+            auto zi = g_.inits.find(dq.in[2]);
+            if (zi == g_.inits.end() || zi->second.dtype != ICX_I32 || numel(zi->second.shape) != ns) return false;
+            if (!zi->second.all_zero()) {
+                // the zero point as f32 (x as f32, round to nearest even), a plan-made operand
+                HostTensor f;
+                f.dtype = ICX_F32;
+                f.shape = sc->second.shape;
+                f.data.resize(4 * (size_t)ns);
+                const int32_t* z = reinterpret_cast<const int32_t*>(zi->second.data.data());
+                for (int64_t j = 0; j < ns; ++j) {
+                    const float v = (float)z[j];
+                    std::memcpy(&f.data[4 * (size_t)j], &v, 4);
+                }
+                zpf = dq.name + "::zero_point_f32";
+                g_.inits[zpf] = f;
+            }
+        }
+        head.steps.clear();
+        if (!zpf.empty()) {
+            Step sub;
+            sub.op = ICX_OP_SUB;
+            sub.opnd0 = zpf;
+            head.steps.push_back(sub);
+        }
+        Step mul;
+        mul.op = ICX_OP_MUL;
+        mul.opnd0 = dq.in[1];
+        head.steps.push_back(mul);
+        mem = {di};
+        std::string cur = dq.out[0];
+        extend_chain(cur, head.steps, mem);
+        head.kind = Kind::FusedHead;
+        head.pattern = Pattern::QuantizedLinear;
+        head.a = m.in[0];
+        head.w = m.in[1];
+        head.a_zp = m.in.size() > 2 ? m.in[2] : "";
+        head.w_zp = m.in.size() > 3 ? m.in[3] : "";
+        head.out = cur;
+        head.w_zp_folded = !head.w_zp.empty() && g_.inits[head.w_zp].all_zero();
+        return true;
+    }
+
+    // Rank of a tensor from the graph's inputs, initializers and the ops on this path; -1
+    // when it cannot be told before a run.
+    int rank_of(const std::string& t, int depth = 0) const {
+        if (depth > 256) return -1;
+        for (auto& in : g_.inputs)
+            if (in.first == t) return (int)in.second.size();
+        auto it = g_.inits.find(t);
+        if (it != g_.inits.end()) return (int)it->second.shape.size();
+        const int pi = producer(t);
+        if (pi < 0) return -1;
+        const Node& n = nodes_[pi];
+        const std::string& op = n.op;
+        if (op == "DynamicQuantizeLinear") return t == n.out[0] ? rank_of(n.in[0], depth + 1) : 0;
+        if (op == "MatMulInteger" || op == "Cast" || op == "Erf" || op == "Softmax" || op == "LayerNormalization" ||
+            op == "DequantizeLinear" || op == "Transpose")
+            return n.in.empty() ? -1 : rank_of(n.in[0], depth + 1);
+        if (op == "Reshape" && n.in.size() == 2) {
+            auto sh = g_.inits.find(n.in[1]);
+            return sh == g_.inits.end() ? -1 : (int)numel(sh->second.shape);
+        }
+        if (op == "Gather" && n.in.size() == 2) {
+            const int rd = rank_of(n.in[0], depth + 1), ri = rank_of(n.in[1], depth + 1);
+            return rd < 1 || ri < 0 ? -1 : rd - 1 + ri;
+        }
+        if ((op_code(op) >= 0 || op == "MatMul") && n.in.size() == 2) {
+            const int a = rank_of(n.in[0], depth + 1), b = rank_of(n.in[1], depth + 1);
+            return a < 0 || b < 0 ? -1 : std::max(a, b);
+        }
+        return -1;
     }
 
     // Two or more binary ops over one running tensor with static operands, or a GELU.
@@ -1095,6 +1193,7 @@ class Runner {
         if (t == "Transpose") return run_transpose(n);
         if (t == "Reshape") return run_reshape(n);
         if (t == "MatMul") return run_matmul_f32(n);
+        if (t == "Gather") return run_gather(n);
         if (op_code(t) >= 0) return run_binary(n);
         set_error("op '%s' is not on the quantized-linear path", t.c_str());
         return ICX_ERR_UNSUPPORTED;
@@ -1769,6 +1868,49 @@ class Runner {
     }
 
     // DequantizeLinear (src/operators/dequantize_linear.rs:32-180): per-tensor or per-axis.
+    // Gather (src/cuda/executor/layout.rs:260-330 -> gpu_gather_from_gpu; CPU
+    // src/operators/gather.rs:21-205): any axis, data of any dtype on this path (the UINT8
+    // embedding table of DistilBERT-INT8 first of all), Int64 or Int32 indices; the output
+    // keeps the data dtype, as the GPU path does.
+    int run_gather(const Node& n) {
+        if (n.in.size() != 2 || n.out.size() != 1) {
+            set_error("Gather requires [data, indices] and one output");
+            return ICX_ERR_INVALID_ARG;
+        }
+        const DevTensor *D, *I;
+        int rc = need(n.in[0], &D, "Gather");
+        if (!rc) rc = need(n.in[1], &I, "Gather");
+        if (rc) return rc;
+        if (I->dtype != ICX_I64 && I->dtype != ICX_I32) {
+            set_error("Gather: indices must be Int64 or Int32, got %s", dtype_name(I->dtype));
+            return ICX_ERR_DTYPE;
+        }
+        const int64_t nd = (int64_t)D->shape.size();
+        const int64_t ax0 = n.attr_or("axis", 0);
+        const int64_t ax = ax0 < 0 ? ax0 + nd : ax0;
+        if (nd < 1 || ax < 0 || ax >= nd) {
+            set_error("Gather: axis %lld out of range for rank-%lld data", (long long)ax0, (long long)nd);
+            return ICX_ERR_SHAPE;
+        }
+        int64_t outer = 1, inner = 1;
+        for (int64_t d = 0; d < ax; ++d) outer *= D->shape[d];
+        for (int64_t d = ax + 1; d < nd; ++d) inner *= D->shape[d];
+        std::vector<int64_t> oshape(D->shape.begin(), D->shape.begin() + ax);
+        oshape.insert(oshape.end(), I->shape.begin(), I->shape.end());
+        oshape.insert(oshape.end(), D->shape.begin() + ax + 1, D->shape.end());
+        const int dt = D->dtype;
+        const void* dptr = D->ptr;
+        const void* iptr = I->ptr;
+        const int idt = I->dtype;
+        const size_t nidx = (size_t)numel(I->shape);
+        const int64_t alen = D->shape[ax];
+        DevTensor* Y;
+        rc = alloc(n.out[0], dt, oshape, &Y);
+        if (rc) return rc;
+        return icx_gather(s_, dptr, dtype_size(dt), (size_t)outer, (size_t)alen, (size_t)inner, iptr, idt, nidx,
+                          Y->ptr);
+    }
+
     int run_dequantize(const Node& n) {
         if (n.in.size() < 2 || n.in.size() > 3) {
             set_error("DequantizeLinear requires 2 or 3 inputs, got %zu", n.in.size());
@@ -1984,7 +2126,6 @@ static int icx_graph_compile_impl(icx_graph* g, icx_stream_t stream) {
     }
     for (auto& kv : g->inits) {
         const HostTensor& h = kv.second;
-        if (h.dtype == ICX_I64) continue;  // shapes: read on the host only
         DevTensor t;
         t.dtype = h.dtype;
         t.shape = h.shape;
@@ -2079,7 +2220,8 @@ extern "C" int icx_graph_set_input(icx_graph* g, const char* name, int dtype, in
                                    const int64_t* dims, const void* data, int on_device) {
     icx::clear_error();
     if (!g || !name || rank < 0 || (rank && !dims)) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_input: bad arguments");
-    if (!valid_dtype(dtype)) ICX_FAIL(ICX_ERR_DTYPE, "set_input: '%s' has unsupported dtype %d", name, dtype);
+    if (!valid_dtype(dtype) && dtype != ICX_I64)
+        ICX_FAIL(ICX_ERR_DTYPE, "set_input: '%s' has unsupported dtype %d", name, dtype);
     BoundInput b;
     b.dtype = dtype;
     b.shape.assign(dims, dims + rank);

@@ -26,7 +26,8 @@ import numpy as np
 from ._lib import ICX_F32, ICX_I8, ICX_I32, ICX_I64, ICX_U8, IconnxError, check, lib
 
 _NP_DT = {np.dtype(np.int8): ICX_I8, np.dtype(np.uint8): ICX_U8,
-          np.dtype(np.int32): ICX_I32, np.dtype(np.float32): ICX_F32}
+          np.dtype(np.int32): ICX_I32, np.dtype(np.float32): ICX_F32,
+          np.dtype(np.int64): ICX_I64}  # Int64: Gather indices
 _INIT_DT = {**_NP_DT, np.dtype(np.int64): ICX_I64}
 _DT_NP = {v: k for k, v in _NP_DT.items()}
 
@@ -43,7 +44,7 @@ def _torch():
 def _torch_dt(code):
     torch = _torch()
     return {ICX_I8: torch.int8, ICX_U8: torch.uint8, ICX_I32: torch.int32,
-            ICX_F32: torch.float32}[code]
+            ICX_F32: torch.float32, ICX_I64: torch.int64}[code]
 
 
 def _dims(shape):

@@ -79,6 +79,41 @@ def add_quantized_linear(ex, x, w, w_zp, w_scale, bias, chain=(), prefix="ql", d
     return y
 
 
+def add_dequantize_linear_head(ex, a, a_zp, w, scale, zp, bias, axis=1, prefix="dq"):
+    """MatMulInteger(a, W, a_zp) -> DequantizeLinear(acc, scale, zp, axis) [-> Add(bias)]:
+    the form of a quantized linear whose graph dequantizes the int32 accumulator with a
+    DequantizeLinear instead of Cast + Mul.  ``a_zp`` a tensor name or None; ``zp`` an Int32
+    scalar / [N] or None; ``scale`` scalar or [N].  Returns the output name."""
+    p = prefix
+    ex.add_initializer(p + ".W", np.asarray(w))
+    ex.add_initializer(p + ".scale", np.asarray(scale, np.float32))
+    mm_in = [a, p + ".W"] + ([a_zp] if a_zp is not None else [])
+    ex.add_node(p + ".mmi", "MatMulInteger", mm_in, [p + ".acc"])
+    dq_in = [p + ".acc", p + ".scale"]
+    if zp is not None:
+        ex.add_initializer(p + ".zp", np.asarray(zp, np.int32))
+        dq_in.append(p + ".zp")
+    ex.add_node(p + ".dequant", "DequantizeLinear", dq_in, [p + ".linear0"], {"axis": axis})
+    y = p + ".linear0"
+    if bias is not None:
+        ex.add_initializer(p + ".bias", np.asarray(bias, np.float32))
+        ex.add_node(p + ".bias_add", "Add", [y, p + ".bias"], [p + ".linear"])
+        y = p + ".linear"
+    return y
+
+
+def add_quantized_embedding(ex, ids, table, scale, zp, prefix="emb"):
+    """DistilBERT-INT8's embedding front end: Gather(UInt8 table [vocab, hidden], ids) ->
+    DequantizeLinear(., scale, zp) -> f32 [..., hidden].  Returns the output name."""
+    p = prefix
+    ex.add_initializer(p + ".table", np.asarray(table, np.uint8))
+    ex.add_initializer(p + ".scale", np.asarray(scale, np.float32))
+    ex.add_initializer(p + ".zp", np.asarray(zp, np.uint8))
+    ex.add_node(p + ".gather", "Gather", [p + ".table", ids], [p + ".q"], {"axis": 0})
+    ex.add_node(p + ".dequant", "DequantizeLinear", [p + ".q", p + ".scale", p + ".zp"], [p + ".out"])
+    return p + ".out"
+
+
 def config_graph(ex, cfg, x_name="x", x_shape=None):
     """The linear configs (cfg1 / cfg2 / cfg4) as a graph on executor ``ex``; returns
     (output name, host data dict).  The input is declared with its batch and sequence

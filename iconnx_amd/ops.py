@@ -15,12 +15,14 @@ Reference counterparts (ryanoneill/iconnx):
   gpu_fused_add_mul / sub_mul  src/cuda/kernels/fused/wrappers.rs:583-650
   gpu_fused_div_mul            src/cuda/kernels/fused/wrappers.rs:652-683
   gpu_mul / gpu_add / gpu_div  src/cuda/kernels/mod.rs (+ broadcast, src/cuda/executor/elementwise.rs:54-200)
+  gpu_gather_from_gpu          src/cuda/ops/layout/mod.rs:900-1020 (gather_u8_kernel,
+                               src/cuda/ops/quantize_kernels.rs:203-224)
 """
 import ctypes
 
 import torch
 
-from ._lib import (BCAST_COL, BCAST_FULL, BCAST_ROW, BCAST_SCALAR, ICX_F32, ICX_I8, ICX_I32,
+from ._lib import (BCAST_COL, BCAST_FULL, BCAST_ROW, BCAST_SCALAR, ICX_F32, ICX_I8, ICX_I32, ICX_I64,
                    ICX_U8, MAX_CHAIN, OP_ADD, OP_DIV, OP_ERF, OP_MUL, OP_MUL_SAVED, OP_SAVE,
                    OP_SUB, Chain, IconnxError, check, lib)
 
@@ -447,4 +449,33 @@ def gpu_attention(q, k, v, heads, scale, scale_div=True, scale_q=False):
                                   _p(v.contiguous()), B, S, heads, D, HD, HD, HD, HD,
                                   ctypes.c_float(scale), 1 if scale_div else 0,
                                   1 if scale_q else 0, _p(out)))
+    return out
+
+
+# ---------------------------------------------------------------------------------------
+# Gather
+# ---------------------------------------------------------------------------------------
+def gpu_gather_from_gpu(data, indices, axis=0):
+    """ONNX Gather with device indices: ``data.shape[:axis] + indices.shape +
+    data.shape[axis+1:]``, the data dtype kept (UInt8 for DistilBERT-INT8's embedding table);
+    a negative index counts from the end and one still outside the axis is clamped, as the
+    reference's gather kernels do (the reference wrapper takes axis 0 only and transposes for
+    the others, src/cuda/executor/layout.rs:260-330)."""
+    _require_cuda(data, indices)
+    if indices.dtype not in (torch.int64, torch.int32):
+        raise IconnxError(ERR_DTYPE, "Gather: indices must be Int64 or Int32, got %s" % _name(indices.dtype))
+    nd = data.dim()
+    ax = axis + nd if axis < 0 else axis
+    if nd < 1 or not 0 <= ax < nd:
+        raise IconnxError(ERR_SHAPE, "Gather: axis %d out of range for rank-%d data" % (axis, nd))
+    data, indices = data.contiguous(), indices.contiguous()
+    shape = list(data.shape)
+    outer, inner = 1, 1
+    for d in shape[:ax]:
+        outer *= d
+    for d in shape[ax + 1:]:
+        inner *= d
+    out = torch.empty(shape[:ax] + list(indices.shape) + shape[ax + 1:], dtype=data.dtype, device=data.device)
+    check(lib().icx_gather(_stream(), _p(data), data.element_size(), outer, shape[ax], inner, _p(indices),
+                           ICX_I64 if indices.dtype == torch.int64 else ICX_I32, indices.numel(), _p(out)))
     return out

@@ -35,7 +35,7 @@ typedef enum {
     ICX_ERR_KERNEL = 7,      /* a kernel reported a failure on the device (icx_graph_status) */
 } icx_status;
 
-/* ICX_I64 is accepted for graph initializers only (Reshape shapes, read on the host). */
+/* ICX_I64: Reshape shapes (graph initializers, read on the host) and Gather indices / data. */
 typedef enum { ICX_I8 = 0, ICX_U8 = 1, ICX_I32 = 2, ICX_F32 = 3, ICX_I64 = 4 } icx_dtype;
 
 const char* icx_status_str(int status);
@@ -43,6 +43,41 @@ const char* icx_status_str(int status);
 const char* icx_last_error(void);
 /* Library / build identification, e.g. "iconnx_hip gfx950 ...". */
 const char* icx_version(void);
+
+/* ---- streams, memory, transfers --------------------------------------------------------
+ * What garboard and IconnxCudaContext / GpuMemoryPool give the reference's wrappers.
+ * icx_stream_create: the context's one stream (src/cuda/context.rs:28-31), default priority.
+ * icx_stream_synchronize: IconnxCudaContext::sync (context.rs:226-232). */
+int icx_stream_create(icx_stream_t* out);
+int icx_stream_destroy(icx_stream_t stream);
+int icx_stream_synchronize(icx_stream_t stream);
+
+/* GpuMemoryPool (src/cuda/memory_pool.rs:47-545) on hipMalloc.  icx_pool_alloc is get_f32 /
+ * get_u8 / get_i32 / ... (:104-400): a buffer of at least `bytes` bytes of a power-of-two size
+ * class (>= 256 B), from the pool or fresh on a miss; NOT zero-filled (the reference clears
+ * reused slices, :120; every kernel here writes its whole output).  icx_pool_free is
+ * return_tensor (:482): at most eight free buffers are kept per class, as max_per_bucket
+ * (:94), and a buffer beyond that is freed; a pointer this pool did not hand out is
+ * ICX_ERR_INVALID_ARG.  Buffers are reused in stream order: return one once the last work
+ * reading it is enqueued on the stream that will use it next.  icx_pool_stats is stats()
+ * (:526): hits, misses (hipMalloc calls) and bytes held.  icx_pool_destroy frees every buffer,
+ * handed out or not.  A pool is used from one host thread at a time (the reference's
+ * executor is !Sync). */
+typedef struct icx_pool icx_pool;
+icx_pool* icx_pool_create(void);
+void icx_pool_destroy(icx_pool* pool);
+int icx_pool_alloc(icx_pool* pool, size_t bytes, void** out);
+int icx_pool_free(icx_pool* pool, void* ptr);
+int icx_pool_stats(icx_pool* pool, int64_t* hits, int64_t* misses, int64_t* bytes_held);
+
+/* IconnxCudaContext::htod / dtoh (context.rs:160-223) as stream-ordered copies: both return
+ * once enqueued (the reference's dtoh blocks the host).  With pinned host memory from
+ * icx_host_alloc the copy runs asynchronously; the destination of a D2H copy is valid after
+ * icx_stream_synchronize. */
+int icx_host_alloc(size_t bytes, void** out);
+int icx_host_free(void* ptr);
+int icx_memcpy_h2d_async(icx_stream_t stream, void* dst, const void* src, size_t bytes);
+int icx_memcpy_d2h_async(icx_stream_t stream, void* dst, const void* src, size_t bytes);
 
 /* ---- DynamicQuantizeLinear ------------------------------------------------------------
  * Replaces gpu_dynamic_quantize_linear (src/cuda/ops/quantize.rs:296-377), which copies x to
@@ -167,6 +202,18 @@ int icx_dequantize_linear_f32(icx_stream_t stream, const void* x, int x_dtype,
                               const float* scale, const void* zp, size_t n,
                               size_t axis_size, size_t inner, float* y);
 
+/* ---- Gather --------------------------------------------------------------------------
+ * Replaces gpu_gather_from_gpu / gpu_gather (src/cuda/ops/layout/mod.rs:689-1020) and its
+ * kernels (gather_kernel / gather_i64_kernel, and gather_u8_kernel,
+ * src/cuda/ops/quantize_kernels.rs:203-224, which DistilBERT-INT8's UINT8 word-embedding table
+ * goes through); ONNX Gather semantics of src/operators/gather.rs:21-205 on any element type:
+ * data viewed as [outer, axis_len, inner] elements of elem_bytes bytes (outer = product of the
+ * dims before `axis`, inner = after), out [outer, n_idx, inner] with out[o, i, :] =
+ * data[o, k, :], k = indices[i] (+ axis_len when negative), clamped into [0, axis_len - 1]
+ * as the reference's kernels do.  indices: device Int64 (ICX_I64) or Int32 (ICX_I32). */
+int icx_gather(icx_stream_t stream, const void* data, size_t elem_bytes, size_t outer,
+               size_t axis_len, size_t inner, const void* indices, int idx_dtype, size_t n_idx,
+               void* out);
 
 /* ---- encoder ops (fp32) --------------------------------------------------------------
  * The fp32 ops a DistilBERT-shaped encoder needs around its quantized linears.  Parity: the

@@ -18,10 +18,13 @@ conditions under which it panics — raised here as :class:`OracleError`):
 * :func:`erf` — ``src/operators/erf.rs:21-31``
 * :func:`matmul_f32` — ``src/operators/matmul.rs:20-150`` (f64-accumulated; tolerance)
 * :func:`transpose` — ``src/operators/transpose.rs:10-40``
+* :func:`gather` — ``src/operators/gather.rs:21-205`` (numpy index arithmetic; the index clamp
+  of the GPU kernels, ``src/cuda/ops/quantize_kernels.rs:203-224``)
 
 Parity pins (tests/test_oracle.py): the ONNX 1.18 node goldens the reference vendors
 (tests/golden/onnx_node_goldens.json), the reference's unit-test literals, brute-force
-int64/float64 checks and closed forms.  The per-column ``b_zero_point`` form of
+int64/float64 checks and closed forms (Gather: the four ONNX ``test_gather_*`` goldens plus a
+brute-force loop with negative and out-of-range indices).  The per-column ``b_zero_point`` form of
 :func:`matmul_integer` is an extension the reference rejects; it is pinned only by the
 ONNX definition (closed form + brute force) — reference parity unpinned for it.
 """
@@ -287,6 +290,34 @@ def qlinear_graph(x, w, w_zp, x_scale_times_w_scale_inputs, bias, chain=(), rows
         y = fn(operand, y) if operand_is_lhs else fn(y, operand)
     out["y"] = y
     return out
+
+
+def gather(data, indices, axis=0):
+    """ONNX Gather as the reference computes it: output shape data.shape[:axis] +
+    indices.shape + data.shape[axis+1:] (src/operators/gather.rs:59-151), a negative index
+    taken from the end (gather.rs:89-114).  An index still outside [0, axis_len) is clamped,
+    as the GPU kernels that the HIP path replaces do (gather_u8_kernel,
+    src/cuda/ops/quantize_kernels.rs:203-224; the CPU forward would panic there).  The data
+    dtype is kept, as on the GPU path (the CPU forward converts non-f32/i64 data to Float32
+    first, gather.rs:203-207 — the same values).  Byte work: plain index arithmetic."""
+    data = np.asarray(data)
+    idx = np.asarray(indices).astype(np.int64)
+    nd = data.ndim
+    ax = axis + nd if axis < 0 else axis
+    if nd < 1 or not 0 <= ax < nd:
+        raise OracleError("Gather: axis %d out of range for rank %d" % (axis, nd))
+    alen = data.shape[ax]
+    out_shape = data.shape[:ax] + idx.shape + data.shape[ax + 1:]
+    outer = int(np.prod(data.shape[:ax], dtype=np.int64))
+    inner = int(np.prod(data.shape[ax + 1:], dtype=np.int64))
+    flat = np.ascontiguousarray(data).reshape(outer, alen, inner)
+    k = idx.reshape(-1).copy()
+    k[k < 0] += alen
+    k = np.clip(k, 0, max(alen - 1, 0))
+    out = np.empty((outer, k.size, inner), data.dtype)
+    for i, kk in enumerate(k.tolist()):
+        out[:, i, :] = flat[:, kk, :]
+    return out.reshape(out_shape)
 
 
 # ---- encoder ops (fp32) ------------------------------------------------------------------

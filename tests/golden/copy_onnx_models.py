@@ -19,6 +19,8 @@ TESTS = [
     "test_layer_normalization_3d_axis_negative_1_epsilon", "test_softmax_axis_2",
     "test_softmax_example", "test_erf", "test_transpose_default",
     "test_transpose_all_permutations_0", "test_matmul_2d", "test_matmul_3d",
+    # Gather (the UINT8 embedding table of DistilBERT-INT8 goes through it)
+    "test_gather_0", "test_gather_1", "test_gather_2d_indices", "test_gather_negative_indices",
 ]
 
 

@@ -56,6 +56,8 @@ TESTS = [
     "test_transpose_all_permutations_3",
     "test_transpose_all_permutations_4",
     "test_transpose_all_permutations_5",
+    # Gather (the UINT8 embedding table of DistilBERT-INT8 goes through it)
+    "test_gather_0", "test_gather_1", "test_gather_2d_indices", "test_gather_negative_indices",
 ]
 
 # TensorProto.DataType values used by these tests.

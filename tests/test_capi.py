@@ -66,3 +66,17 @@ def test_noalloc_matmul_rejects_an_oversized_workspace_before_any_gpu_work(L):
                                       None, None, 1, None, fake)
     assert rc == 4
     assert b"static scratch" in L.icx_last_error()
+
+
+def test_pool_bookkeeping_is_host_only(L):
+    """An empty pool is created, queried and destroyed without a GPU; returning a pointer it
+    never handed out is an error, as the reference pool only takes back its own slices."""
+    p = L.icx_pool_create()
+    assert p
+    h, m, b = ctypes.c_int64(-1), ctypes.c_int64(-1), ctypes.c_int64(-1)
+    assert L.icx_pool_stats(p, ctypes.byref(h), ctypes.byref(m), ctypes.byref(b)) == 0
+    assert (h.value, m.value, b.value) == (0, 0, 0)
+    assert L.icx_pool_free(p, ctypes.c_void_p(0x1000)) == 1
+    assert b"not handed out" in L.icx_last_error()
+    assert L.icx_pool_free(p, None) == 0
+    L.icx_pool_destroy(p)

@@ -427,3 +427,41 @@ def test_encoder_ffn_up_quantizes_its_own_output():
     entries, _ = ex.plan()
     dql_of = {e.node: e for e in entries if e.op_type == "DynamicQuantizeLinear"}
     assert all(d in dql_of for d in planned.values())
+
+
+def _dq_graph(rank, scale_n, axis, zp):
+    ex = GpuGraphExecutor()
+    ex.add_input("a", [None] * (rank - 1) + [8])
+    ex.add_input("a_zp", [])
+    rng = np.random.default_rng(3)
+    w = rng.integers(-127, 128, (8, 16)).astype(np.int8)
+    scale = np.float32(0.01) if scale_n == 1 else rng.uniform(0.01, 0.02, 16).astype(np.float32)
+    y = graphs.add_dequantize_linear_head(ex, "a", "a_zp", w, scale, zp, np.zeros(16, np.float32), axis=axis)
+    ex.add_output(y)
+    return ex, y
+
+
+@pytest.mark.parametrize("rank,scale_n,axis,zp,steps", [
+    (2, 1, 1, np.int32(5), 3),                  # Sub(zp), Mul(scale), Add(bias)
+    (2, 16, 1, None, 2),                         # per-column scale, axis 1 = last of [M, N]
+    (2, 16, 1, np.zeros(16, np.int32), 2),       # all-zero zero point: no Sub
+    (3, 16, 2, np.arange(16, dtype=np.int32), 3),
+    (3, 16, -1, None, 2),
+    (3, 1, 1, np.int32(-2), 3),                  # per-tensor: any axis
+])
+def test_matmul_integer_dequantize_linear_is_one_head(rank, scale_n, axis, zp, steps):
+    ex, y = _dq_graph(rank, scale_n, axis, zp)
+    entries, _ = ex.plan()
+    (h,) = heads(entries)
+    assert h.pattern == "QuantizedLinear" and h.op_type == "MatMulInteger" and h.out == y
+    assert h.steps == steps
+    kinds = by_node(entries)
+    assert kinds["dq.dequant"].kind == "Skip" and kinds["dq.bias_add"].kind == "Skip"
+
+
+def test_dequantize_linear_along_a_non_last_axis_stays_unfused():
+    """A [N] scale along axis 1 of a 3-D [B, S, N] accumulator scales rows, not columns."""
+    ex, _ = _dq_graph(3, 16, 1, None)
+    entries, _ = ex.plan()
+    assert heads(entries) == [] or all(h.op_type != "MatMulInteger" for h in heads(entries))
+    assert by_node(entries)["dq.dequant"].kind == "Regular"

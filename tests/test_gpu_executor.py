@@ -79,7 +79,9 @@ def test_unfused_path_matches_fused():
 
 
 def test_dequantize_linear_epilogue_and_standalone_chain():
-    """MatMulInteger -> DequantizeLinear(acc, scale) and a MulAdd chain after it."""
+    """MatMulInteger -> DequantizeLinear(acc, scale) -> Mul -> Add: one QuantizedLinear head
+    (Mul(scale), Mul(m), Add(b) in the GEMM store); with the accumulator requested, the
+    DequantizeLinear runs on its own and the Mul / Add become a MulAdd head."""
     rng = np.random.default_rng(5)
     a = rng.integers(0, 256, (96, 64)).astype(np.uint8)
     w = rng.integers(-127, 128, (64, 80)).astype(np.int8)
@@ -96,10 +98,14 @@ def test_dequantize_linear_epilogue_and_standalone_chain():
     ex.add_node("add", "Add", ["y1", "b"], ["y2"])
     out = ex.run({"a": a}, ["y2"])["y2"]
     entries, _ = ex.plan()
-    assert [e.pattern for e in entries if e.kind == "FusedHead"] == ["MulAdd"]
+    assert [(e.pattern, e.steps) for e in entries if e.kind == "FusedHead"] == [("QuantizedLinear", 3)]
     acc = oracle.matmul_integer(a, w, a_zp, None)
     want = oracle.add(oracle.mul(oracle.dequantize_linear(acc, s, None), m), b)
-    assert_bits_equal(out, want, "dequantize + MulAdd")
+    assert_bits_equal(out, want, "MatMulInteger + DequantizeLinear + Mul + Add in one head")
+    got = ex.run({"a": a}, ["y2", "acc"])
+    assert [e.pattern for e in ex.plan()[0] if e.kind == "FusedHead"] == ["MulAdd"]
+    assert np.array_equal(got["acc"], acc)
+    assert_bits_equal(got["y2"], want, "dequantize + MulAdd")
 
 
 def test_shape_guard_and_dynamic_dims():

@@ -73,11 +73,13 @@ def oracle_of(op, ins, attrs):
         return oracle.transpose(v[0], tuple(perm))
     if op == "MatMul":
         return oracle.matmul_f32(*v)
+    if op == "Gather":
+        return oracle.gather(*v, axis=attrs.get("axis", 0))
     return None
 
 
 # (op -> how the GPU result must relate to the file's expected output)
-EXACT_VS_FILE = {"Add", "Sub", "Mul", "Div", "MatMulInteger", "DequantizeLinear", "Transpose"}
+EXACT_VS_FILE = {"Add", "Sub", "Mul", "Div", "MatMulInteger", "DequantizeLinear", "Transpose", "Gather"}
 TOL_VS_FILE = {"LayerNormalization": 1e-5, "Softmax": 1e-6, "Erf": 5e-7, "MatMul": 1e-6}
 
 

@@ -333,3 +333,44 @@ def test_qlinear_graph_close_to_float64():
     xq, xs, xzp = out["xq"], float(out["x_scale"]), int(out["x_zp"])
     ref = ((xq.astype(np.float64) - xzp) @ w.astype(np.float64)) * xs * 0.02 + bias
     np.testing.assert_allclose(out["linear"], ref, rtol=1e-5, atol=1e-5)
+
+
+# --------------------------------------------------------------------------------------
+# Gather
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("case", ["test_gather_0", "test_gather_1", "test_gather_2d_indices",
+                                  "test_gather_negative_indices"])
+def test_gather_onnx_goldens(goldens, case):
+    g = goldens[case]
+    data, idx = (tensor(t) for t in g["inputs"])
+    out = oracle.gather(data, idx, axis=(g["attributes"] or {}).get("axis", 0))
+    want = tensor(g["outputs"][0])
+    assert out.shape == want.shape and out.dtype == want.dtype
+    np.testing.assert_array_equal(bits(out), bits(want))
+
+
+def test_gather_bruteforce_negative_and_clamped_indices():
+    """Element by element in pure Python: out[pre, idx, post] = data[pre, k(idx), post] with
+    k = i + len when negative, then clamped into the axis (the GPU kernels' rule)."""
+    rng = np.random.default_rng(5)
+    data = rng.integers(0, 256, (3, 5, 4)).astype(np.uint8)
+    for axis in (0, 1, 2, -1):
+        ax = axis % 3
+        n = data.shape[ax]
+        idx = np.array([[0, n - 1, -1], [-n, n + 2, -n - 3]], np.int64)
+        out = oracle.gather(data, idx, axis=axis)
+        assert out.dtype == np.uint8
+        assert out.shape == data.shape[:ax] + idx.shape + data.shape[ax + 1:]
+        for o in np.ndindex(out.shape):
+            i = idx[o[ax:ax + 2]]
+            k = i + n if i < 0 else i
+            k = min(max(k, 0), n - 1)
+            src = o[:ax] + (k,) + o[ax + 2:]
+            assert out[o] == data[src], (axis, o)
+
+
+def test_gather_identity_and_reversal():
+    x = np.arange(2 * 7 * 3, dtype=np.float32).reshape(2, 7, 3)
+    np.testing.assert_array_equal(oracle.gather(x, np.arange(7), axis=1), x)
+    np.testing.assert_array_equal(oracle.gather(x, np.arange(-1, -8, -1), axis=1), np.flip(x, axis=1))
+    assert oracle.gather(x, np.array(3, np.int64), axis=1).shape == (2, 3)
