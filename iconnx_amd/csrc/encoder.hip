@@ -10,7 +10,9 @@
 //   MatMul f32 (batched)           src/operators/matmul.rs:20-150; LDS-tiled FMA kernel.
 //   Attention (fused)              the decomposed Reshape/Transpose/MatMul/scale/Softmax/
 //       MatMul/Transpose/Reshape subgraph of a BERT self-attention, over [B, S, H*D]
-//       activations, with fp32 MFMA (v_mfma_f32_32x32x2f32) and the softmax in registers.
+//       activations, with fp32 MFMA (v_mfma_f32_16x16x4f32): two blocks per (batch, head),
+//       each of four waves of 16 queries; S^T = K Q^T leaves every lane one query's scores in
+//       the A-operand layout of the P V product, so the softmax stays in registers.
 #include "icx_common.hpp"
 #include "internal.hpp"
 #include <cmath>
