@@ -266,6 +266,25 @@ def time_replays(step, steps, warmup, torch):
     return e0.elapsed_time(e1) / steps, time.perf_counter() - t0
 
 
+def host_info():
+    """The CPU the baseline ran on: logical CPUs this process may use (nproc) and the model
+    name from /proc/cpuinfo (what lscpu prints as 'Model name')."""
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        cores = os.cpu_count()
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"host_cores": cores, "cpu_model": model, "threads_used": 1}
+
+
 def encoder_cpu_baseline():
     """The oracle (single-threaded C restatement of the reference CPU ops, composed op by op)
     running the same 6-layer encoder on one sequence [1, 128, 768] — a bounded sample of the
@@ -284,7 +303,8 @@ def encoder_cpu_baseline():
     dt = time.perf_counter() - t0
     assert npx.all(npx.isfinite(x))
     return {"value": round(1.0 / dt, 4), "unit": "seq/s", "cores": 1, "kind": "port",
-            "sample": "one sequence [1,128,768] through the 6 layers op by op (%.1f s measured)" % dt}
+            "sample": "one sequence [1,128,768] through the 6 layers op by op (%.1f s measured)" % dt,
+            **host_info()}
 
 
 def measured_traffic(cfg):
@@ -484,6 +504,12 @@ def main():
                 "kernel_avg_us": round(k_us, 3), "algorithmic_bytes": alg_bytes}
         if r.ops_count is not None:
             roof["kernel_int8_TOPS"] = round(r.ops_count / (k_us * 1e-6) / 1e12, 2)
+    mfma = None
+    if r.ops_count is not None:  # the metric's "% MFMA peak": step and dominant kernel
+        k_tops = r.ops_count / (k_us * 1e-6) / 1e12
+        mfma = {"peak_TOPS": PEAK_INT8_TOPS, "step_TOPS": round(value, 2),
+                "step_frac": round(value / PEAK_INT8_TOPS, 4), "kernel_TOPS": round(k_tops, 2),
+                "kernel_frac": round(k_tops / PEAK_INT8_TOPS, 4)}
 
     workload = {
         "cfg1": "cfg1: DQL + quantized linear x[1,128,768] W[768,768] + bias",
@@ -504,6 +530,7 @@ def main():
         "data": "synthetic: seeded N(0,1) activations (SplitMix64 + Box-Muller), random-init int8 weights",
         "config": cfg, "roofline": roof,
         "timing": {"graph_replay": not args.no_graph, "wall_s": round(wall, 4), **extra},
+        **({"mfma": mfma} if mfma else {}),
         "traffic_source": "profiles/traffic_hbm_pmc.txt (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
     }
     if args.config in ("cfg5b", "copy"):
@@ -513,13 +540,17 @@ def main():
         enc = EncoderRunner()
         ms_e, _ = time_replays(enc.step, 50, 5, torch)
         enc.ex.check_status()  # a quantized-output launch that failed on the device raises
+        e_tops = enc.int8_ops / (ms_e * 1e-3) / 1e12
         out["encoder"] = {"metric": "encoder seq/s", "value": round(enc.B / (ms_e * 1e-3), 1),
                           "unit": "seq/s", "ms_per_forward": round(ms_e, 4),
-                          "int8_TOPS": round(enc.int8_ops / (ms_e * 1e-3) / 1e12, 2),
+                          "int8_TOPS": round(e_tops, 2), "int8_frac_of_mfma_peak": round(e_tops / PEAK_INT8_TOPS, 4),
                           "workload": ENCODER_WORKLOAD, "graph_replay": True}
+        if not args.no_cpu_baseline:
+            out["encoder"]["cpu_baseline"] = encoder_cpu_baseline()
     if not args.no_cpu_baseline and args.config != "copy":
         cb = cpu_baseline(args.config, args.cpu_rows)
         cb["cores"] = 1
+        cb.update(host_info())
         out["cpu_baseline"] = cb
     print(json.dumps(out), flush=True)
 

@@ -10,11 +10,20 @@
 //   Block b of both launches runs on the same XCD (b mod 8) and reads the same bytes, so
 //   launch 2 re-reads x from that XCD's L2 (small tensors) or the Infinity Cache.
 //
+// The graph executor also has a single-launch form for small inputs (icx::dql_exchange, flat
+// mode, at most kExchangeMaxBlocks blocks): every block keeps its 1024 elements of x in
+// registers, the blocks trade their (min, max) pairs through the tagged-slot exchange of
+// qexchange.hpp, and each block quantizes from its registers.  Measured on MI355X (kernel
+// durations): 7.1 us against 3.2 + 4.9 us for the two launches at 98304 elements, but 9.2
+// against 8.3 us at 393216 and 13.0 against 10.6 us at 3.1M — the exchange's agent-scope
+// round trips cost ~4 us, which only beats a second launch while the pass itself is short.
+//
 // Semantics and per-element rounding: dql_core.hpp (DynamicQuantizeLinear::forward,
 // src/operators/dynamic_quantize_linear.rs:32-112).
 #include "icx_common.hpp"
 #include "internal.hpp"
 #include "dql_core.hpp"
+#include "qexchange.hpp"
 
 namespace {
 
@@ -221,11 +230,73 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
     }
 }
 
+// Single launch, flat mode: block b holds the float4s [256 b, 256 b + 256) of x in registers
+// (one per lane), the last block also the n % 4 scalar tail.  The block's (min, max) goes
+// through the exchange; once every block's pair is in, each block quantizes its registers
+// and writes y.  A block whose wait ran out writes its part of y as 0 (the last block out
+// then writes the scale as NaN and counts the launch in the exchange buffer's error word).
+// `poison` is 0 but for the fault test hook, which makes every wait expect a tag no block
+// publishes.
+constexpr int kExchangeMaxBlocks = 128;  // inputs up to 128 * 1024 (+ 3) elements
+
+__global__ void __launch_bounds__(kThreads)
+dql_exchange_kernel(const float* __restrict__ x, size_t n4, int tail, uint8_t* __restrict__ y,
+                    float* __restrict__ y_scale, uint8_t* __restrict__ y_zp, unsigned* sync,
+                    unsigned poison, int spin) {
+    const unsigned tag = icx::qx::read_tag(sync);
+    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    const float4 v = i < n4 ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool has_tail = blockIdx.x == gridDim.x - 1 && (int)threadIdx.x < tail;
+    const float xt = has_tail ? x[n4 * 4 + threadIdx.x] : 0.0f;  // 0.0 never moves the range
+    float mn = 0.0f, mx = 0.0f;
+    acc4(v, mn, mx);
+    acc_minmax(xt, mn, mx);
+    block_minmax<kThreads>(mn, mx);
+    if (threadIdx.x == 0) icx::qx::publish(sync, tag, mn, mx);
+    bool ok;
+    const DqlParams p = icx::qx::gather<kThreads>(sync, tag ^ poison, spin, ok);
+    if (i < n4) reinterpret_cast<uint32_t*>(y)[i] = ok ? quant4(v, p) : 0u;
+    if (has_tail) y[n4 * 4 + threadIdx.x] = ok ? (uint8_t)quant1(xt, p) : (uint8_t)0;
+    if (threadIdx.x == 0) icx::qx::finish(sync, ok, p, y_scale, y_zp);
+}
 
 }  // namespace
 
-// The single-launch path: aligned operands, whole float4s, and a slice that fits kFRegs
-// float4 per lane (flat) or whole rows that do (row mode).
+int icx::dql_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                      unsigned* sync) {
+    if (!x || !y || !y_scale || !y_zp || !sync)
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "DQL exchange: null pointer");
+    if (n == 0 || !icx::aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 3u) != 0)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: empty or unaligned operands");
+    const size_t n4 = n / 4;
+    const size_t G = icx::cdiv(std::max<size_t>(n4, 1), (size_t)kThreads);
+    if (G > (size_t)kExchangeMaxBlocks)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: %zu elements need %zu blocks, more than %d", n, G,
+                 kExchangeMaxBlocks);
+    static int per_cu[64] = {0};
+    int d = 0;
+    ICX_HIP_CHECK(hipGetDevice(&d));
+    if (d < 0 || d >= 64) ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: device index %d", d);
+    if (!per_cu[d]) {
+        int nb = 0;
+        ICX_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, dql_exchange_kernel, kThreads, 0));
+        per_cu[d] = nb > 0 ? nb : -1;
+    }
+    if (per_cu[d] < 0 || G > (size_t)per_cu[d] * icx::num_cus())
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: %zu blocks exceed the %d resident ones", G,
+                 per_cu[d] * icx::num_cus());
+    int spin = 1 << 20;
+    unsigned poison = 0;
+    if (const int f = icx::qout_fault_spin()) {  // test hook
+        spin = f;
+        poison = 0x80000000u;
+    }
+    hipLaunchKernelGGL(dql_exchange_kernel, dim3((unsigned)G), dim3(kThreads), 0, s, x, n4, (int)(n % 4), y,
+                       y_scale, y_zp, sync, poison, spin);
+    ICX_LAUNCH_CHECK("dql_exchange_kernel");
+    return ICX_OK;
+}
+
 extern "C" size_t icx_dql_workspace_size(size_t) { return sizeof(float2) * kMaxBlocks; }
 
 // The quantize launch alone, folding partials a producing kernel left (the same grid choice

@@ -262,7 +262,8 @@ struct icx_graph {
     std::map<std::string, std::pair<std::string, int>> range_of;  // DQL x -> (partials tensor, count)
     std::set<std::string> dql_done;  // DQL outputs already written by their producer's GEMM
     int64_t quant_fused = 0;         // GEMM launches that quantized their own output
-    unsigned* qsync = nullptr;       // exchange buffer of those launches (zeroed once)
+    int64_t dql_single = 0;          // DynamicQuantizeLinear runs done as one launch
+    unsigned* qsync = nullptr;       // exchange buffer of both kinds of launch (zeroed once)
     hipStream_t last_stream = nullptr;
     bool ran = false;
     Pool pool;
@@ -1783,6 +1784,16 @@ class Runner {
                                            static_cast<uint8_t*>(Z->ptr), R ? static_cast<int32_t*>(R->ptr) : nullptr,
                                            row_len, static_cast<const float2*>(P->ptr), rg->second.second);
         }
+        if (!R && g_.qsync && cnt > 0) {  // one launch, the blocks trading ranges through qsync
+            rc = icx::dql_exchange(s_, x, cnt, static_cast<uint8_t*>(Y->ptr), static_cast<float*>(S->ptr),
+                                   static_cast<uint8_t*>(Z->ptr), g_.qsync);
+            if (rc == ICX_OK) {
+                ++g_.dql_single;
+                return ICX_OK;
+            }
+            if (rc != ICX_ERR_UNSUPPORTED) return rc;
+            icx::clear_error();  // too large or unaligned: the two-launch path
+        }
         rc = workspace(icx_dql_workspace_size(cnt));
         if (rc) return rc;
         return icx_dynamic_quantize_linear(s_, x, cnt, static_cast<uint8_t*>(Y->ptr), static_cast<float*>(S->ptr),
@@ -2092,6 +2103,7 @@ static int icx_graph_plan_impl(icx_graph* g, char* buf, size_t buf_len) {
         for (auto& r : g->range_wanted) o << "range " << r << "\n";
         for (auto& q : g->quant_out) o << "quantout " << q.first << " " << q.second.name << "\n";
         if (g->quant_fused) o << "quantout-launches " << g->quant_fused << "\n";
+        if (g->dql_single) o << "dql-single-launches " << g->dql_single << "\n";
         const std::string s = o.str();
         if (s.size() + 1 > buf_len)
             ICX_FAIL(ICX_ERR_INVALID_ARG, "plan: summary needs %zu bytes, buffer has %zu", s.size() + 1, buf_len);
@@ -2109,7 +2121,11 @@ static int icx_graph_compile_impl(icx_graph* g, icx_stream_t stream) {
     if (g->ran && g->last_stream) ICX_HIP_CHECK(hipStreamSynchronize(g->last_stream));
     g->clear_run();
     g->free_weights();
-    if (!g->quant_out.empty()) {  // zeroed once; every launch leaves it valid for the next
+    // the range-exchange buffer, for quantized-output GEMMs and single-launch DQLs
+    bool exchange = !g->quant_out.empty();
+    for (auto& op : g->plan)
+        if (op.kind == Kind::Regular && op.node.op == "DynamicQuantizeLinear") exchange = true;
+    if (exchange) {  // zeroed once; every launch leaves it valid for the next
         ICX_HIP_CHECK(hipMalloc(&g->qsync, icx::kQoutSyncBytes));
         ICX_HIP_CHECK(hipMemsetAsync(g->qsync, 0, icx::kQoutSyncBytes, s));
         ICX_HIP_CHECK(hipStreamSynchronize(s));
@@ -2376,9 +2392,10 @@ extern "C" int icx_graph_status(icx_graph* g, icx_stream_t stream) {
         ICX_HIP_CHECK(hipMemsetAsync(word, 0, sizeof failed, s));
         ICX_HIP_CHECK(hipStreamSynchronize(s));
         ICX_FAIL(ICX_ERR_KERNEL,
-                 "QuantizedLinear+DynamicQuantizeLinear: %u launch(es) since the last status check had a block "
-                 "whose wait for the other blocks' ranges ran out (they were not all resident, e.g. other work "
-                 "held CUs); their quantized outputs are invalid (y = 0, scale = NaN)",
+                 "DynamicQuantizeLinear range exchange: %u launch(es) since the last status check (quantized-output "
+                 "GEMMs or single-launch DQLs) had a block whose wait for the other blocks' ranges ran out (they "
+                 "were not all resident, e.g. other work held CUs); their quantized outputs are invalid (y = 0, "
+                 "scale = NaN)",
                  failed);
     }
     return ICX_OK;

@@ -1275,18 +1275,6 @@ void launch_dma_narrow(int out_kind, int ch, unsigned blocks, hipStream_t s, con
 
 // Persistent producer / consumer kernel: grid = min(tiles, resident blocks), resident
 // blocks from the occupancy calculator (cached per instantiation and device).
-int num_cus() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
 
 template <int BM, int BN, int WGM, int WGN, int NP, int NS, int OUT, int CH>
 int launch_stream_one(unsigned tiles, hipStream_t s, GemmArgs g) {
@@ -1303,7 +1291,7 @@ int launch_stream_one(unsigned tiles, hipStream_t s, GemmArgs g) {
             nb = 1;
         per_cu[d] = nb;
     }
-    unsigned grid = (unsigned)(per_cu[d] * num_cus());
+    unsigned grid = (unsigned)(per_cu[d] * icx::num_cus());
     if (grid > tiles) grid = tiles;
     if (grid > (unsigned)icx::kMaxRangeParts) g.part = nullptr;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), 0, s, g);
@@ -1336,9 +1324,9 @@ int launch_qout(unsigned blocks, hipStream_t s, const GemmArgs& g) {
         ICX_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 768, 0));
         per_cu[d] = n > 0 ? n : -1;
     }
-    if (per_cu[d] < 0 || blocks > (unsigned)(per_cu[d] * num_cus()))
+    if (per_cu[d] < 0 || blocks > (unsigned)(per_cu[d] * icx::num_cus()))
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: %u blocks exceed the %d resident ones", blocks,
-                 per_cu[d] * num_cus());
+                 per_cu[d] * icx::num_cus());
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(768), 0, s, g);
     ICX_LAUNCH_CHECK("gemm_i8_dma128_kernel (quantized output)");
     return ICX_OK;
@@ -1448,7 +1436,7 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     // kernel, whose 8 MFMA waves per tile hide the long K loop better than 4.  (The encoder's
     // FFN-down projection, 4096x3072x768, runs faster as 768 tiles of 64x64.)
     const bool stream = dma && (out_kind == OUT_I32 || ch != CH_GENERAL) && K >= 2048 &&
-                        icx::cdiv(M, 64) * icx::cdiv(N, 64) < (size_t)num_cus();
+                        icx::cdiv(M, 64) * icx::cdiv(N, 64) < (size_t)icx::num_cus();
     if (stream) {
         g.tiles_m = (int)icx::cdiv(M, 128);
         g.tiles_n = (int)icx::cdiv(N, 128);
@@ -1461,17 +1449,17 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     // 256x192 tiles when they give every CU at least one (and no partial column tile):
     // fewer operand bytes per output than three 128x128 tiles per CU
     const bool mid = !big && dma && K % 128 == 0 && N % 192 == 0 && (out_kind == OUT_I32 || ch != CH_GENERAL) &&
-                     icx::cdiv(M, 256) * (N / 192) >= (size_t)num_cus() &&
+                     icx::cdiv(M, 256) * (N / 192) >= (size_t)icx::num_cus() &&
                      (n_seg == 0 || (N / n_seg) % 192 == 0);
     // 128x96 tiles (12 waves of 32x32) when those give every CU at least one, for a single
     // output (the encoder's FFN-down 4096x3072x768: 24.3 -> 21.0 us; its output projection
     // 4096x768x768: 10.2 -> 9.1 us; over a Q/K/V group the segmented store ran slower)
     const bool narrow = !big && !mid && dma && K % 128 == 0 && N % 96 == 0 && n_seg == 0 &&
                         (out_kind == OUT_I32 || ch != CH_GENERAL) &&
-                        icx::cdiv(M, 128) * (N / 96) >= (size_t)num_cus();
+                        icx::cdiv(M, 128) * (N / 96) >= (size_t)icx::num_cus();
     // 64x64 tiles when 128x128 ones would leave CUs idle (up to six blocks per CU to hide
     // each K step's latency)
-    const bool small = dma && !big && !mid && !narrow && icx::cdiv(M, 128) * icx::cdiv(N, 128) < (size_t)num_cus();
+    const bool small = dma && !big && !mid && !narrow && icx::cdiv(M, 128) * icx::cdiv(N, 128) < (size_t)icx::num_cus();
     if (big) {
         g.tiles_m = (int)icx::cdiv(M, 256);
         g.tiles_n = (int)icx::cdiv(N, 256);
@@ -1605,6 +1593,8 @@ static std::atomic<int> g_qout_fault_spin{0};
 
 extern "C" void icx_debug_qout_fault(int spin) { g_qout_fault_spin.store(spin > 0 ? spin : 0); }
 
+int icx::qout_fault_spin() { return g_qout_fault_spin.load(std::memory_order_relaxed); }
+
 int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int b_dtype,
                      const int32_t* b_colsum, size_t M, size_t K, size_t N, const void* a_zp,
                      const icx_chain* chain, uint8_t* y, float* y_scale, uint8_t* y_zp, unsigned* sync) {
@@ -1650,7 +1640,7 @@ int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp
     g.q_sync = sync;
     g.q_spin = 1 << 20;
     g.q_poison = 0;
-    if (const int f = g_qout_fault_spin.load(std::memory_order_relaxed)) {  // test hook
+    if (const int f = icx::qout_fault_spin()) {  // test hook
         g.q_spin = f;
         g.q_poison = 0x80000000u;
     }

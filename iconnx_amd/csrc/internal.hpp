@@ -7,6 +7,20 @@
 
 namespace icx {
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+inline int num_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 // icx_layer_norm_f32 leaving up to kMaxRangeParts (min, max) partials of y in `part`
 // (may be null); *n_part = partials written, 0 when this shape's kernel leaves none.
 int layer_norm_f32(hipStream_t s, const float* x, const float* residual, size_t rows, size_t cols,
@@ -48,6 +62,18 @@ constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 int qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int b_dtype, const int32_t* b_colsum,
                 size_t M, size_t K, size_t N, const void* a_zp, const icx_chain* chain, uint8_t* y,
                 float* y_scale, uint8_t* y_zp, unsigned* sync);
+
+// DynamicQuantizeLinear of a small flat x as one launch: the blocks keep x in registers and
+// trade their (min, max) through `sync` (the layout, contract and failure reporting of
+// qlinear_dql's).  Needs 16-byte aligned x, 4-byte aligned y and n <= 128 * 1024 + 3 (it is
+// slower than the two launches beyond that); otherwise ICX_ERR_UNSUPPORTED, having launched
+// nothing.  y, y_scale, y_zp equal icx_dynamic_quantize_linear's bit for bit.
+int dql_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                 unsigned* sync);
+
+// The fault test hook of the exchange launches (icx_debug_qout_fault): 0 normally, else the
+// number of polls after which a wait gives up, every wait expecting a tag nobody publishes.
+int qout_fault_spin();
 
 // DynamicQuantizeLinear of x from the n_part partials its producer left: one launch (the
 // quantize pass of icx_dynamic_quantize_linear, which folds them).

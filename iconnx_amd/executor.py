@@ -164,7 +164,7 @@ class GpuGraphExecutor:
                 check(rc)
             size *= 4
         entries, rowsums, ranges, quant_out = [], [], [], {}
-        self._quant_launches = 0
+        self._quant_launches = self._dql_single = 0
         for line in buf.value.decode().splitlines():
             parts = line.split()
             if parts[0] == "rowsum":
@@ -178,6 +178,9 @@ class GpuGraphExecutor:
                 continue
             if parts[0] == "quantout-launches":
                 self._quant_launches = int(parts[1])
+                continue
+            if parts[0] == "dql-single-launches":
+                self._dql_single = int(parts[1])
                 continue
             extra = dict(p.split("=", 1) for p in parts[4:])
             entries.append(PlanEntry(parts[0], parts[1], parts[2], parts[3],
@@ -193,6 +196,12 @@ class GpuGraphExecutor:
         tensor is never formed.  Second value: how many GEMM launches so far did that."""
         self.plan()
         return dict(self._quant_out), self._quant_launches
+
+    def single_launch_dqls(self):
+        """How many DynamicQuantizeLinear runs so far were one launch (the blocks trading
+        their ranges through the graph's exchange buffer) rather than two."""
+        self.plan()
+        return self._dql_single
 
     def range_inputs(self):
         """DynamicQuantizeLinear inputs whose producing kernel (LayerNorm, attention, a

@@ -215,6 +215,47 @@ def test_ffn_down_shape_fused_epilogue():
         assert_f32_equal(y[r0:r1], ref["y"][r0:r1], "rows %d:%d" % (r0, r1))
 
 
+def test_division_fast_path_edge_values():
+    """The GEMM epilogues divide by a column operand d as q0 = RN(v * RN(1/d)) plus one FMA
+    correction when v and d lie in [2^-60, 2^60) in magnitude, and by the IEEE division
+    otherwise.  cfg2's shape (one 256x192 tile per CU) with a Mul before the Div that makes
+    the numerators of chosen columns exactly +-0, subnormal, tiny, huge, inf or NaN, and
+    divisors that are 0, tiny, huge, negative or have an all-ones significand (blocks holding
+    an out-of-range divisor take the IEEE division for the whole step): bit-exact against the
+    oracle's op-by-op graph on every sampled row."""
+    rng = np.random.default_rng(41)
+    M, K, N = 4096, 768, 3072
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    w_scale = np.float32(0.01)
+    bias = (0.05 * rng.standard_normal(N)).astype(np.float32)
+    m = rng.uniform(0.5, 2.0, N).astype(np.float32)
+    specials = [0.0, -0.0, 1e-40, -3e-39, 1e-35, 1e-19, 1e19, 1e30, -1e30, np.inf, -np.inf, np.nan]
+    for i, v in enumerate(specials):  # every special numerator in a few columns of several tiles
+        m[[7 + i, 200 + 3 * i, 1500 + i, N - 1 - i]] = v
+    d = rng.uniform(0.25, 4.0, N).astype(np.float32)
+    d[::5] *= -1.0
+    d[11::97] = np.float32(1.9999999)  # all-ones significand
+    d[3::211] = np.float32(-1.9999999)
+    # out-of-range divisors in three column tiles only: the other tiles keep the fast path
+    d[[400, 2000, 2001, 2900]] = np.array([0.0, 1e-30, -1e25, 5e-19], np.float32)
+    chain = [("Mul", m, False), ("Div", d, False), ("Add", bias, False), ("Div", d[::-1].copy(), False)]
+    xq, xs, xzp, rs = ops.gpu_dynamic_quantize_linear(dev(x), rowsum_row_len=K)
+    pw = ops.PackedWeight(dev(w))
+    epi = [("Mul", (xs, dev(np.array(w_scale))), False), ("Add", dev(bias), False)]
+    epi += [(op, dev(v), lhs) for op, v, lhs in chain]
+    y = ops.gpu_qlinear(xq, pw, xzp, None, epilogue=epi, a_rowsum=rs)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    with np.errstate(all="ignore"):
+        for r0, r1 in [(0, 40), (1024, 1040), (2040, 2056), (M - 40, M)]:
+            ref = oracle.qlinear_graph(x, w, np.array(0, np.int8), np.array(w_scale), bias, chain,
+                                       rows=(r0, r1))
+            got, want = y[r0:r1], ref["y"][r0:r1]
+            bad = int(np.count_nonzero(bits(got) != bits(want)))
+            assert bad == 0, "rows %d:%d: %d of %d differ" % (r0, r1, bad, want.size)
+
+
 def test_persistent_kernel_gelu_epilogue():
     """The operand-free erf / save steps through the persistent kernel (K = 2048)."""
     rng = np.random.default_rng(37)
