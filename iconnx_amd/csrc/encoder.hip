@@ -307,6 +307,12 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int ATT_S = 128, ATT_D = 64, ATT_QB = 64;  // keys, head size, queries per block
 constexpr int K_STRIDE = ATT_D + 4;   // floats per LDS row of K: 16-byte reads conflict-free
 constexpr int VT_STRIDE = ATT_S + 4;  // V^T rows [dim][key]
+// Key k of V^T row d is stored at column k ^ vt_swz(d).  With the 132-float rows alone, the
+// transposing stores (a wave writes 16 dims x 4 keys of one component per instruction) hit
+// only 16 of the 64 banks; the XOR of bits 2-3 of the key by bits 4-5 of the dim spreads them
+// over all 64, keeps every 4-key group contiguous and 16-byte aligned for the P V reads, and
+// leaves those reads (16 dims of one 4-key group per 16 lanes) conflict-free as well.
+__device__ __forceinline__ int vt_swz(int d) { return 4 * ((d >> 4) & 3); }
 constexpr int ATT_LDS_FLOATS = ATT_S * K_STRIDE > ATT_D * VT_STRIDE ? ATT_S * K_STRIDE : ATT_D * VT_STRIDE;
 
 struct AttnArgs {
@@ -410,7 +416,7 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
     __syncthreads();  // every wave is done with K: the region takes V^T
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-        const int r = u * 16 + (t >> 4);
+        const int r = (u * 16 + (t >> 4)) ^ vt_swz(c4);  // c4 .. c4 + 3 share bits 4-5
         lds[(c4 + 0) * VT_STRIDE + r] = vr[u].x;
         lds[(c4 + 1) * VT_STRIDE + r] = vr[u].y;
         lds[(c4 + 2) * VT_STRIDE + r] = vr[u].z;
@@ -460,7 +466,8 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
         float4 vq[4];
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
-            vq[dt] = *reinterpret_cast<const float4*>(lds + (16 * dt + lq) * VT_STRIDE + 16 * kt + 4 * lg);
+            vq[dt] = *reinterpret_cast<const float4*>(lds + (16 * dt + lq) * VT_STRIDE +
+                                                      ((16 * kt + 4 * lg) ^ vt_swz(16 * dt + lq)));
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
