@@ -158,7 +158,8 @@ struct EpiLayout {
     static constexpr int WN = BN / WGN;
     static constexpr int SROW = WN + 8;  // floats per staged row (4-row offset = 32 banks)
     static constexpr int STAGE_BYTES = NW * 32 * SROW * 4;
-    static constexpr int BYTES = STAGE_BYTES + ICX_MAX_CHAIN * BN * 4;  // + column operands
+    static constexpr int ROWT_OFF = STAGE_BYTES + ICX_MAX_CHAIN * BN * 4;  // after the column operands
+    static constexpr int BYTES = ROWT_OFF + BM * 4;                        // + the tile's row terms
 };
 
 // ---- epilogue ---------------------------------------------------------------------------
@@ -210,17 +211,20 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
     const bool vec_out = (ov.ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(ov.base) & 15u) == 0);
     const bool rng = OUT == OUT_F32 && g.part != nullptr;  // uniform: track the DQL range
     float* stage = reinterpret_cast<float*>(smem) + wid * 32 * SROW;
+    // The row terms of the tile's BM rows, staged once (one load per thread) rather than 16
+    // loads per lane per slab, whose latency every slab would wait for.
+    uint32_t* srow = reinterpret_cast<uint32_t*>(smem + EL::ROWT_OFF);
+    if (g.rowsum_raw)
+        for (int r = t; r < BM; r += NT) srow[r] = (uint32_t)g.rowsum_raw[min(m0 + r, g.M - 1)] - aK;
 
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
         const int rbase = m0 + wm * WM + i * 32;
+        __syncthreads();  // previous slab read back; column operands and row terms written
         uint32_t rterm[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = min(rbase + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), g.M - 1);
-            rterm[r] = g.rowsum_raw ? (uint32_t)g.rowsum_raw[row] - aK : 0u;
-        }
-        __syncthreads();  // previous slab read back; column operands written
+        for (int r = 0; r < 16; ++r)
+            rterm[r] = g.rowsum_raw ? srow[wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] : 0u;
         // without row sums (the weight zero point folded away) the row term is 0: a uniform
         // branch drops its 32-bit multiply (a quarter-rate instruction) from every element
         auto stage_slab = [&](bool with_rows) {
