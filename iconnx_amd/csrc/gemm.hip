@@ -159,7 +159,98 @@ struct EpiLayout {
     static constexpr int SROW = WN + 8;  // floats per staged row (4-row offset = 32 banks)
     static constexpr int STAGE_BYTES = NW * 32 * SROW * 4;
     static constexpr int ROWT_OFF = STAGE_BYTES + ICX_MAX_CHAIN * BN * 4;  // after the column operands
-    static constexpr int BYTES = ROWT_OFF + BM * 4;                        // + the tile's row terms
+    static constexpr int COLT_OFF = ROWT_OFF + BM * 4;                     // after the row terms
+    static constexpr int BYTES = COLT_OFF + 2 * BN * 4;                    // + column terms and factors
+};
+
+__device__ const uint8_t kZeroByte = 0;
+__device__ const float kOneF = 1.0f;
+
+// A load through a global-address-space pointer: a generic (flat) load would also count in
+// lgkmcnt, so every later scalar-load wait would wait for it too.
+template <typename T>
+__device__ __forceinline__ T load_global(const T* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
+
+// The global operands of a tile's epilogue, held in registers by the wave that stages them:
+// both factors of the chain's column operands, the column sums, the zero points and the row
+// sums.  The tiled kernels load them before their main loop, so that the loads' latency
+// (about 1.7 us at the start of a chip-wide epilogue) hides under it; gemm_epilogue writes
+// them to LDS.  Wave w covers columns 64 (w % CG) .. +63 and chain steps OPW (w / CG) ..
+// +OPW-1; waves w < BM / 64 cover rows 64 w .. +63.  Every load is unconditional (an absent
+// factor or zero point reads a constant), so all of them are in flight at once.
+template <int BM, int BN, int NW, bool OPS>
+struct EpiOperands {
+    static constexpr int CG = (BN + 63) / 64;
+    static_assert(NW % CG == 0, "column groups must split over the waves");
+    static constexpr int OPW = OPS ? (ICX_MAX_CHAIN + NW / CG - 1) / (NW / CG) : 1;
+    static constexpr int RG = (BM + 63) / 64;
+    static_assert(RG <= NW, "one row group per wave");
+    float f0[OPW], f1[OPW];
+    int32_t csum = 0, rsum = 0;
+    uint8_t azp = 0, bzp = 0;
+
+    // `wid` must be wave-uniform (readfirstlane): the op fields are then scalar loads of the
+    // kernel arguments and the selects below are branch-free, so no load waits for another.
+    __device__ __forceinline__ void load(const GemmArgs& g, int m0, int n0, int wid, int lane) {
+        const int c = min(n0 + (wid % CG) * 64 + lane, g.N - 1);
+        const int og = wid / CG;
+        if constexpr (OPS) {
+#pragma unroll
+            for (int i = 0; i < OPW; ++i) {
+                const int k = og * OPW + i;
+                const icx_chain_op& op = g.chain.ops[min(k, ICX_MAX_CHAIN - 1)];
+                const bool live = k < g.chain.n_ops && icx::op_takes_operand(op.op);
+                f0[i] = load_global(live ? op.p0 + (op.kind0 == ICX_BCAST_SCALAR ? 0 : c) : &kOneF);
+                f1[i] = load_global((live && op.p1) ? op.p1 + (op.kind1 == ICX_BCAST_SCALAR ? 0 : c) : &kOneF);
+            }
+        }
+        // a zero offset the compiler cannot see through: as a uniform value the activation's
+        // zero point would be moved to a scalar register right after its load, a wait for it
+        int zero = 0;
+        asm volatile("" : "+v"(zero));
+        azp = load_global((g.a_zp ? reinterpret_cast<const uint8_t*>(g.a_zp) : &kZeroByte) + zero);
+        if (og == 0) {
+            csum = load_global(g.colsum + c);
+            bzp = load_global(g.b_zp ? reinterpret_cast<const uint8_t*>(g.b_zp) + (g.b_zp_len == 1 ? 0 : c) : &kZeroByte);
+        }
+        if (g.rowsum_raw && wid < RG) rsum = load_global(g.rowsum_raw + min(m0 + wid * 64 + lane, g.M - 1));
+    }
+
+    // Column terms (the zero-point correction's per-column part and factor), chain operands
+    // and row terms of the tile into the epilogue's LDS areas (read after a barrier).
+    __device__ __forceinline__ void stage(const GemmArgs& g, int8_t* smem, int stage_bytes, int rowt_off,
+                                          int colt_off, int wid, int lane) const {
+        const int cl = (wid % CG) * 64 + lane;
+        const int og = wid / CG;
+        const int a_zp = g.a_zp_u8 ? (int)azp : (int)(int8_t)azp;
+        const uint32_t amz = (uint32_t)(g.alpha - a_zp);
+        const uint32_t aK = (uint32_t)g.alpha * (uint32_t)g.K;
+        if (cl < BN) {
+            if constexpr (OPS) {
+                float* sop = reinterpret_cast<float*>(smem + stage_bytes);
+#pragma unroll
+                for (int k = 0; k < ICX_MAX_CHAIN; ++k) {
+                    if (k / OPW != og) continue;
+                    if (k < g.chain.n_ops && icx::op_takes_operand(g.chain.ops[k].op)) {
+                        float a = f0[k % OPW];
+                        if (g.chain.ops[k].p1) a = __fmul_rn(a, f1[k % OPW]);
+                        sop[k * BN + cl] = icx::div_feeds_erf(g.chain, k) ? __fdiv_rn(1.0f, a) : a;
+                    }
+                }
+            }
+            if (og == 0) {
+                const int b_zp = g.b_zp_u8 ? (int)bzp : (int)(int8_t)bzp;
+                const uint32_t colfac = (uint32_t)(g.beta - b_zp);
+                uint32_t* sct = reinterpret_cast<uint32_t*>(smem + colt_off);
+                sct[cl] = amz * (uint32_t)csum + (uint32_t)g.K * amz * colfac;
+                sct[BN + cl] = colfac;
+            }
+        }
+        if (g.rowsum_raw && wid < RG && wid * 64 + lane < BM)
+            reinterpret_cast<uint32_t*>(smem + rowt_off)[wid * 64 + lane] = (uint32_t)rsum - aK;
+    }
 };
 
 // ---- epilogue ---------------------------------------------------------------------------
@@ -169,12 +260,15 @@ struct EpiLayout {
 // consecutive columns per lane with its column operands in LDS, and the global stores are
 // 16-byte and contiguous along rows.  `smem` must not be in use by the main loop any more.
 template <int BM, int BN, int WGM, int WGN, int OUT, int CH>
+using EpiOperandsFor = EpiOperands<BM, BN, WGM * WGN, OUT == OUT_F32 && CH != CH_GENERAL>;
+
+template <int BM, int BN, int WGM, int WGN, int OUT, int CH>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
                                               v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
-                                              int8_t* smem, int m0, int n0, float& mn, float& mx) {
+                                              int8_t* smem, int m0, int n0, float& mn, float& mx,
+                                              const EpiOperandsFor<BM, BN, WGM, WGN, OUT, CH>& eo) {
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
-    constexpr int NT = 64 * WGM * WGN;
     using EL = EpiLayout<BM, BN, WGM, WGN>;
     constexpr int SROW = EL::SROW;
     const int t = threadIdx.x;
@@ -182,45 +276,33 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g,
     const int wm = wid / WGN, wn = wid % WGN;
     const int lr = lane & 31;
 
-    const int azp = load_zp(g.a_zp, g.a_zp_u8, 0);
-    const uint32_t amz = (uint32_t)(g.alpha - azp);
-    const uint32_t aK = (uint32_t)g.alpha * (uint32_t)g.K;
+    eo.stage(g, smem, EL::STAGE_BYTES, EL::ROWT_OFF, EL::COLT_OFF, __builtin_amdgcn_readfirstlane(wid), lane);
+    const uint32_t* sct = reinterpret_cast<const uint32_t*>(smem + EL::COLT_OFF);
     uint32_t colterm[TJ], colfac[TJ];
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int col = min(n0 + wn * WN + j * 32 + lr, g.N - 1);
-        const int bzp = load_zp(g.b_zp, g.b_zp_u8, g.b_zp_len == 1 ? 0 : col);
-        colfac[j] = (uint32_t)(g.beta - bzp);
-        colterm[j] = amz * (uint32_t)g.colsum[col] + (uint32_t)g.K * amz * colfac[j];
-    }
     constexpr int LPR = WN / 4;       // lanes per staged row in the read phase
     constexpr int RPI = 64 / LPR;     // rows per read iteration
     const int cc = (lane % LPR) * 4;  // this lane's 4 columns within the wave tile
     const int rsub = lane / LPR;
     const int gcol = n0 + wn * WN + cc;
-    float* sop = reinterpret_cast<float*>(smem + EL::STAGE_BYTES);
-    if (OUT == OUT_F32 && CH != CH_GENERAL) {
-#pragma unroll
-        for (int k = 0; k < ICX_MAX_CHAIN; ++k) {
-            if (k < g.chain.n_ops && icx::op_takes_operand(g.chain.ops[k].op)) {
-                for (int c = t; c < BN; c += NT) sop[k * BN + c] = icx::col_operand(g.chain, k, min(n0 + c, g.N - 1));
-            }
-        }
-    }
+    const float* sop = reinterpret_cast<const float*>(smem + EL::STAGE_BYTES);
     const OutView ov = out_view(g, n0);
     const bool vec_out = (ov.ld % 4 == 0) && ((reinterpret_cast<uintptr_t>(ov.base) & 15u) == 0);
     const bool rng = OUT == OUT_F32 && g.part != nullptr;  // uniform: track the DQL range
     float* stage = reinterpret_cast<float*>(smem) + wid * 32 * SROW;
-    // The row terms of the tile's BM rows, staged once (one load per thread) rather than 16
-    // loads per lane per slab, whose latency every slab would wait for.
-    uint32_t* srow = reinterpret_cast<uint32_t*>(smem + EL::ROWT_OFF);
-    if (g.rowsum_raw)
-        for (int r = t; r < BM; r += NT) srow[r] = (uint32_t)g.rowsum_raw[min(m0 + r, g.M - 1)] - aK;
+    // the tile's row terms, staged once rather than loaded by every lane for every slab
+    const uint32_t* srow = reinterpret_cast<const uint32_t*>(smem + EL::ROWT_OFF);
 
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
         const int rbase = m0 + wm * WM + i * 32;
         __syncthreads();  // previous slab read back; column operands and row terms written
+        if (i == 0) {
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                colterm[j] = sct[wn * WN + j * 32 + lr];
+                colfac[j] = sct[BN + wn * WN + j * 32 + lr];
+            }
+        }
         uint32_t rterm[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r)
@@ -382,7 +464,9 @@ __global__ void __launch_bounds__(kThreads) gemm_i8_kernel(GemmArgs g) {
     }
 
     float mn = 0.0f, mx = 0.0f;
-    gemm_epilogue<BM, BN, 2, 2, OUT, CH>(g, acc, smem, m0, n0, mn, mx);
+    EpiOperandsFor<BM, BN, 2, 2, OUT, CH> eo;
+    eo.load(g, m0, n0, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), threadIdx.x & 63);
+    gemm_epilogue<BM, BN, 2, 2, OUT, CH>(g, acc, smem, m0, n0, mn, mx, eo);
     if (OUT == OUT_F32 && g.part) icx::block_range_store<kThreads>(mn, mx, g.part);
 }
 
@@ -485,8 +569,15 @@ gemm_i8_dma_kernel(GemmArgs g) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
     const int KT = g.K / ROWB;
+    // the epilogue's operands are requested between the first stage's copies and the next
+    // ones: loads complete in issue order, so the stage-0 wait below (which leaves the last
+    // stage's copies in flight) also covers them, and the main loop's waits count the same
+    // copies as without them
+    EpiOperandsFor<BM, BN, WGM, WGN, OUT, CH> eo;
+    issue(0, 0);
+    eo.load(g, m0, n0, __builtin_amdgcn_readfirstlane(wid), lane);
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) issue(s, min(s, KT - 1));
+    for (int s = 1; s < NS - 1; ++s) issue(s, min(s, KT - 1));
 
     // Fragment double buffering: the reads of one 32-wide half step are issued a phase
     // ahead of its MFMAs.  Per K step kt:
@@ -543,7 +634,7 @@ gemm_i8_dma_kernel(GemmArgs g) {
     wait_vmcnt<0>();
     __syncthreads();  // all copies landed and all fragment reads done: LDS is free
     float mn = 0.0f, mx = 0.0f;
-    gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0, mn, mx);
+    gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0, mn, mx, eo);
     if (OUT == OUT_F32 && g.part) icx::block_range_store<64 * WGM * WGN>(mn, mx, g.part);
 }
 
@@ -759,7 +850,12 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
         }
     };
 
+    // the epilogue's operands are requested between stage 0's copies and stage 1's: loads
+    // complete in issue order, so the stage-0 wait below also covers them, and the main
+    // loop's waits count the same copies as without them
+    EpiOperandsFor<BM, BN, WGM, WGN, OUT, CH> eo;
     issue(0, 0);
+    if constexpr (QOUT == 0) eo.load(g, m0, n0, __builtin_amdgcn_readfirstlane(wid), lane);
     issue(1, min(1, KT - 1));
     wait_vmcnt<PA + PB>();  // stage 0 has landed
     __syncthreads();
@@ -796,7 +892,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
         qout_epilogue<BM, BN, WGM, WGN, CH>(g, acc, smem, m0, n0, q_tag);
         return;
     }
-    gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0, mn, mx);
+    gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0, mn, mx, eo);
     if (OUT == OUT_F32 && g.part) icx::block_range_store<64 * WGM * WGN>(mn, mx, g.part);
 }
 
