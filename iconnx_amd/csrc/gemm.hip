@@ -650,36 +650,35 @@ gemm_i8_dma_kernel(GemmArgs g) {
 // The exchange (q_sync, bounded waits, NaN scale on failure) is qexchange.hpp's.
 template <int BM, int BN, int WGM, int WGN, int CH>
 __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
-                                              int8_t* smem, int m0, int n0, unsigned tag) {
+                                              int8_t* smem, int m0, int n0, unsigned tag,
+                                              const EpiOperandsFor<BM, BN, WGM, WGN, OUT_F32, CH>& eo) {
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
     constexpr int NT = 64 * WGM * WGN;
     constexpr int MODE = CH == CH_COL_EXT ? 2 : 0;
     constexpr int QS = BN + 16;                          // bytes per staged u8 row
     constexpr int SOP_BYTES = ICX_MAX_CHAIN * BN * 4;
-    static_assert(SOP_BYTES + BM * QS <= (BM + BN) * 256, "LDS regions fit the tile buffer");
+    constexpr int COLT_OFF = SOP_BYTES + BM * QS;        // column terms after the byte tile
+    constexpr int ROWT_OFF = COLT_OFF + 2 * BN * 4;      // (no row terms here: unused)
+    static_assert(ROWT_OFF + BM * 4 <= (BM + BN) * 256, "LDS regions fit the tile buffer");
     const int t = threadIdx.x;
     const int lane = t & 63, wid = t >> 6;
     const int wm = wid / WGN, wn = wid % WGN;
     const int lr = lane & 31;
-    float* sop = reinterpret_cast<float*>(smem);
+    const float* sop = reinterpret_cast<const float*>(smem);
     uint8_t* qs = reinterpret_cast<uint8_t*>(smem) + SOP_BYTES;
-    if (t < BN) {
-#pragma unroll
-        for (int k = 0; k < ICX_MAX_CHAIN; ++k)
-            if (k < g.chain.n_ops && icx::op_takes_operand(g.chain.ops[k].op))
-                sop[k * BN + t] = icx::col_operand(g.chain, k, min(n0 + t, g.N - 1));
-    }
-    const int azp = load_zp(g.a_zp, g.a_zp_u8, 0);
-    const uint32_t amz = (uint32_t)(g.alpha - azp);
+    // chain operands and column terms (the weight zero point is folded away: beta = 0 and no
+    // b_zp, so the column term is (alpha - a_zp) * colsum) from the operands loaded before
+    // the main loop
+    eo.stage(g, smem, 0, ROWT_OFF, COLT_OFF, __builtin_amdgcn_readfirstlane(wid), lane);
+    const uint32_t* sct = reinterpret_cast<const uint32_t*>(smem + COLT_OFF);
     __syncthreads();
 
     float mn = 0.0f, mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int c = wn * WN + j * 32 + lr;  // column within the tile
-        const int col = min(n0 + c, g.N - 1);
-        const uint32_t colterm = amz * (uint32_t)g.colsum[col] + (uint32_t)g.K * amz * (uint32_t)g.beta;
+        const uint32_t colterm = sct[c];
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
             float4 v[4];
@@ -855,7 +854,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
     // loop's waits count the same copies as without them
     EpiOperandsFor<BM, BN, WGM, WGN, OUT, CH> eo;
     issue(0, 0);
-    if constexpr (QOUT == 0) eo.load(g, m0, n0, __builtin_amdgcn_readfirstlane(wid), lane);
+    eo.load(g, m0, n0, __builtin_amdgcn_readfirstlane(wid), lane);
     issue(1, min(1, KT - 1));
     wait_vmcnt<PA + PB>();  // stage 0 has landed
     __syncthreads();
@@ -889,7 +888,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
     __syncthreads();  // all copies landed and all fragment reads done: LDS is free
     float mn = 0.0f, mx = 0.0f;
     if constexpr (QOUT != 0) {
-        qout_epilogue<BM, BN, WGM, WGN, CH>(g, acc, smem, m0, n0, q_tag);
+        qout_epilogue<BM, BN, WGM, WGN, CH>(g, acc, smem, m0, n0, q_tag, eo);
         return;
     }
     gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0, mn, mx, eo);
