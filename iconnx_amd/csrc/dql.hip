@@ -243,15 +243,17 @@ __global__ void __launch_bounds__(kThreads)
 dql_exchange_kernel(const float* __restrict__ x, size_t n4, int tail, uint8_t* __restrict__ y,
                     float* __restrict__ y_scale, uint8_t* __restrict__ y_zp, unsigned* sync,
                     unsigned poison, int spin) {
-    const unsigned tag = icx::qx::read_tag(sync);
     const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
     const float4 v = i < n4 ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     const bool has_tail = blockIdx.x == gridDim.x - 1 && (int)threadIdx.x < tail;
     const float xt = has_tail ? x[n4 * 4 + threadIdx.x] : 0.0f;  // 0.0 never moves the range
+    __shared__ unsigned s_tag;
+    if (threadIdx.x == 0) s_tag = icx::qx::read_tag(sync);
     float mn = 0.0f, mx = 0.0f;
     acc4(v, mn, mx);
     acc_minmax(xt, mn, mx);
-    block_minmax<kThreads>(mn, mx);
+    block_minmax<kThreads>(mn, mx);  // (its barrier also shares s_tag)
+    const unsigned tag = s_tag;
     if (threadIdx.x == 0) icx::qx::publish(sync, tag, mn, mx);
     bool ok;
     const DqlParams p = icx::qx::gather<kThreads>(sync, tag ^ poison, spin, ok);

@@ -650,7 +650,7 @@ gemm_i8_dma_kernel(GemmArgs g) {
 // The exchange (q_sync, bounded waits, NaN scale on failure) is qexchange.hpp's.
 template <int BM, int BN, int WGM, int WGN, int CH>
 __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
-                                              int8_t* smem, int m0, int n0, unsigned tag,
+                                              int8_t* smem, int m0, int n0, const unsigned& tag,
                                               const EpiOperandsFor<BM, BN, WGM, WGN, OUT_F32, CH>& eo) {
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
@@ -801,9 +801,12 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
         srcB[i] = g.Bp + (size_t)min(n0 + row, g.N - 1) * g.K + 16 * kc;
     }
     const int KT = g.K / ROWB;
-    // the launch number of a quantized-output launch, read before the main loop hides its latency
-    unsigned q_tag = 0;
-    if constexpr (QOUT != 0) q_tag = icx::qx::read_tag(g.q_sync);
+    // the launch number of a quantized-output launch: read by one thread before its first
+    // copies (so the stage-0 wait covers it and the main loop hides its latency), shared
+    // through LDS at the epilogue
+    __shared__ unsigned s_qtag;
+    unsigned q_tag0 = 0;
+    if (QOUT != 0 && t == 0) q_tag0 = icx::qx::read_tag(g.q_sync);
     auto issue = [&](int buf, int kt) {
         if (!copier) return;
         const int k0 = kt * ROWB;
@@ -888,7 +891,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
     __syncthreads();  // all copies landed and all fragment reads done: LDS is free
     float mn = 0.0f, mx = 0.0f;
     if constexpr (QOUT != 0) {
-        qout_epilogue<BM, BN, WGM, WGN, CH>(g, acc, smem, m0, n0, q_tag, eo);
+        if (t == 0) s_qtag = q_tag0;  // read by every thread after the epilogue's first barrier
+        qout_epilogue<BM, BN, WGM, WGN, CH>(g, acc, smem, m0, n0, s_qtag, eo);
         return;
     }
     gemm_epilogue<BM, BN, WGM, WGN, OUT, CH>(g, acc, smem, m0, n0, mn, mx, eo);

@@ -38,7 +38,10 @@ __device__ __forceinline__ unsigned long long* slots(unsigned* sync) {
     return reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(sync) + 256);
 }
 
-// E + 1 for this launch; read it early (before the main work) to hide the latency.
+// E + 1 for this launch; read it early (before the main work) to hide the latency, in one
+// thread of the block, and share it through LDS after a barrier: a read by every thread puts
+// thousands of loads on one address at once, and since a wave's loads complete in issue
+// order, that wave's later loads would wait behind the queue.
 __device__ __forceinline__ unsigned read_tag(unsigned* sync) {
     return __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
 }
