@@ -394,13 +394,25 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
     __syncthreads();
 
     // S^T: A = K (lane = key), B = Q^T (lane = query); K fragments of tile kt+1 are read
-    // during the MFMAs of tile kt
+    // during the MFMAs of tile kt, and tile kt-1's scores are scaled, masked and folded into
+    // the row max then (VALU work under the MFMAs)
     v4f st[8];
     float4 kf[2][4];
     auto read_k = [&](int kt, float4 (&f)[4]) {
         const float* kp = lds + (16 * kt + lq) * K_STRIDE + 16 * lg;
 #pragma unroll
         for (int u = 0; u < 4; ++u) f[u] = *reinterpret_cast<const float4*>(kp + 4 * u);
+    };
+    float m = -INFINITY;
+    auto scale_mask_max = [&](int kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = 16 * kt + 4 * lg + r;
+            float x = a.scale_q ? st[kt][r] : apply_scale(st[kt][r], a);
+            if (key >= S) x = -INFINITY;
+            st[kt][r] = x;
+            m = fmaxf(m, x);
+        }
     };
     read_k(0, kf[0]);
 #pragma unroll
@@ -412,7 +424,9 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4c(kf[kt & 1][u], e), f4c(qr[u], e), st[kt], 0, 0, 0);
+        if (kt > 0) scale_mask_max(kt - 1);
     }
+    scale_mask_max(7);
     __syncthreads();  // every wave is done with K: the region takes V^T
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -423,38 +437,23 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
         lds[(c4 + 3) * VT_STRIDE + r] = vr[u].w;
     }
 
-    // softmax of row qi over its S keys: 32 in this lane, the rest in lanes l ^ 16, l ^ 32
-    float m = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int key = 16 * kt + 4 * lg + r;
-            float x = a.scale_q ? st[kt][r] : apply_scale(st[kt][r], a);
-            if (key >= S) x = -INFINITY;
-            st[kt][r] = x;
-            m = fmaxf(m, x);
-        }
+    // softmax of row qi over its S keys: 32 in this lane, the rest in lanes l ^ 16, l ^ 32.
+    // The row max is complete; the exponentials of key tile kt + 1 are computed during the
+    // P V MFMAs of tile kt, and the context is divided by the row sum once at the end
+    // (ctx = (sum_k e_k v_k) / sum_k e_k): the hardware exp2 and one reciprocal per row, within
+    // a few ulp of expf and of e / sum, far inside the attention's tolerance.
     m = fmaxf(m, __shfl_xor(m, 16, 64));
     m = fmaxf(m, __shfl_xor(m, 32, 64));
-    // hardware exp2 and one reciprocal per row: within a few ulp of expf and of e / sum,
-    // far inside the attention's tolerance, at a fraction of the VALU work
     float sum = 0.0f;
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
+    auto expo = [&](int kt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const float e = __expf(__fsub_rn(st[kt][r], m));
             st[kt][r] = e;
             sum = __fadd_rn(sum, e);
         }
-    sum = __fadd_rn(sum, __shfl_xor(sum, 16, 64));
-    sum = __fadd_rn(sum, __shfl_xor(sum, 32, 64));
-    const float inv = __fdiv_rn(1.0f, sum);
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) st[kt][r] = __fmul_rn(st[kt][r], inv);
+    };
+    expo(0);
     __syncthreads();  // V^T written
 
     // ctx = P V: A = P from the S^T registers, B = V^T rows of dims 16 dt + lq
@@ -473,7 +472,19 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[kt][r], f4c(vq[dt], r), o[dt], 0, 0, 0);
+        if (kt + 1 < 8) expo(kt + 1);
     }
+    sum = __fadd_rn(sum, __shfl_xor(sum, 16, 64));
+    sum = __fadd_rn(sum, __shfl_xor(sum, 32, 64));
+    // lane l's context rows are queries 4 lg + r (of its 16): their sums sit in lanes 4 lg + r
+    const float inv = __fdiv_rn(1.0f, sum);
+    float inv_r[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inv_r[r] = __shfl(inv, 4 * lg + r, 64);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[dt][r] = __fmul_rn(o[dt][r], inv_r[r]);
     // lane l holds ctx rows (queries) 16 w + 4 lg + r, dims 16 dt + lq
     float mn = 0.0f, mx = 0.0f;  // DQL range of out (when a.part is given)
 #pragma unroll
