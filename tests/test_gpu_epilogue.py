@@ -277,3 +277,52 @@ def test_persistent_kernel_gelu_epilogue():
                                                np.float32(1.0))), np.float32(0.5))
     err = float(np.max(np.abs(y.astype(np.float64) - want)) / np.max(np.abs(want)))
     assert err < 1e-6, err
+
+
+# One shape per tile configuration of the fused GEMM (gemm.hip picks the tile from the shape):
+# 256x256 on 128-byte K rows and on 64-byte K rows, 256x192, 128x96, 128x128, 64x64, and the
+# register-staged kernel (K not a multiple of 16).
+TILE_SHAPES = [
+    ("256x256", 8192, 256, 4096),
+    ("256x256 64-byte rows", 8192, 192, 4096),
+    ("256x192", 4096, 256, 3072),
+    ("128x96", 4096, 256, 768),
+    ("128x128", 2048, 128, 2048),
+    ("64x64", 128, 256, 768),
+    ("register-staged", 300, 100, 512),
+]
+
+
+@pytest.mark.parametrize("name,M,K,N", TILE_SHAPES, ids=[s[0] for s in TILE_SHAPES])
+@pytest.mark.parametrize("w_kind", ["i8", "u8 per-channel zp"])
+def test_full_length_chain_every_tile(name, M, K, N, w_kind):
+    """The longest epilogue the chain descriptor holds (ICX_MAX_CHAIN = 8 steps: dequant Mul,
+    bias Add and six more), with per-column and scalar operands on both sides, IEEE
+    divisions, and products of two factors in its last steps, on every tile configuration:
+    each kernel loads the operands of its tile's columns before its main loop, spread over
+    its waves (column groups x chain steps), so every step position and column group is
+    exercised.  Bit-exact against the oracle run op by op, on sampled rows."""
+    rng = np.random.default_rng(M + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if w_kind == "i8":
+        w = rng.integers(-127, 128, (K, N)).astype(np.int8)
+        w_zp = np.array(0, np.int8)
+    else:
+        w = rng.integers(0, 256, (K, N)).astype(np.uint8)
+        w_zp = rng.integers(120, 136, N).astype(np.uint8)
+    w_scale = (0.01 + 0.01 * rng.random(N)).astype(np.float32)
+    bias = (0.05 * rng.standard_normal(N)).astype(np.float32)
+    col = [(0.5 + rng.random(N)).astype(np.float32) for _ in range(5)]
+    s1, s2, s3 = (np.array(v, np.float32) for v in (1.25, 0.75, 3.0))
+    chain = [("Mul", col[0], False), ("Sub", s1, True), ("Div", col[1], False),
+             ("Add", col[2], True), ("Mul", (s2, col[3]), False), ("Div", (col[4], s3), True)]
+    xq, xs, xzp, rs = ops.gpu_dynamic_quantize_linear(dev(x), rowsum_row_len=K)
+    epi = [("Mul", (xs, dev(w_scale)), False), ("Add", dev(bias), False)]
+    epi += [(op, tuple(dev(t) for t in c) if isinstance(c, tuple) else dev(c), lhs) for op, c, lhs in chain]
+    y = ops.gpu_qlinear(xq, ops.PackedWeight(dev(w)), xzp, dev(w_zp), epilogue=epi, a_rowsum=rs)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    ochain = [(op, oracle.mul(*c) if isinstance(c, tuple) else c, lhs) for op, c, lhs in chain]
+    for r0, r1 in ((0, 8), (M // 2 - 3, M // 2 + 5), (M - 8, M)):
+        ref = oracle.qlinear_graph(x, w, w_zp, w_scale, bias, ochain, rows=(r0, r1))
+        assert_f32_equal(y[r0:r1], ref["y"][r0:r1], "%s %s rows %d:%d" % (name, w_kind, r0, r1))
