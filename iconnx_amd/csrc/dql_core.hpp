@@ -138,11 +138,15 @@ __device__ __forceinline__ uint32_t quant4(float4 v, const DqlParams& p) {
         const bool ok = fabsf(q0 - r0) < 0.4999f && fabsf(q1 - r1) < 0.4999f &&
                         fabsf(q2 - r2) < 0.4999f && fabsf(q3 - r3) < 0.4999f;
         if (ok) {
-            const uint32_t a = (uint32_t)__builtin_amdgcn_fmed3f(r0 + (float)p.zp, 0.0f, 255.0f);
-            const uint32_t b = (uint32_t)__builtin_amdgcn_fmed3f(r1 + (float)p.zp, 0.0f, 255.0f);
-            const uint32_t c = (uint32_t)__builtin_amdgcn_fmed3f(r2 + (float)p.zp, 0.0f, 255.0f);
-            const uint32_t d = (uint32_t)__builtin_amdgcn_fmed3f(r3 + (float)p.zp, 0.0f, 255.0f);
-            return a | (b << 8) | (c << 16) | (d << 24);
+            // r + zp is an integer (exact in f32, or huge and then clamped anyway);
+            // v_cvt_pk_u8_f32 clamps it to [0, 255] and writes it into its byte of the word
+            // (checked on the MI355X: clamp and round-to-nearest-even, the other bytes kept),
+            // one instruction per element instead of med3, convert, shift and or
+            const float zf = (float)p.zp;
+            uint32_t q = __builtin_amdgcn_cvt_pk_u8_f32(r0 + zf, 0, 0u);
+            q = __builtin_amdgcn_cvt_pk_u8_f32(r1 + zf, 1, q);
+            q = __builtin_amdgcn_cvt_pk_u8_f32(r2 + zf, 2, q);
+            return __builtin_amdgcn_cvt_pk_u8_f32(r3 + zf, 3, q);
         }
     }
     return quant1(v.x, p) | (quant1(v.y, p) << 8) | (quant1(v.z, p) << 16) |
