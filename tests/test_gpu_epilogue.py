@@ -280,13 +280,14 @@ def test_persistent_kernel_gelu_epilogue():
 
 
 # One shape per tile configuration of the fused GEMM (gemm.hip picks the tile from the shape):
-# 256x256 on 128-byte K rows and on 64-byte K rows, 256x192, 128x96, 128x128, 64x64, and the
-# register-staged kernel (K not a multiple of 16).
+# 256x256 on 128-byte K rows and on 64-byte K rows, 256x192, 128x96, 64x96, 128x128, 64x64,
+# and the register-staged kernel (K not a multiple of 16).
 TILE_SHAPES = [
     ("256x256", 8192, 256, 4096),
     ("256x256 64-byte rows", 8192, 192, 4096),
     ("256x192", 4096, 256, 3072),
-    ("128x96", 4096, 256, 768),
+    ("128x96", 8192, 256, 768),
+    ("64x96", 4096, 256, 768),
     ("128x128", 2048, 128, 2048),
     ("64x64", 128, 256, 768),
     ("register-staged", 300, 100, 512),
