@@ -81,26 +81,28 @@ layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ res, si
 }
 
 // The same arithmetic, in the same order, for the BERT hidden sizes (cols = 8 * PER): a
-// block of four waves normalises 8 consecutive rows.  All four stage the rows (x +
-// residual, formed once) into LDS with float4 loads; wave 0 then runs the order-fixed
-// reductions — lane (r, j) walks its strided partial x[j], x[j+8], ... of row r from LDS
-// into registers — and leaves each row's mean and standard deviation in LDS; the output
-// pass, independent per element, is spread over all 256 lanes with coalesced stores.  A
-// staged row is cols + 8 floats long, so the strided reads of the 8 rows fall into
-// distinct banks.
-template <int PER>
+// block of four waves normalises ROWS (4 or 8) consecutive rows.  All four stage the rows
+// (x + residual, formed once) into LDS with float4 loads; the first 8·ROWS lanes of wave 0
+// then run the order-fixed reductions — lane (r, j) walks its strided partial x[j], x[j+8],
+// ... of row r from LDS into registers — and leave each row's mean and standard deviation in
+// LDS; the output pass, independent per element, is spread over all 256 lanes with
+// coalesced stores.  A staged row is cols + 8 floats long, so the strided reads of the rows
+// fall into distinct banks.  Every block is resident at once and its phases (loads, the
+// serial reductions, stores) are latency-bound, so more, smaller blocks finish sooner: 4 rows
+// per block where the range partials allow it.
+template <int PER, int ROWS>
 __global__ void __launch_bounds__(256)
-layer_norm_rows8_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t rows,
+layer_norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t rows,
                         const float* __restrict__ scale, const float* __restrict__ bias, float eps,
                         float* __restrict__ y, float2* __restrict__ part) {
     constexpr int cols = 8 * PER, C4 = cols / 4, STRIDE = cols + 8;
-    constexpr int PL = 8 * C4 / 256;  // float4 per lane for 8 rows
-    static_assert(PL * 256 == 8 * C4, "8 rows split evenly over the block");
-    __shared__ __attribute__((aligned(16))) float tile[8 * STRIDE];
-    __shared__ float stat[2][8];  // mean, sd per row
+    constexpr int PL = ROWS * C4 / 256;  // float4 per lane for ROWS rows
+    static_assert(PL * 256 == ROWS * C4, "the rows split evenly over the block");
+    __shared__ __attribute__((aligned(16))) float tile[ROWS * STRIDE];
+    __shared__ float stat[2][ROWS];  // mean, sd per row
     const int t = threadIdx.x;
-    const size_t row0 = (size_t)blockIdx.x * 8;
-    const int nr = (int)(rows - row0 < 8 ? rows - row0 : 8);
+    const size_t row0 = (size_t)blockIdx.x * ROWS;
+    const int nr = (int)(rows - row0 < ROWS ? rows - row0 : ROWS);
     const float4* x4 = reinterpret_cast<const float4*>(x + row0 * cols);
     const float4* r4 = res ? reinterpret_cast<const float4*>(res + row0 * cols) : nullptr;
     {
@@ -130,7 +132,7 @@ layer_norm_rows8_kernel(const float* __restrict__ x, const float* __restrict__ r
         }
     }
     __syncthreads();
-    if (t < 64) {
+    if (t < 8 * ROWS) {
         const int r = t >> 3, j = t & 7;
         if (r < nr) {  // whole 8-lane groups
             const float* tr = tile + r * STRIDE + j;
@@ -502,6 +504,15 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
 }
 
 
+template <int PER>
+void launch_ln_rows(bool rows4, dim3 grid, hipStream_t s, const float* x, const float* res, size_t rows,
+                    const float* scale, const float* bias, float eps, float* y, float2* part) {
+    if (rows4)
+        hipLaunchKernelGGL((layer_norm_rows_kernel<PER, 4>), grid, dim3(256), 0, s, x, res, rows, scale, bias, eps, y, part);
+    else
+        hipLaunchKernelGGL((layer_norm_rows_kernel<PER, 8>), grid, dim3(256), 0, s, x, res, rows, scale, bias, eps, y, part);
+}
+
 unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
     size_t b = icx::cdiv(work, per_block);
     if (b < 1) b = 1;
@@ -517,16 +528,18 @@ int icx::layer_norm_f32(hipStream_t s, const float* x, const float* residual, si
     if (!x || !scale || !bias || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "LayerNormalization: null pointer argument");
     if (cols == 0 && rows) ICX_FAIL(ICX_ERR_SHAPE, "LayerNormalization: empty normalized axis");
     if (rows == 0) return ICX_OK;
-    const dim3 g8((unsigned)icx::cdiv(rows, 8));
-    // partials only from the LDS-staged kernel, one per block of 8 rows
+    // partials only from the LDS-staged kernel, one per block: blocks of 4 rows while their
+    // partials fit, else of 8
+    const bool rows4 = icx::cdiv(rows, 4) <= (size_t)icx::kMaxRangeParts;
+    const dim3 g8((unsigned)icx::cdiv(rows, rows4 ? 4 : 8));
     float2* pp = (part && g8.x <= (unsigned)icx::kMaxRangeParts) ? part : nullptr;
     // the hidden sizes of the BERT family, float4-aligned: rows staged through LDS
     const bool a16 = icx::aligned16(x) && icx::aligned16(y) && icx::aligned16(scale) &&
                      icx::aligned16(bias) && (!residual || icx::aligned16(residual));
     switch (a16 ? cols : 0) {
-        case 512: hipLaunchKernelGGL(layer_norm_rows8_kernel<64>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y, pp); break;
-        case 768: hipLaunchKernelGGL(layer_norm_rows8_kernel<96>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y, pp); break;
-        case 1024: hipLaunchKernelGGL(layer_norm_rows8_kernel<128>, g8, dim3(256), 0, s, x, residual, rows, scale, bias, eps, y, pp); break;
+        case 512: launch_ln_rows<64>(rows4, g8, s, x, residual, rows, scale, bias, eps, y, pp); break;
+        case 768: launch_ln_rows<96>(rows4, g8, s, x, residual, rows, scale, bias, eps, y, pp); break;
+        case 1024: launch_ln_rows<128>(rows4, g8, s, x, residual, rows, scale, bias, eps, y, pp); break;
         default:
             pp = nullptr;
             hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)icx::cdiv(rows, 32)), dim3(kThreads), 0, s, x,

@@ -34,7 +34,7 @@ def rel_err(got, want):
     return float(np.max(np.abs(got - want)) / max(float(np.max(np.abs(want))), 1e-30))
 
 
-@pytest.mark.parametrize("rows,cols", [(4096, 768), (97, 1024), (33, 3072), (5, 13), (64, 5)])
+@pytest.mark.parametrize("rows,cols", [(4096, 768), (4109, 768), (4100, 768), (3, 768), (97, 1024), (33, 3072), (5, 13), (64, 5)])
 def test_layer_norm_bit_exact(rows, cols):
     rng = np.random.default_rng(cols)
     x = (rng.standard_normal((rows, cols)) * 2 + 0.5).astype(np.float32)
