@@ -33,6 +33,20 @@ constexpr int kU = 8;  // float4 loads per lane in flight in the streaming loops
 
 using namespace icx::dql;
 
+// y's stores in the flat quantize launch: non-temporal for the stand-alone op, plain for
+// the graph executor's DQLs.  Measured on MI355X: non-temporal stores take the dirty y lines
+// out of the launch's end-of-kernel L2 write-back (cfg2 step: quantize 8.16 -> 6.84 us, the
+// GEMM after it unchanged, 435 -> 442 TOPS), but the encoder's consumer GEMMs then run
+// 0.4-0.6 us slower each (forward 1.03 -> 1.04 ms), and in the row-sum form the cfg4 step
+// loses 2.6 us (921 -> 910 TOPS), so that form keeps plain stores.
+template <bool NT>
+__device__ __forceinline__ void put_y(uint32_t* p, uint32_t v) {
+    if constexpr (NT)
+        icx::store_nt_u32(p, v);
+    else
+        *p = v;
+}
+
 __device__ __forceinline__ uint32_t bytesum4(uint32_t q) {
     return __builtin_amdgcn_udot4(q, 0x01010101u, 0u, false);
 }
@@ -109,6 +123,7 @@ dql_minmax_kernel(const float* __restrict__ x, size_t units, size_t unit, size_t
 
 // Flat quantize of this block's slice: lane-consecutive float4 in, 4 bytes out.
 // `vec`: x 16-byte and y 4-byte aligned (unit == 4).
+template <bool NT>
 __global__ void __launch_bounds__(kThreads)
 dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size_t tail, int vec,
                     uint8_t* __restrict__ y, const float2* __restrict__ part, int G,
@@ -136,7 +151,7 @@ dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size
         while (true) {
 #pragma unroll
             for (int j = 0; j < kU; ++j)
-                if (i + j * kThreads < end4) y4[i + j * kThreads] = quant4(v[j], p);
+                if (i + j * kThreads < end4) put_y<NT>(&y4[i + j * kThreads], quant4(v[j], p));
             i += kU * kThreads;
             if (i >= end4) break;
 #pragma unroll
@@ -332,17 +347,14 @@ int icx::dql_from_parts(hipStream_t s, const float* x, size_t n, uint8_t* y, flo
     }
     const int G = (int)std::max<size_t>(1, std::min<size_t>({(size_t)kMaxBlocks, icx::cdiv(n, (size_t)kThreads * 16), units}));
     const int qvec = (x16 && y4 && unit == 4) ? 1 : 0;
-    hipLaunchKernelGGL(dql_quantize_kernel, dim3(G), dim3(kThreads), 0, s, x, units, unit, tail, qvec, y, part,
+    hipLaunchKernelGGL(dql_quantize_kernel<false>, dim3(G), dim3(kThreads), 0, s, x, units, unit, tail, qvec, y, part,
                        n_part, y_scale, y_zp);
     ICX_LAUNCH_CHECK("dql_quantize_kernel");
     return ICX_OK;
 }
 
-extern "C" int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, size_t n,
-                                           uint8_t* y, float* y_scale, uint8_t* y_zp,
-                                           int32_t* opt_rowsum, size_t row_len, void* ws,
-                                           size_t ws_bytes) {
-    icx::clear_error();
+int icx::dql_two_launch(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                        int32_t* opt_rowsum, size_t row_len, void* ws, size_t ws_bytes, bool nt_y) {
     if (!x || !y || !y_scale || !y_zp)
         ICX_FAIL(ICX_ERR_INVALID_ARG, "DynamicQuantizeLinear: null pointer argument");
     if (!ws || ws_bytes < icx_dql_workspace_size(n))
@@ -351,7 +363,6 @@ extern "C" int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, 
     if (opt_rowsum && (row_len == 0 || n % row_len != 0))
         ICX_FAIL(ICX_ERR_SHAPE, "DynamicQuantizeLinear: row_len %zu does not divide n = %zu",
                  row_len, n);
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     float2* part = reinterpret_cast<float2*>(ws);
     const bool x16 = icx::aligned16(x), y4 = (reinterpret_cast<uintptr_t>(y) & 3u) == 0;
     // Partition: rows in row mode, float4 groups (or single elements) otherwise.  Both
@@ -388,9 +399,22 @@ extern "C" int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, 
         ICX_LAUNCH_CHECK("dql_quantize_rows_kernel");
     } else {
         const int qvec = (x16 && y4 && unit == 4) ? 1 : 0;
-        hipLaunchKernelGGL(dql_quantize_kernel, dim3(G), dim3(kThreads), 0, s, x, units, unit,
-                           tail, qvec, y, part, G, y_scale, y_zp);
+        if (nt_y)
+            hipLaunchKernelGGL(dql_quantize_kernel<true>, dim3(G), dim3(kThreads), 0, s, x, units, unit,
+                               tail, qvec, y, part, G, y_scale, y_zp);
+        else
+            hipLaunchKernelGGL(dql_quantize_kernel<false>, dim3(G), dim3(kThreads), 0, s, x, units, unit,
+                               tail, qvec, y, part, G, y_scale, y_zp);
         ICX_LAUNCH_CHECK("dql_quantize_kernel");
     }
     return ICX_OK;
+}
+
+extern "C" int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, size_t n,
+                                           uint8_t* y, float* y_scale, uint8_t* y_zp,
+                                           int32_t* opt_rowsum, size_t row_len, void* ws,
+                                           size_t ws_bytes) {
+    icx::clear_error();
+    return icx::dql_two_launch(reinterpret_cast<hipStream_t>(stream), x, n, y, y_scale, y_zp, opt_rowsum,
+                               row_len, ws, ws_bytes, true);
 }

@@ -1796,9 +1796,9 @@ class Runner {
         }
         rc = workspace(icx_dql_workspace_size(cnt));
         if (rc) return rc;
-        return icx_dynamic_quantize_linear(s_, x, cnt, static_cast<uint8_t*>(Y->ptr), static_cast<float*>(S->ptr),
-                                           static_cast<uint8_t*>(Z->ptr), R ? static_cast<int32_t*>(R->ptr) : nullptr,
-                                           row_len, g_.ws, g_.ws_bytes);
+        return icx::dql_two_launch(s_, x, cnt, static_cast<uint8_t*>(Y->ptr), static_cast<float*>(S->ptr),
+                                   static_cast<uint8_t*>(Z->ptr), R ? static_cast<int32_t*>(R->ptr) : nullptr,
+                                   row_len, g_.ws, g_.ws_bytes, false);
     }
 
     int run_chain(const std::string& in_name, const std::vector<Step>& steps, const std::string& out_name,

@@ -75,6 +75,11 @@ int dql_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_s
 // number of polls after which a wait gives up, every wait expecting a tag nobody publishes.
 int qout_fault_spin();
 
+// icx_dynamic_quantize_linear's two launches; `nt_y` writes a flat (no row sums) y with
+// non-temporal stores (the C entry point); the graph executor passes false.
+int dql_two_launch(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                   int32_t* opt_rowsum, size_t row_len, void* ws, size_t ws_bytes, bool nt_y);
+
 // DynamicQuantizeLinear of x from the n_part partials its producer left: one launch (the
 // quantize pass of icx_dynamic_quantize_linear, which folds them).
 int dql_from_parts(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
