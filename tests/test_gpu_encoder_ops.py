@@ -107,6 +107,26 @@ def test_qlinear_with_gelu_epilogue():
     assert rel_err(y, want) < 1e-6
 
 
+def test_gelu_epilogue_straight_line_matches_the_chain_loop():
+    """The 8-op dequant + erf-GELU epilogue runs as straight-line code; the same ops through
+    the per-op loop (the dequant and bias in the GEMM store, then the 6-op GELU chain as a
+    separate launch) give the same bits."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((512, 768)).astype(np.float32)
+    w = rng.integers(-127, 128, (768, 3072)).astype(np.int8)
+    w_scale, bias = np.float32(0.01), (0.02 * rng.standard_normal(3072)).astype(np.float32)
+    xq, xs, xzp, rs = ops.gpu_dynamic_quantize_linear(dev(x), rowsum_row_len=768)
+    pw = ops.PackedWeight(dev(w))
+    c0, c1, c2 = (dev(np.array(v, np.float32)) for v in (1.4142135, 1.0, 0.5))
+    lin = [("Mul", (xs, dev(np.array(w_scale))), False), ("Add", dev(bias), False)]
+    gelu = [("Save", None, False), ("Div", c0, False), ("Erf", None, False), ("Add", c1, False),
+            ("MulSaved", None, False), ("Mul", c2, False)]
+    y8 = host(ops.gpu_qlinear(xq, pw, xzp, None, epilogue=lin + gelu, a_rowsum=rs))
+    t = ops.gpu_qlinear(xq, pw, xzp, None, epilogue=lin, a_rowsum=rs)
+    y2 = host(ops.gpu_fused_chain(t, gelu))
+    assert np.array_equal(bits(y8), bits(y2))
+
+
 def test_qlinear_with_gelu_epilogue_narrow_tile():
     """The erf-GELU epilogue on the 128x96 tile (4096 x 768 x 768: 256 tiles)."""
     rng = np.random.default_rng(12)
