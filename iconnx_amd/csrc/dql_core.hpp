@@ -126,27 +126,29 @@ __device__ __forceinline__ uint32_t quant1(float x, const DqlParams& p) {
     return (uint32_t)v;
 }
 
-// Four elements at once.  With `fast` (a scale in [1e-30, 1e30]) the f32 quotient q and
-// r = rne(q) decide every element with |q - r| < 0.4999 (the condition of quant1 written
-// without its tie-distance arithmetic: |q - r| <= 0.5 always).  Subnormal x need no
-// separate test here: |q| < 2e-8 then, so r = 0 = rne of the exact quotient.  NaN and inf
-// make q - r NaN, which fails the test and goes to quant1.
+// Four elements at once.  With `fast` (a scale in [1e-30, 1e30]) t = fma(x, fl32(1/s), zp)
+// and r = rne(t) decide every element with |t - r| < 0.4999.  The elements of a DQL lie in
+// [min, max] with max - min = 255 s, so |x/s| <= 255 and |t| < 256: t is within
+// 255·2^-24 (the reciprocal's rounding) + 2^-17 (the fma's) < 2.4e-5 of x/s + zp, so r is
+// rne(x/s) + zp (no tie lies within the margin, so shifting by the integer zp cannot flip a
+// tie's rounding) — the condition of quant1 without its tie-distance arithmetic.  Subnormal
+// x give t = zp.  NaN and inf make t - r NaN, which fails the test and goes to quant1.
 __device__ __forceinline__ uint32_t quant4(float4 v, const DqlParams& p) {
     if (p.fast) {
-        const float q0 = v.x * p.inv32, q1 = v.y * p.inv32, q2 = v.z * p.inv32, q3 = v.w * p.inv32;
-        const float r0 = rintf(q0), r1 = rintf(q1), r2 = rintf(q2), r3 = rintf(q3);
-        const bool ok = fabsf(q0 - r0) < 0.4999f && fabsf(q1 - r1) < 0.4999f &&
-                        fabsf(q2 - r2) < 0.4999f && fabsf(q3 - r3) < 0.4999f;
+        const float zf = (float)p.zp;
+        const float t0 = __builtin_fmaf(v.x, p.inv32, zf), t1 = __builtin_fmaf(v.y, p.inv32, zf);
+        const float t2 = __builtin_fmaf(v.z, p.inv32, zf), t3 = __builtin_fmaf(v.w, p.inv32, zf);
+        const float r0 = rintf(t0), r1 = rintf(t1), r2 = rintf(t2), r3 = rintf(t3);
+        const bool ok = fabsf(t0 - r0) < 0.4999f && fabsf(t1 - r1) < 0.4999f &&
+                        fabsf(t2 - r2) < 0.4999f && fabsf(t3 - r3) < 0.4999f;
         if (ok) {
-            // r + zp is an integer (exact in f32, or huge and then clamped anyway);
-            // v_cvt_pk_u8_f32 clamps it to [0, 255] and writes it into its byte of the word
-            // (checked on the MI355X: clamp and round-to-nearest-even, the other bytes kept),
-            // one instruction per element instead of med3, convert, shift and or
-            const float zf = (float)p.zp;
-            uint32_t q = __builtin_amdgcn_cvt_pk_u8_f32(r0 + zf, 0, 0u);
-            q = __builtin_amdgcn_cvt_pk_u8_f32(r1 + zf, 1, q);
-            q = __builtin_amdgcn_cvt_pk_u8_f32(r2 + zf, 2, q);
-            return __builtin_amdgcn_cvt_pk_u8_f32(r3 + zf, 3, q);
+            // v_cvt_pk_u8_f32 clamps the integer r to [0, 255] and writes it into its byte of
+            // the word (checked on the MI355X: clamp and round-to-nearest-even, the other
+            // bytes kept), one instruction per element instead of med3, convert, shift and or
+            uint32_t q = __builtin_amdgcn_cvt_pk_u8_f32(r0, 0, 0u);
+            q = __builtin_amdgcn_cvt_pk_u8_f32(r1, 1, q);
+            q = __builtin_amdgcn_cvt_pk_u8_f32(r2, 2, q);
+            return __builtin_amdgcn_cvt_pk_u8_f32(r3, 3, q);
         }
     }
     return quant1(v.x, p) | (quant1(v.y, p) << 8) | (quant1(v.z, p) << 16) |
