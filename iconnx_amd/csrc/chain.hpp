@@ -198,6 +198,19 @@ __device__ __forceinline__ void run_chain4(uint32_t codes, int n_ops, float4 (&v
             return;
         }
     }
+    // The plain dequant + bias (Mul, Add) of every quantized linear, straight-line for the
+    // same reason.
+    if (n_ops == 2 && (codes & 0x77u) == 0x02u) {
+        const float4 o0 = opnd(0), o1 = opnd(1);
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            v[u].x = __fadd_rn(__fmul_rn(v[u].x, o0.x), o1.x);
+            v[u].y = __fadd_rn(__fmul_rn(v[u].y, o0.y), o1.y);
+            v[u].z = __fadd_rn(__fmul_rn(v[u].z, o0.z), o1.z);
+            v[u].w = __fadd_rn(__fmul_rn(v[u].w, o0.w), o1.w);
+        }
+        return;
+    }
     float4 sv[MODE == 2 ? NV : 1];
 #pragma unroll 1
     for (int k = 0; k < n_ops; ++k) {
