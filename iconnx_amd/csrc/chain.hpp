@@ -198,9 +198,12 @@ __device__ __forceinline__ void run_chain4(uint32_t codes, int n_ops, float4 (&v
             return;
         }
     }
-    // The plain dequant + bias (Mul, Add) of every quantized linear, straight-line for the
-    // same reason.
-    if (n_ops == 2 && (codes & 0x77u) == 0x02u) {
+    // The dequant (Mul) and bias (Add) that head every quantized linear's chain, straight-line
+    // for the same reason; the ops after them, if any, go through the loop.  Binary-only
+    // chains (MODE 0) only: in the GELU kernels the extra code costs registers.
+    int k0 = 0;
+    if (MODE != 0) {
+    } else if (n_ops >= 2 && (codes & 0x77u) == 0x02u) {
         const float4 o0 = opnd(0), o1 = opnd(1);
 #pragma unroll
         for (int u = 0; u < NV; ++u) {
@@ -209,11 +212,22 @@ __device__ __forceinline__ void run_chain4(uint32_t codes, int n_ops, float4 (&v
             v[u].z = __fadd_rn(__fmul_rn(v[u].z, o0.z), o1.z);
             v[u].w = __fadd_rn(__fmul_rn(v[u].w, o0.w), o1.w);
         }
+        if (n_ops == 2) return;
+        k0 = 2;
+    } else if (n_ops == 1 && (codes & 7u) == ICX_OP_MUL) {  // the dequant alone
+        const float4 o0 = opnd(0);
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            v[u].x = __fmul_rn(v[u].x, o0.x);
+            v[u].y = __fmul_rn(v[u].y, o0.y);
+            v[u].z = __fmul_rn(v[u].z, o0.z);
+            v[u].w = __fmul_rn(v[u].w, o0.w);
+        }
         return;
     }
     float4 sv[MODE == 2 ? NV : 1];
 #pragma unroll 1
-    for (int k = 0; k < n_ops; ++k) {
+    for (int k = k0; k < n_ops; ++k) {
         const uint32_t code = (codes >> (4 * k)) & 15u;
         if constexpr (MODE == 2) {
             if ((code & 7u) > ICX_OP_DIV) {
