@@ -302,7 +302,7 @@ int icx::dql_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float
     if (per_cu[d] < 0 || G > (size_t)per_cu[d] * icx::num_cus())
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: %zu blocks exceed the %d resident ones", G,
                  per_cu[d] * icx::num_cus());
-    int spin = 1 << 20;
+    int spin = 1 << 22;
     unsigned poison = 0;
     if (const int f = icx::qout_fault_spin()) {  // test hook
         spin = f;

@@ -1757,7 +1757,7 @@ int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp
     g.q_scale = y_scale;
     g.q_zp = y_zp;
     g.q_sync = sync;
-    g.q_spin = 1 << 20;
+    g.q_spin = 1 << 22;
     g.q_poison = 0;
     if (const int f = icx::qout_fault_spin()) {  // test hook
         g.q_spin = f;

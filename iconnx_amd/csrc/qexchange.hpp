@@ -73,7 +73,7 @@ __device__ __forceinline__ dql::DqlParams gather(unsigned* sync, unsigned tag, i
                 late = 1;
                 break;
             }
-            __builtin_amdgcn_s_sleep(8);
+            __builtin_amdgcn_s_sleep(2);
         }
         dql::acc_minmax(__uint_as_float((uint32_t)lo), mn, mx);
         dql::acc_minmax(__uint_as_float((uint32_t)hi), mn, mx);
