@@ -72,6 +72,9 @@ SIGNATURES = {
     "icx_gather": ([P, P, S, S, S, S, P, I, S, P], I),
     "icx_layer_norm_f32": ([P, P, P, S, S, P, P, ctypes.c_float, P], I),
     "icx_softmax_f32": ([P, P, S, S, P], I),
+    "icx_reduce_mean_f32": ([P, P, S, S, S, I, P], I),
+    "icx_pow_f32": ([P, P, S, S, P, I, P], I),
+    "icx_sqrt_f32": ([P, P, S, P], I),
     "icx_transpose": ([P, P, S, I, P, P, P], I),
     "icx_matmul_f32": ([P, P, P, S, I, S, S, S, P], I),
     "icx_attention_f32": ([P, P, P, P, S, S, S, S, S, S, S, S, ctypes.c_float, I, I, P], I),

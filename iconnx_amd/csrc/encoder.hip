@@ -13,6 +13,7 @@
 //       activations, with fp32 MFMA (v_mfma_f32_16x16x4f32): two blocks per (batch, head),
 //       each of four waves of 16 queries; S^T = K Q^T leaves every lane one query's scores in
 //       the A-operand layout of the P V product, so the softmax stays in registers.
+#include "chain.hpp"
 #include "icx_common.hpp"
 #include "internal.hpp"
 #include <cmath>
@@ -76,7 +77,7 @@ layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ res, si
     float* yr = y + row * cols;
     for (size_t i = j; i < cols; i += 8) {
         const float c = __fsub_rn(ln_in(xr, rr, i), mean);
-        yr[i] = __fadd_rn(__fmul_rn(__fdiv_rn(c, sd), scale[i]), bias[i]);
+        yr[i] = __fadd_rn(__fmul_rn(__fdiv_rn(c, sd), scale ? scale[i] : 1.0f), bias ? bias[i] : -0.0f);
     }
 }
 
@@ -168,7 +169,8 @@ layer_norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ re
             const int r = q / C4, c4 = q % C4;
             const float mean = stat[0][r], sd = stat[1][r];
             const float4 a = *reinterpret_cast<const float4*>(&tile[r * STRIDE + c4 * 4]);
-            const float4 sc = s4[c4], bi = b4[c4];
+            const float4 sc = s4 ? s4[c4] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            const float4 bi = b4 ? b4[c4] : make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
             float4 o;
             o.x = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(a.x, mean), sd), sc.x), bi.x);
             o.y = __fadd_rn(__fmul_rn(__fdiv_rn(__fsub_rn(a.y, mean), sd), sc.y), bi.y);
@@ -214,6 +216,64 @@ softmax_kernel(const float* __restrict__ x, size_t rows, size_t cols, float* __r
     for (size_t i = j; i < n8; i += 8) yr[i] = __fdiv_rn(yr[i], acc);
     if (j == 0)
         for (size_t i = n8; i < cols; ++i) yr[i] = __fdiv_rn(yr[i], acc);
+}
+
+// ---- ReduceMean, Pow, Sqrt: the ops of a LayerNorm exported node by node ----------------
+// ReduceMean over the last axis (or over every element, as one row): ndarray 0.16's
+// mean_axis over a contiguous lane — unrolled_fold's eight partial sums, combined as
+// combine8 does, then the < 8 leftover elements in order — divided by the lane length
+// converted to f32 (src/operators/reduce_mean.rs:64-72).  Eight lanes per row, 32 rows per
+// block.
+__global__ void __launch_bounds__(kThreads)
+reduce_mean_last_kernel(const float* __restrict__ x, size_t rows, size_t cols, float* __restrict__ y) {
+    const int j = threadIdx.x & 7;
+    const size_t row = (size_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    if (row >= rows) return;  // a whole 8-lane group leaves together
+    const float* xr = x + row * cols;
+    const size_t n8 = cols / 8 * 8;
+    float p = 0.0f;
+    for (size_t i = j; i < n8; i += 8) p = __fadd_rn(p, xr[i]);
+    float acc = combine8(p);
+    if (j) return;
+    for (size_t i = n8; i < cols; ++i) acc = __fadd_rn(acc, xr[i]);
+    y[row] = __fdiv_rn(acc, (float)cols);
+}
+
+// ReduceMean over an axis that is not the last: ndarray's sum_axis adds the sub-views along
+// the axis one after the other into a zero array (res = 0 + x[.., 0, ..] + x[.., 1, ..] + ...),
+// then mean_axis divides by the axis length.  One thread per output of [outer, inner].
+__global__ void __launch_bounds__(kThreads)
+reduce_mean_seq_kernel(const float* __restrict__ x, size_t outer, size_t axis_len, size_t inner,
+                       float* __restrict__ y) {
+    const size_t n = outer * inner, stride = (size_t)gridDim.x * kThreads;
+    const float fa = (float)axis_len;
+    for (size_t o = (size_t)blockIdx.x * kThreads + threadIdx.x; o < n; o += stride) {
+        const float* p = x + (o / inner) * axis_len * inner + o % inner;
+        float acc = 0.0f;
+        for (size_t a = 0; a < axis_len; ++a) acc = __fadd_rn(acc, p[a * inner]);
+        y[o] = __fdiv_rn(acc, fa);
+    }
+}
+
+// Pow (src/operators/pow.rs:18-45): y = x ^ e, the exponent broadcast over x [rows, cols].
+// An exponent of exactly 2 gives the correctly rounded square x * x — LayerNormalization's
+// c * c — and any other exponent the device powf.
+__global__ void __launch_bounds__(kThreads)
+pow_kernel(const float* __restrict__ x, size_t rows, size_t cols, const float* __restrict__ e,
+           int e_kind, float* __restrict__ y) {
+    const size_t n = rows * cols, stride = (size_t)gridDim.x * kThreads;
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        const float v = x[i];
+        const float p = icx::load_bcast(e, e_kind, i / cols, i % cols, cols);
+        y[i] = p == 2.0f ? __fmul_rn(v, v) : powf(v, p);
+    }
+}
+
+// Sqrt (src/operators/sqrt.rs:18-30): the correctly rounded square root (f32::sqrt).
+__global__ void __launch_bounds__(kThreads)
+sqrt_kernel(const float* __restrict__ x, size_t n, float* __restrict__ y) {
+    const size_t stride = (size_t)gridDim.x * kThreads;
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) y[i] = sqrtf(x[i]);
 }
 
 // ---- transpose ---------------------------------------------------------------------------
@@ -525,7 +585,7 @@ int icx::layer_norm_f32(hipStream_t s, const float* x, const float* residual, si
                         const float* scale, const float* bias, float eps, float* y, float2* part,
                         int* n_part) {
     if (n_part) *n_part = 0;
-    if (!x || !scale || !bias || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "LayerNormalization: null pointer argument");
+    if (!x || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "LayerNormalization: null pointer argument");
     if (cols == 0 && rows) ICX_FAIL(ICX_ERR_SHAPE, "LayerNormalization: empty normalized axis");
     if (rows == 0) return ICX_OK;
     // partials only from the LDS-staged kernel, one per block: blocks of 4 rows while their
@@ -567,6 +627,52 @@ extern "C" int icx_softmax_f32(icx_stream_t stream, const float* x, size_t rows,
     hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)icx::cdiv(rows, 32)), dim3(kThreads), 0,
                        reinterpret_cast<hipStream_t>(stream), x, rows, cols, y);
     ICX_LAUNCH_CHECK("softmax_kernel");
+    return ICX_OK;
+}
+
+extern "C" int icx_reduce_mean_f32(icx_stream_t stream, const float* x, size_t outer, size_t axis_len,
+                                   size_t inner, int sequential, float* y) {
+    icx::clear_error();
+    if (!x || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "ReduceMean: null pointer argument");
+    if (x == y) ICX_FAIL(ICX_ERR_INVALID_ARG, "ReduceMean: input and output must not alias");
+    if (outer == 0 || inner == 0) return ICX_OK;
+    if (axis_len == 0) ICX_FAIL(ICX_ERR_SHAPE, "ReduceMean: the reduced axis is empty (the mean is undefined)");
+    if (!sequential && inner != 1)
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "ReduceMean: the unrolled order needs a contiguous axis (inner == 1)");
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (!sequential) {
+        if (icx::cdiv(outer, 32) > 0x7fffffffu) ICX_FAIL(ICX_ERR_SHAPE, "ReduceMean: too many rows");
+        hipLaunchKernelGGL(reduce_mean_last_kernel, dim3((unsigned)icx::cdiv(outer, 32)), dim3(kThreads), 0, s,
+                           x, outer, axis_len, y);
+        ICX_LAUNCH_CHECK("reduce_mean_last_kernel");
+    } else {
+        hipLaunchKernelGGL(reduce_mean_seq_kernel, dim3(grid_for(outer * inner, kThreads, 65536)), dim3(kThreads),
+                           0, s, x, outer, axis_len, inner, y);
+        ICX_LAUNCH_CHECK("reduce_mean_seq_kernel");
+    }
+    return ICX_OK;
+}
+
+extern "C" int icx_pow_f32(icx_stream_t stream, const float* x, size_t rows, size_t cols, const float* e,
+                           int e_kind, float* y) {
+    icx::clear_error();
+    if (!x || !e || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "Pow: null pointer argument");
+    if (e_kind < ICX_BCAST_SCALAR || e_kind > ICX_BCAST_FULL)
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "Pow: unknown exponent broadcast kind %d", e_kind);
+    if (rows == 0 || cols == 0) return ICX_OK;
+    hipLaunchKernelGGL(pow_kernel, dim3(grid_for(rows * cols, kThreads, 65536)), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), x, rows, cols, e, e_kind, y);
+    ICX_LAUNCH_CHECK("pow_kernel");
+    return ICX_OK;
+}
+
+extern "C" int icx_sqrt_f32(icx_stream_t stream, const float* x, size_t n, float* y) {
+    icx::clear_error();
+    if (!x || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "Sqrt: null pointer argument");
+    if (n == 0) return ICX_OK;
+    hipLaunchKernelGGL(sqrt_kernel, dim3(grid_for(n, kThreads, 65536)), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), x, n, y);
+    ICX_LAUNCH_CHECK("sqrt_kernel");
     return ICX_OK;
 }
 

@@ -11,6 +11,8 @@
 //                               Reshape of a BERT self-attention -> one fused kernel
 //              QuantizedLinear  MatMulInteger -> Cast -> Mul -> [Add] -> [chain] [-> GELU]
 //              AddLayerNorm     LayerNormalization(Add(a, b))
+//              DecomposedLayerNorm  [Add(a, b) ->] ReduceMean -> Sub -> Pow(2) -> ReduceMean
+//                               -> Add(eps) -> Sqrt -> Div [-> Mul(gamma)] [-> Add(beta)]
 //              MulAdd / AddMul / SubMul / DivMul / ElementwiseChain / Gelu
 //            weight zero-point folding; Reshape outputs alias their input; last use of
 //            every tensor
@@ -119,7 +121,8 @@ enum class Pattern {
     ElementwiseChain,
     Gelu,
     Attention,
-    AddLayerNorm
+    AddLayerNorm,
+    DecomposedLayerNorm
 };
 
 const char* kind_name(Kind k) {
@@ -137,6 +140,7 @@ const char* pattern_name(Pattern p) {
         case Pattern::Gelu: return "Gelu";
         case Pattern::Attention: return "Attention";
         case Pattern::AddLayerNorm: return "AddLayerNorm";
+        case Pattern::DecomposedLayerNorm: return "DecomposedLayerNorm";
         default: return "-";
     }
 }
@@ -158,7 +162,7 @@ struct PlannedOp {
     float scale = 1.0f;
     bool scale_div = false, scale_q = false;
     std::string q_shape, k_shape, v_shape, o_shape;  // Reshape shape initializers
-    // AddLayerNorm: LN(x + res)
+    // AddLayerNorm, DecomposedLayerNorm: LN(x + res); the decomposed form may lack scale / bias
     std::string ln_x, ln_res, ln_scale, ln_bias;
     float eps = 1e-5f;
     // QuantizedLinear sibling group (heads over one activation, e.g. Q / K / V): the first
@@ -374,7 +378,7 @@ class Planner {
                 switch (pass) {
                     case 0: hit = match_attention(i, head, mem); break;
                     case 1: hit = match_qlinear(i, head, mem); break;
-                    case 2: hit = match_add_layer_norm(i, head, mem); break;
+                    case 2: hit = match_add_layer_norm(i, head, mem) || match_layer_norm_chain(i, head, mem); break;
                     default: hit = match_chain(i, head, mem); break;
                 }
                 if (!hit) continue;
@@ -418,7 +422,8 @@ class Planner {
             std::set<std::string> heads_out;
             for (auto& op : g_.plan)
                 if (op.kind == Kind::FusedHead && op.group.empty() &&
-                    (op.pattern == Pattern::AddLayerNorm || op.pattern == Pattern::Attention ||
+                    (op.pattern == Pattern::AddLayerNorm || op.pattern == Pattern::DecomposedLayerNorm ||
+                     op.pattern == Pattern::Attention ||
                      op.pattern == Pattern::QuantizedLinear))
                     heads_out.insert(op.out);
             for (auto& op : g_.plan)
@@ -857,7 +862,8 @@ class Planner {
         const std::string& op = n.op;
         if (op == "DynamicQuantizeLinear") return t == n.out[0] ? rank_of(n.in[0], depth + 1) : 0;
         if (op == "MatMulInteger" || op == "Cast" || op == "Erf" || op == "Softmax" || op == "LayerNormalization" ||
-            op == "DequantizeLinear" || op == "Transpose")
+            op == "DequantizeLinear" || op == "Transpose" || op == "Sqrt" || op == "Pow" ||
+            (op == "ReduceMean" && n.attr_or("keepdims", 1) != 0 && (n.in.size() > 1 || n.iattrs.count("axes"))))
             return n.in.empty() ? -1 : rank_of(n.in[0], depth + 1);
         if (op == "Reshape" && n.in.size() == 2) {
             auto sh = g_.inits.find(n.in[1]);
@@ -942,6 +948,122 @@ class Planner {
         head.eps = (float)ln.fattr_or("epsilon", 1e-5);
         head.out = ln.out[0];
         mem = {ai};
+        return true;
+    }
+
+    // ReduceMean over the last axis with keepdims: axes [-1] or [rank - 1] from its Int64
+    // initializer input (opset 18) or its `axes` attribute (earlier opsets).
+    bool last_axis_mean(int i) const {
+        const Node& n = nodes_[i];
+        if (n.op != "ReduceMean" || n.in.empty() || n.out.size() != 1 || n.attr_or("keepdims", 1) == 0) return false;
+        int64_t ax;
+        if (n.in.size() > 1 && !n.in[1].empty()) {
+            auto it = g_.inits.find(n.in[1]);
+            if (it == g_.inits.end() || it->second.dtype != ICX_I64 || numel(it->second.shape) != 1) return false;
+            std::memcpy(&ax, it->second.data.data(), 8);
+        } else {
+            auto it = n.iattrs.find("axes");
+            if (it == n.iattrs.end() || it->second.size() != 1) return false;
+            ax = it->second[0];
+        }
+        if (ax == -1) return true;
+        const int r = rank_of(n.in[0]);
+        return r > 0 && ax == r - 1;
+    }
+    // The static per-column operand of Mul / Add node k over `cur`: an f32 initializer of
+    // shape [.., C] with only ones before C, C >= 2 (checked against the normalised axis at run).
+    bool affine_operand(int k, const std::string& cur, std::string* o) const {
+        const Node& n = nodes_[k];
+        if (n.in.size() != 2 || n.out.size() != 1) return false;
+        const bool left = n.in[0] == cur, right = n.in[1] == cur;
+        if (left == right) return false;
+        const std::string& t = left ? n.in[1] : n.in[0];
+        auto it = g_.inits.find(t);
+        if (it == g_.inits.end() || it->second.dtype != ICX_F32) return false;
+        const auto& sh = it->second.shape;
+        if (sh.empty() || sh.back() < 2) return false;
+        for (size_t d = 0; d + 1 < sh.size(); ++d)
+            if (sh[d] != 1) return false;
+        *o = t;
+        return true;
+    }
+
+    // LayerNorm as an export that decomposes it writes it (PyTorch below opset 17; the
+    // reference's DistilBERT-INT8, whose ops include ReduceMean, Pow and Sqrt):
+    //     mean = ReduceMean(x); c = Sub(x, mean); v = ReduceMean(Pow(c, 2));
+    //     y = Div(c, Sqrt(Add(v, eps))) [-> Mul(., gamma)] [-> Add(., beta)]
+    // with both means over the last axis (keepdims), optionally of x = Add(a, b) read by the
+    // two only.  Node by node this is exactly the arithmetic of the LayerNormalization kernel,
+    // in its order: the means are ndarray's unrolled sums divided by the length
+    // (src/operators/reduce_mean.rs:64-72), the square is c * c, then one rounding each for
+    // the Add, Sqrt, Div, Mul and Add (src/operators/{sub,pow,add,sqrt,div,mul}.rs) — so the
+    // chain runs as one launch of that kernel (icx_layer_norm_f32; no Mul / Add tail: NULL
+    // scale / bias).  The reference CPU squares with powf(c, 2), which differs from c * c in
+    // the last bit for ~0.07 % of c; the reference GPU fuses only the Add -> Sqrt -> Div tail
+    // (DivRsqrt, src/cuda/kernels/fused/mod.rs:131-173).
+    bool match_layer_norm_chain(int mi, PlannedOp& head, std::vector<int>& mem) {
+        if (!last_axis_mean(mi)) return false;
+        const Node& m1 = nodes_[mi];
+        const std::string x = m1.in[0], mean = m1.out[0];
+        const int si = sole_consumer(mean);
+        if (!is_op(si, "Sub") || nodes_[si].in.size() != 2 || nodes_[si].in[0] != x || nodes_[si].in[1] != mean ||
+            nodes_[si].out.size() != 1)
+            return false;
+        const std::string c = nodes_[si].out[0];
+        auto cs = gi_.consumers.find(c);
+        if (outs_.count(c) || cs == gi_.consumers.end() || cs->second.size() != 2) return false;
+        int pi = -1, di = -1;
+        for (int k : cs->second) {
+            if (is_op(k, "Pow") && nodes_[k].in.size() == 2 && nodes_[k].in[0] == c && nodes_[k].out.size() == 1) pi = k;
+            if (is_op(k, "Div") && nodes_[k].in.size() == 2 && nodes_[k].in[0] == c && nodes_[k].out.size() == 1) di = k;
+        }
+        float ex;
+        if (pi < 0 || di < 0 || !static_scalar(nodes_[pi].in[1], &ex) || ex != 2.0f) return false;
+        const std::string sq = nodes_[pi].out[0];
+        const int m2 = sole_consumer(sq);
+        if (m2 < 0 || claimed_.count(m2) || !last_axis_mean(m2) || nodes_[m2].in[0] != sq) return false;
+        const std::string var = nodes_[m2].out[0];
+        const int ai = sole_consumer(var);
+        if (!is_op(ai, "Add") || nodes_[ai].in.size() != 2 || nodes_[ai].out.size() != 1) return false;
+        const Node& an = nodes_[ai];
+        if ((an.in[0] == var) == (an.in[1] == var)) return false;
+        float eps;
+        if (!static_scalar(an.in[0] == var ? an.in[1] : an.in[0], &eps)) return false;
+        const int qi = sole_consumer(an.out[0]);
+        if (!is_op(qi, "Sqrt") || nodes_[qi].in.size() != 1 || nodes_[qi].out.size() != 1) return false;
+        if (sole_consumer(nodes_[qi].out[0]) != di || nodes_[di].in[1] != nodes_[qi].out[0]) return false;
+        mem = {si, pi, m2, ai, qi, di};
+        std::string cur = nodes_[di].out[0], o;
+        head.ln_scale.clear();
+        head.ln_bias.clear();
+        int k = sole_consumer(cur);
+        if (is_op(k, "Mul") && affine_operand(k, cur, &o)) {
+            head.ln_scale = o;
+            mem.push_back(k);
+            cur = nodes_[k].out[0];
+            k = sole_consumer(cur);
+        }
+        if (is_op(k, "Add") && affine_operand(k, cur, &o)) {
+            head.ln_bias = o;
+            mem.push_back(k);
+            cur = nodes_[k].out[0];
+        }
+        // a residual Add read only by the two nodes that read x
+        head.ln_x = x;
+        head.ln_res.clear();
+        const int xi = producer(x);
+        auto xc = gi_.consumers.find(x);
+        if (is_op(xi, "Add") && nodes_[xi].in.size() == 2 && nodes_[xi].out.size() == 1 && !outs_.count(x) &&
+            xc != gi_.consumers.end() && xc->second.size() == 2 && !static_f32(nodes_[xi].in[0]) &&
+            !static_f32(nodes_[xi].in[1])) {
+            head.ln_x = nodes_[xi].in[0];
+            head.ln_res = nodes_[xi].in[1];
+            mem.push_back(xi);
+        }
+        head.kind = Kind::FusedHead;
+        head.pattern = Pattern::DecomposedLayerNorm;
+        head.eps = eps;
+        head.out = cur;
         return true;
     }
 
@@ -1137,8 +1259,9 @@ class Runner {
                 case Pattern::QuantizedLinear: return run_qlinear(op);
                 case Pattern::Attention: return run_attention(op);
                 case Pattern::AddLayerNorm:
+                case Pattern::DecomposedLayerNorm:
                     return run_layer_norm(op.ln_x, op.ln_res, op.ln_scale, op.ln_bias, op.eps, op.out,
-                                          "AddLayerNorm");
+                                          pattern_name(op.pattern));
                 default: return run_chain(op.chain_in, op.steps, op.out, pattern_name(op.pattern));
             }
         }
@@ -1195,6 +1318,9 @@ class Runner {
         if (t == "Reshape") return run_reshape(n);
         if (t == "MatMul") return run_matmul_f32(n);
         if (t == "Gather") return run_gather(n);
+        if (t == "ReduceMean") return run_reduce_mean(n);
+        if (t == "Pow") return run_pow(n);
+        if (t == "Sqrt") return run_sqrt(n);
         if (op_code(t) >= 0) return run_binary(n);
         set_error("op '%s' is not on the quantized-linear path", t.c_str());
         return ICX_ERR_UNSUPPORTED;
@@ -1524,11 +1650,11 @@ class Runner {
 
     int run_layer_norm(const std::string& xn, const std::string& resn, const std::string& sn, const std::string& bn,
                        float eps, const std::string& out, const char* who) {
-        const DevTensor *X, *R = nullptr, *S, *B;
+        const DevTensor *X, *R = nullptr, *S = nullptr, *B = nullptr;  // no scale / bias: x 1, + (-0)
         int rc = need_f32(xn, &X, who);
         if (!rc && !resn.empty()) rc = need_f32(resn, &R, who);
-        if (!rc) rc = need_f32(sn, &S, who);
-        if (!rc) rc = need_f32(bn, &B, who);
+        if (!rc && !sn.empty()) rc = need_f32(sn, &S, who);
+        if (!rc && !bn.empty()) rc = need_f32(bn, &B, who);
         if (rc) return rc;
         if (R && R->shape != X->shape) {
             // the Add broadcasts: materialise it, then normalise
@@ -1549,14 +1675,15 @@ class Runner {
             return ICX_ERR_SHAPE;
         }
         const int64_t cols = X->shape.back();
-        if (numel(S->shape) != cols || numel(B->shape) != cols) {
+        if ((S && numel(S->shape) != cols) || (B && numel(B->shape) != cols)) {
             set_error("%s: scale %s / bias %s do not match the normalised axis (%lld)", who,
-                      shape_str(S->shape).c_str(), shape_str(B->shape).c_str(), (long long)cols);
+                      S ? shape_str(S->shape).c_str() : "-", B ? shape_str(B->shape).c_str() : "-", (long long)cols);
             return ICX_ERR_SHAPE;
         }
         const std::vector<int64_t> shape = X->shape;
         const float *x = static_cast<const float*>(X->ptr), *r = R ? static_cast<const float*>(R->ptr) : nullptr,
-                    *sc = static_cast<const float*>(S->ptr), *bi = static_cast<const float*>(B->ptr);
+                    *sc = S ? static_cast<const float*>(S->ptr) : nullptr,
+                    *bi = B ? static_cast<const float*>(B->ptr) : nullptr;
         DevTensor* Y;
         rc = alloc(out, ICX_F32, shape, &Y);
         if (rc) return rc;
@@ -1799,6 +1926,140 @@ class Runner {
         return icx::dql_two_launch(s_, x, cnt, static_cast<uint8_t*>(Y->ptr), static_cast<float*>(S->ptr),
                                    static_cast<uint8_t*>(Z->ptr), R ? static_cast<int32_t*>(R->ptr) : nullptr,
                                    row_len, g_.ws, g_.ws_bytes, false);
+    }
+
+    // Values of a small integer tensor known on the host: an Int64 (or, as the reference's
+    // ReduceMean also takes, Float32) initializer, or a graph input bound from host memory.
+    int host_ints(const std::string& name, std::vector<int64_t>* v, const char* who) const {
+        v->clear();
+        const uint8_t* data = nullptr;
+        int dt = -1;
+        int64_t cnt = 0;
+        auto it = g_.inits.find(name);
+        if (it != g_.inits.end()) {
+            data = it->second.data.data();
+            dt = it->second.dtype;
+            cnt = numel(it->second.shape);
+        } else {
+            auto b = g_.bound.find(name);
+            if (b != g_.bound.end() && !b->second.dev) {
+                data = b->second.host.data();
+                dt = b->second.dtype;
+                cnt = numel(b->second.shape);
+            }
+        }
+        if (dt != ICX_I64 && dt != ICX_F32) {
+            set_error("%s: '%s' must be an Int64 (or Float32) initializer or input bound from host memory", who,
+                      name.c_str());
+            return ICX_ERR_UNSUPPORTED;
+        }
+        for (int64_t i = 0; i < cnt; ++i) {
+            if (dt == ICX_I64) {
+                int64_t a;
+                std::memcpy(&a, data + 8 * i, 8);
+                v->push_back(a);
+            } else {
+                float f;
+                std::memcpy(&f, data + 4 * i, 4);
+                v->push_back((int64_t)f);
+            }
+        }
+        return ICX_OK;
+    }
+
+    // ReduceMean (src/operators/reduce_mean.rs:19-105): axes from the second input (opset 18)
+    // or the `axes` attribute (earlier opsets; the reference's CPU forward reads the input
+    // only, its GPU dispatch always reduces the last axis, src/cuda/executor/reduction.rs:
+    // 88-104); none, or an empty list, reduces every element (data.mean()).  keepdims
+    // (default 1) keeps the reduced axis as 1 — for the full reduction every axis, as ONNX
+    // defines it (the reference's CPU forward returns a rank-0 tensor there, same value).  The
+    // reference reduces only axes[0] of a longer list; more than one axis is refused here.
+    int run_reduce_mean(const Node& n) {
+        const DevTensor* X;
+        int rc = need_f32(n.in[0], &X, "ReduceMean");
+        if (rc) return rc;
+        std::vector<int64_t> axes;
+        if (n.in.size() > 1 && !n.in[1].empty()) {
+            rc = host_ints(n.in[1], &axes, "ReduceMean");
+            if (rc) return rc;
+        } else {
+            auto it = n.iattrs.find("axes");
+            if (it != n.iattrs.end()) axes = it->second;
+        }
+        const std::vector<int64_t> shape = X->shape;
+        const int r = (int)shape.size();
+        const bool keep = n.attr_or("keepdims", 1) != 0;
+        size_t outer = 1, len = (size_t)numel(shape), inner = 1;
+        int seq = 0;
+        std::vector<int64_t> oshape;
+        if (axes.empty()) {
+            if (keep) oshape.assign(r, 1);
+        } else {
+            if (axes.size() > 1) {
+                set_error("ReduceMean: %zu axes; one axis is on this path", axes.size());
+                return ICX_ERR_UNSUPPORTED;
+            }
+            const int64_t a = axes[0] < 0 ? axes[0] + r : axes[0];
+            if (a < 0 || a >= r) {
+                set_error("ReduceMean: axis %lld out of range for rank %d", (long long)axes[0], r);
+                return ICX_ERR_SHAPE;
+            }
+            for (int64_t d = 0; d < a; ++d) outer *= (size_t)shape[d];
+            len = (size_t)shape[a];
+            for (int64_t d = a + 1; d < r; ++d) inner *= (size_t)shape[d];
+            seq = a != r - 1;  // ndarray sums the last (least-strided) axis unrolled, others in order
+            oshape = shape;
+            if (keep) oshape[a] = 1;
+            else oshape.erase(oshape.begin() + a);
+        }
+        if (len == 0 && outer * inner) {
+            set_error("ReduceMean: the reduced axis of %s is empty", shape_str(shape).c_str());
+            return ICX_ERR_SHAPE;
+        }
+        const float* x = static_cast<const float*>(X->ptr);
+        DevTensor* Y;
+        rc = alloc(n.out[0], ICX_F32, oshape, &Y);
+        if (rc) return rc;
+        return icx_reduce_mean_f32(s_, x, outer, len, inner, seq, static_cast<float*>(Y->ptr));
+    }
+
+    // Pow (src/operators/pow.rs:18-45): the exponent broadcasts over the base, whose shape the
+    // output keeps (the reference's .broadcast(base.raw_dim()) panics otherwise).
+    int run_pow(const Node& n) {
+        if (n.in.size() != 2 || n.out.size() != 1) {
+            set_error("Pow: expected 2 inputs and 1 output");
+            return ICX_ERR_INVALID_ARG;
+        }
+        const DevTensor *X, *E;
+        int rc = need_f32(n.in[0], &X, "Pow");
+        if (!rc) rc = need_f32(n.in[1], &E, "Pow");
+        if (rc) return rc;
+        const int kind = bcast_kind(E->shape, X->shape);
+        if (kind < 0) {
+            set_error("Pow: exponent %s does not broadcast over the base %s", shape_str(E->shape).c_str(),
+                      shape_str(X->shape).c_str());
+            return ICX_ERR_SHAPE;
+        }
+        const std::vector<int64_t> shape = X->shape;
+        const int64_t cols = shape.empty() ? 1 : shape.back();
+        const int64_t rows = cols ? numel(shape) / cols : 0;
+        const float *x = static_cast<const float*>(X->ptr), *e = static_cast<const float*>(E->ptr);
+        DevTensor* Y;
+        rc = alloc(n.out[0], ICX_F32, shape, &Y);
+        if (rc) return rc;
+        return icx_pow_f32(s_, x, (size_t)rows, (size_t)cols, e, kind, static_cast<float*>(Y->ptr));
+    }
+
+    int run_sqrt(const Node& n) {
+        const DevTensor* X;
+        int rc = need_f32(n.in[0], &X, "Sqrt");
+        if (rc) return rc;
+        const std::vector<int64_t> shape = X->shape;
+        const float* x = static_cast<const float*>(X->ptr);
+        DevTensor* Y;
+        rc = alloc(n.out[0], ICX_F32, shape, &Y);
+        if (rc) return rc;
+        return icx_sqrt_f32(s_, x, (size_t)numel(shape), static_cast<float*>(Y->ptr));
     }
 
     int run_chain(const std::string& in_name, const std::vector<Step>& steps, const std::string& out_name,

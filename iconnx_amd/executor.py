@@ -10,12 +10,14 @@ device tensors across the boundary.
 Differences from the reference that a caller can see:
   * only the ops of the quantized-linear path and the encoder around it dispatch
     (DynamicQuantizeLinear, MatMulInteger, DequantizeLinear, Cast to FLOAT, Mul/Add/Sub/Div,
-    LayerNormalization, Softmax, Erf, Transpose, Reshape, f32 MatMul); any other op raises
-    IconnxError at run naming the node;
+    LayerNormalization, ReduceMean, Pow, Sqrt, Softmax, Erf, Transpose, Reshape, Gather,
+    f32 MatMul); any other op raises IconnxError at run naming the node;
   * ``MatMulInteger -> Cast -> Mul(scale) [-> Add(bias)] [-> chain] [-> erf-GELU]`` runs as
     one fused GEMM (pattern ``QuantizedLinear``), a BERT self-attention subgraph as one
-    kernel (``Attention``), and ``LayerNormalization(Add(a, b))`` as one (``AddLayerNorm``);
-    the reference leaves these unfused;
+    kernel (``Attention``), ``LayerNormalization(Add(a, b))`` as one (``AddLayerNorm``) and
+    the node-by-node LayerNorm ``ReduceMean -> Sub -> Pow -> ReduceMean -> Add -> Sqrt ->
+    Div [-> Mul -> Add]`` as the same kernel (``DecomposedLayerNorm``); the reference leaves
+    these unfused (it fuses only the Add -> Sqrt -> Div tail, ``DivRsqrt``);
   * ``run_device`` returns device tensors without the host round trip.
 """
 import ctypes
@@ -73,6 +75,26 @@ def _hip_memcpy_d2d(dst, src, nbytes, stream):
         raise IconnxError(5, "hipMemcpyAsync of an output failed (hipError %d)" % rc)
 
 
+def constant_value(node):
+    """The static tensor of a promotable ``Constant`` node (one non-empty output), else None:
+    the ``value`` tensor, else ``value_int`` / ``value_ints`` as Int64, ``value_float`` /
+    ``value_floats`` as Float32 (src/attributes.rs:103-133)."""
+    if node.op_type != "Constant" or len(node.outputs) != 1 or not node.outputs[0]:
+        return None
+    a = node.attributes
+    if isinstance(a.get("value"), np.ndarray):
+        return a["value"]
+    if isinstance(a.get("value_int"), (int, np.integer)):
+        return np.array(a["value_int"], np.int64)
+    if isinstance(a.get("value_ints"), list):
+        return np.array(a["value_ints"], np.int64).reshape(-1)
+    if isinstance(a.get("value_float"), (float, np.floating)):
+        return np.array(a["value_float"], np.float32)
+    if isinstance(a.get("value_floats"), list):
+        return np.array(a["value_floats"], np.float32).reshape(-1)
+    return None
+
+
 class GpuGraphExecutor:
     """Build a graph, then ``run`` it on the GPU (one executor per thread, as in the
     reference)."""
@@ -94,13 +116,22 @@ class GpuGraphExecutor:
     @classmethod
     def from_model(cls, model):
         """Seed inputs, initializers and nodes from a parsed model
-        (src/cuda/inference/mod.rs:250-271): node names are synthesised as ``n{i}``."""
+        (src/cuda/inference/mod.rs:250-271): node names are synthesised as ``n{i}``.  A
+        ``Constant`` node with one output and a static value becomes an initializer of that
+        name, as the reference's constant-promotion pass does
+        (src/ir/passes/constant_promotion.rs:1-160, values resolved as
+        src/attributes.rs:103-133): exporters write the exponent and epsilon of a
+        node-by-node LayerNorm that way."""
         exec_ = cls()
         for name, shape in model.input_shapes():
             exec_.add_input(name, shape)
         for name, arr in model.extract_weights().items():
             exec_.add_initializer(name, arr)
         for i, node in enumerate(model.computation_graph()):
+            value = constant_value(node)
+            if value is not None:
+                exec_.add_initializer(node.outputs[0], value)
+                continue
             exec_.add_node("n%d" % i, node.op_type, node.inputs, node.outputs, node.attributes)
         return exec_
 

@@ -184,9 +184,61 @@ def add_layer_norm(ex, x, residual, scale, bias, eps, prefix):
     return p + ".out"
 
 
-def add_encoder_layer(ex, x, params, heads, eps, prefix):
-    """One post-LN transformer layer; returns a dict of the layer's tensor names."""
+def add_layer_norm_decomposed(ex, x, residual, scale, bias, eps, prefix, axes_attr=False,
+                              constants=False):
+    """The LayerNorm an export below opset 17 writes node by node (PyTorch's exporter; the
+    reference's DistilBERT-INT8): [Add(x, residual) ->] ReduceMean -> Sub -> Pow(., 2) ->
+    ReduceMean -> Add(., eps) -> Sqrt -> Div [-> Mul(., gamma)] [-> Add(., beta)].
+    ``axes_attr``: the means' axes as an attribute (opsets before 18) instead of an Int64
+    input; ``constants``: the exponent, epsilon and axes as Constant nodes (for a ModelWriter,
+    whose file ``from_model`` reads back); ``scale`` / ``bias`` None: no Mul / Add.  Returns
+    the output name."""
     p = prefix
+    if residual is not None:
+        ex.add_node(p + ".residual", "Add", [x, residual], [p + ".sum"])
+        x = p + ".sum"
+
+    def const(name, arr):
+        if constants:
+            ex.add_node(name + ".const", "Constant", [], [name], {"value": arr})
+        else:
+            ex.add_initializer(name, arr)
+
+    const(p + ".two", np.array(2.0, np.float32))
+    const(p + ".eps", np.array(eps, np.float32))
+    attrs = {"keepdims": 1}
+    if axes_attr:
+        attrs["axes"] = [-1]
+        mean_in = lambda t: [t]  # noqa: E731
+    else:
+        const(p + ".axes", np.array([-1], np.int64))
+        mean_in = lambda t: [t, p + ".axes"]  # noqa: E731
+    ex.add_node(p + ".mean", "ReduceMean", mean_in(x), [p + ".mu"], attrs)
+    ex.add_node(p + ".sub", "Sub", [x, p + ".mu"], [p + ".c"])
+    ex.add_node(p + ".pow", "Pow", [p + ".c", p + ".two"], [p + ".sq"])
+    ex.add_node(p + ".var", "ReduceMean", mean_in(p + ".sq"), [p + ".v"], attrs)
+    ex.add_node(p + ".add_eps", "Add", [p + ".v", p + ".eps"], [p + ".ve"])
+    ex.add_node(p + ".sqrt", "Sqrt", [p + ".ve"], [p + ".sd"])
+    ex.add_node(p + ".div", "Div", [p + ".c", p + ".sd"], [p + ".n"])
+    y = p + ".n"
+    if scale is not None:
+        ex.add_initializer(p + ".gamma", np.asarray(scale, np.float32))
+        ex.add_node(p + ".mul_gamma", "Mul", [y, p + ".gamma"], [p + ".scaled"])
+        y = p + ".scaled"
+    if bias is not None:
+        ex.add_initializer(p + ".beta", np.asarray(bias, np.float32))
+        ex.add_node(p + ".add_beta", "Add", [y, p + ".beta"], [p + ".out"])
+        y = p + ".out"
+    return y
+
+
+def add_encoder_layer(ex, x, params, heads, eps, prefix, layer_norm="fused", **ln_kw):
+    """One post-LN transformer layer; returns a dict of the layer's tensor names.
+    ``layer_norm``: "fused" (LayerNormalization nodes) or "decomposed" (the node-by-node form
+    of add_layer_norm_decomposed, with ``ln_kw`` passed to it)."""
+    p = prefix
+    norm = add_layer_norm if layer_norm == "fused" else (
+        lambda *a: add_layer_norm_decomposed(ex, *a[1:], **ln_kw))
     hidden = params["q"]["w"].shape[0]
     lin = lambda name, inp, **kw: add_quantized_linear(
         ex, inp, params[name]["w"], params[name]["w_zp"], params[name]["w_scale"],
@@ -195,22 +247,23 @@ def add_encoder_layer(ex, x, params, heads, eps, prefix):
     q, k, v = (lin(n, x, dql=dql) for n in ("q", "k", "v"))
     ctx = add_self_attention(ex, q, k, v, heads, hidden // heads, p + ".attn")
     o = lin("o", ctx)
-    x1 = add_layer_norm(ex, o, x, params["ln1"]["scale"], params["ln1"]["bias"], eps, p + ".ln1")
+    x1 = norm(ex, o, x, params["ln1"]["scale"], params["ln1"]["bias"], eps, p + ".ln1")
     h = lin("ff1", x1, gelu=True)
     f = lin("ff2", h)
-    x2 = add_layer_norm(ex, f, x1, params["ln2"]["scale"], params["ln2"]["bias"], eps, p + ".ln2")
+    x2 = norm(ex, f, x1, params["ln2"]["scale"], params["ln2"]["bias"], eps, p + ".ln2")
     return dict(x=x, xq=dql[0], q=q, k=k, v=v, ctx=ctx, o=o, x1=x1, h=h, f=f, out=x2)
 
 
 def encoder_graph(ex, layers=6, heads=12, hidden=768, ffn=3072, eps=1e-12, x_name="x",
-                  x_shape=None, seed=3000):
-    """The DistilBERT-shaped encoder on executor ``ex``.  Returns (output name, per-layer
-    tensor names, per-layer params)."""
+                  x_shape=None, seed=3000, layer_norm="fused", **ln_kw):
+    """The DistilBERT-shaped encoder on executor ``ex``; ``layer_norm`` = "decomposed" writes
+    every LayerNorm node by node (ReduceMean / Sub / Pow / Sqrt / Div ...) as an export below
+    opset 17 does.  Returns (output name, per-layer tensor names, per-layer params)."""
     ex.add_input(x_name, x_shape if x_shape is not None else [None, None, hidden])
     x, names, params = x_name, [], []
     for l in range(layers):
         prm = encoder_layer_params(l, hidden, ffn, seed)
-        t = add_encoder_layer(ex, x, prm, heads, eps, "L%d" % l)
+        t = add_encoder_layer(ex, x, prm, heads, eps, "L%d" % l, layer_norm, **ln_kw)
         names.append(t)
         params.append(prm)
         x = t["out"]

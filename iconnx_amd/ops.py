@@ -17,16 +17,20 @@ Reference counterparts (ryanoneill/iconnx):
   gpu_mul / gpu_add / gpu_div  src/cuda/kernels/mod.rs (+ broadcast, src/cuda/executor/elementwise.rs:54-200)
   gpu_gather_from_gpu          src/cuda/ops/layout/mod.rs:900-1020 (gather_u8_kernel,
                                src/cuda/ops/quantize_kernels.rs:203-224)
+  gpu_reduce_mean_axis         src/cuda/reduction.rs:623-700 (CPU src/operators/reduce_mean.rs)
+  gpu_pow / gpu_sqrt           src/cuda/kernels/mod.rs:1407 / the "Sqrt" arm of
+                               src/cuda/executor/elementwise.rs:233-250
 """
 import ctypes
 
+import numpy as np
 import torch
 
 from ._lib import (BCAST_COL, BCAST_FULL, BCAST_ROW, BCAST_SCALAR, ICX_F32, ICX_I8, ICX_I32, ICX_I64,
                    ICX_U8, MAX_CHAIN, OP_ADD, OP_DIV, OP_ERF, OP_MUL, OP_MUL_SAVED, OP_SAVE,
                    OP_SUB, Chain, IconnxError, check, lib)
 
-ERR_SHAPE, ERR_DTYPE, ERR_INVALID = 2, 3, 1
+ERR_SHAPE, ERR_DTYPE, ERR_INVALID, ERR_UNSUPPORTED = 2, 3, 1, 6
 _DT = {torch.int8: ICX_I8, torch.uint8: ICX_U8, torch.int32: ICX_I32, torch.float32: ICX_F32}
 _DT_NAME = {torch.int8: "Int8", torch.uint8: "UInt8", torch.int32: "Int32",
             torch.float32: "Float32", torch.int64: "Int64", torch.float16: "Float16"}
@@ -378,11 +382,12 @@ def _f32_cuda(*ts):
 
 
 def gpu_layer_norm(x, scale, bias, eps=1e-5, residual=None):
-    """LayerNormalization over the last axis of x (or of x + residual)."""
+    """LayerNormalization over the last axis of x (or of x + residual).  ``scale`` / ``bias``
+    may be None: no Mul / Add (the node-by-node norm without its affine tail)."""
     _f32_cuda(x, scale, bias, residual)
     x = x.contiguous()
     cols = x.shape[-1]
-    if scale.numel() != cols or bias.numel() != cols:
+    if (scale is not None and scale.numel() != cols) or (bias is not None and bias.numel() != cols):
         raise IconnxError(ERR_SHAPE, "LayerNorm: scale/bias must have %d elements" % cols)
     if residual is not None:
         if residual.shape != x.shape:
@@ -390,8 +395,66 @@ def gpu_layer_norm(x, scale, bias, eps=1e-5, residual=None):
         residual = residual.contiguous()
     y = torch.empty_like(x)
     check(lib().icx_layer_norm_f32(_stream(), _p(x), _p(residual), x.numel() // cols, cols,
-                                   _p(scale.contiguous()), _p(bias.contiguous()),
+                                   _p(None if scale is None else scale.contiguous()),
+                                   _p(None if bias is None else bias.contiguous()),
                                    ctypes.c_float(eps), _p(y)))
+    return y
+
+
+def gpu_reduce_mean(x, axes=None, keepdims=True):
+    """ReduceMean (src/operators/reduce_mean.rs:19-105; the reference GPU's
+    gpu_reduce_mean_axis, src/cuda/reduction.rs:623-700, is the last-axis case): one axis
+    (negative from the end), or None / [] for every element; ndarray's summation order."""
+    _f32_cuda(x)
+    x = x.contiguous()
+    r = x.dim()
+    if not axes:
+        y = torch.empty([1] * r if keepdims else [], dtype=torch.float32, device=x.device)
+        check(lib().icx_reduce_mean_f32(_stream(), _p(x), 1, x.numel(), 1, 0, _p(y)))
+        return y
+    if len(axes) != 1:
+        raise IconnxError(ERR_UNSUPPORTED, "ReduceMean: one axis is on this path")
+    a = axes[0] + r if axes[0] < 0 else axes[0]
+    if not 0 <= a < r:
+        raise IconnxError(ERR_SHAPE, "ReduceMean: axis %d out of range for rank %d" % (axes[0], r))
+    shape = list(x.shape)
+    outer, alen = int(np.prod(shape[:a], dtype=np.int64)), shape[a]
+    inner = int(np.prod(shape[a + 1:], dtype=np.int64))
+    oshape = shape[:a] + ([1] if keepdims else []) + shape[a + 1:]
+    y = torch.empty(oshape, dtype=torch.float32, device=x.device)
+    check(lib().icx_reduce_mean_f32(_stream(), _p(x), outer, alen, inner, int(a != r - 1), _p(y)))
+    return y
+
+
+def gpu_reduce_mean_axis(x):
+    """The reference GPU's last-axis ReduceMean (src/cuda/reduction.rs:623-700): [..., N] ->
+    [...] (a 1-D input gives [1])."""
+    y = gpu_reduce_mean(x, [-1], keepdims=False)
+    return y.reshape(1) if y.dim() == 0 else y
+
+
+def gpu_pow(base, exp):
+    """Pow (src/operators/pow.rs:18-45; GPU gpu_pow, src/cuda/kernels/mod.rs:1407): the
+    exponent broadcast over the base; exponent 2 is the correctly rounded square."""
+    _f32_cuda(base, exp)
+    base = base.contiguous()
+    cols = base.shape[-1] if base.dim() else 1
+    rows = base.numel() // max(cols, 1)
+    kind = _bcast_kind(exp, rows, cols) if base.dim() else BCAST_SCALAR
+    if kind is None or (exp.numel() != 1 and exp.dim() > base.dim()):
+        raise IconnxError(ERR_SHAPE, "Pow: exponent %s does not broadcast over the base %s"
+                          % (list(exp.shape), list(base.shape)))
+    y = torch.empty_like(base)
+    check(lib().icx_pow_f32(_stream(), _p(base), rows, cols, _p(exp.contiguous()), kind, _p(y)))
+    return y
+
+
+def gpu_sqrt(x):
+    """Sqrt (src/operators/sqrt.rs:18-30): correctly rounded."""
+    _f32_cuda(x)
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    check(lib().icx_sqrt_f32(_stream(), _p(x), x.numel(), _p(y)))
     return y
 
 

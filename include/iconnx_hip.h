@@ -224,12 +224,38 @@ int icx_gather(icx_stream_t stream, const void* data, size_t elem_bytes, size_t 
 
 /* LayerNormalization over the last axis (src/operators/layer_normalization.rs:25-80) of
  * x [rows, cols], or of (x + residual) when residual is not NULL (the Add feeding the norm,
- * one f32 rounding).  scale, bias: [cols]. */
+ * one f32 rounding).  scale, bias: [cols], or NULL for none (x * 1 and x + (-0.0), which
+ * change no bit: the node-by-node form ReduceMean -> Sub -> Pow -> ReduceMean -> Add ->
+ * Sqrt -> Div without its Mul / Add tail). */
 int icx_layer_norm_f32(icx_stream_t stream, const float* x, const float* residual, size_t rows,
                        size_t cols, const float* scale, const float* bias, float eps, float* y);
 
 /* Softmax over the last axis (src/operators/softmax.rs:25-40).  x and y must not alias. */
 int icx_softmax_f32(icx_stream_t stream, const float* x, size_t rows, size_t cols, float* y);
+
+/* ReduceMean (src/operators/reduce_mean.rs:19-105; GPU gpu_reduce_mean_axis,
+ * src/cuda/reduction.rs:623-700, dispatched by src/cuda/executor/reduction.rs:88-104) of x
+ * viewed as [outer, axis_len, inner] over its middle axis: y [outer, inner] = sum / axis_len
+ * (the length converted to f32, one division).  The sum follows ndarray 0.16's order:
+ * sequential == 0 — the contiguous last axis (inner must be 1), or every element of x as one
+ * lane (outer = inner = 1) — unrolled_fold's eight partial sums; sequential != 0 — any other
+ * axis — 0 + x[.., 0, ..] + x[.., 1, ..] + ... in order.  axis_len == 0 is ICX_ERR_SHAPE (the
+ * reference's mean_axis returns None and it panics). */
+int icx_reduce_mean_f32(icx_stream_t stream, const float* x, size_t outer, size_t axis_len,
+                        size_t inner, int sequential, float* y);
+
+/* Pow (src/operators/pow.rs:18-45; GPU: the "Pow" arm of src/cuda/executor/elementwise.rs:
+ * 194-230): y [rows, cols] = x ^ e, the exponent broadcast over x as e_kind (ICX_BCAST_*:
+ * scalar, [cols], [rows] or full).  An exponent of exactly 2 gives the correctly rounded
+ * square x * x; any other the device powf.  The reference CPU calls the C library's powf
+ * (glibc 2.35 here), which is not correctly rounded: for exponent 2 it differs from x * x in
+ * the last bit for ~0.07 % of inputs, so Pow matches it within one ulp, not bit for bit. */
+int icx_pow_f32(icx_stream_t stream, const float* x, size_t rows, size_t cols, const float* e,
+                int e_kind, float* y);
+
+/* Sqrt (src/operators/sqrt.rs:18-30; GPU: the "Sqrt" arm of src/cuda/executor/
+ * elementwise.rs:233-250): y = sqrt(x), correctly rounded like f32::sqrt. */
+int icx_sqrt_f32(icx_stream_t stream, const float* x, size_t n, float* y);
 
 /* Transpose (src/operators/transpose.rs:10-40): y = x.permuted_axes(perm), standard layout;
  * rank <= 6; elements of 1 or 4 bytes. */

@@ -14,6 +14,11 @@ conditions under which it panics — raised here as :class:`OracleError`):
 * :func:`add`/:func:`sub`/:func:`mul`/:func:`div` — ``src/operators/{add,mul,div}.rs``
 * :func:`dequantize_linear` — ``src/operators/dequantize_linear.rs:32-214``
 * :func:`layer_norm` — ``src/operators/layer_normalization.rs:25-80`` (last axis)
+* :func:`reduce_mean` — ``src/operators/reduce_mean.rs:19-105``
+* :func:`pow` — ``src/operators/pow.rs:18-45`` (the C library's powf, as Rust's f32::powf)
+* :func:`sqrt` — ``src/operators/sqrt.rs:18-30``
+* :func:`layer_norm_decomposed` — the node-by-node LayerNorm of an export below opset 17
+  (ReduceMean, Sub, Pow, ReduceMean, Add, Sqrt, Div, Mul, Add), composed from the above
 * :func:`softmax` — ``src/operators/softmax.rs:25-40`` (last axis)
 * :func:`erf` — ``src/operators/erf.rs:21-31``
 * :func:`matmul_f32` — ``src/operators/matmul.rs:20-150`` (f64-accumulated; tolerance)
@@ -84,6 +89,12 @@ def _load():
     lib.orc_matmul_f32.restype = None
     lib.orc_transpose.argtypes = [P, S, ctypes.c_int, P, P, P]
     lib.orc_transpose.restype = None
+    lib.orc_reduce_mean.argtypes = [P, S, S, S, ctypes.c_int, P]
+    lib.orc_reduce_mean.restype = None
+    lib.orc_pow_f32.argtypes = [P, P, S, P]
+    lib.orc_pow_f32.restype = None
+    lib.orc_sqrt_f32.argtypes = [P, S, P]
+    lib.orc_sqrt_f32.restype = None
     _lib = lib
     return lib
 
@@ -347,6 +358,85 @@ def layer_norm(x, scale, bias, eps=1e-5, axis=-1):
     y = np.empty_like(x)
     _load().orc_layer_norm(_ptr(x), x.size // max(cols, 1), cols, _ptr(scale), _ptr(bias),
                            ctypes.c_float(eps), _ptr(y))
+    return y
+
+
+def reduce_mean(x, axes=None, keepdims=True):
+    """ReduceMean::forward (src/operators/reduce_mean.rs:19-105).  ``axes`` as the second
+    input gives them (negative ones counted from the end); None or empty reduces every
+    element (data.mean()).  Like the reference, only ``axes[0]`` is reduced.  keepdims keeps
+    the reduced axis as 1; the full reduction returns the reference's rank-0 result (ONNX
+    would keep every axis as 1: same value)."""
+    x = _f32(x)
+    lib = _load()
+    if axes is None or len(axes) == 0:
+        flat = x.reshape(-1)
+        if flat.size == 0:
+            raise OracleError("ReduceMean: mean of an empty tensor")
+        y = np.empty((), np.float32)
+        lib.orc_reduce_mean(_ptr(flat), 1, flat.size, 1, 0, _ptr(y))
+        return y
+    a = int(axes[0])
+    a = a + x.ndim if a < 0 else a
+    if not 0 <= a < x.ndim:
+        raise OracleError("ReduceMean: axis %d out of range for rank %d" % (axes[0], x.ndim))
+    outer = int(np.prod(x.shape[:a], dtype=np.int64))
+    alen = x.shape[a]
+    inner = int(np.prod(x.shape[a + 1:], dtype=np.int64))
+    if alen == 0:
+        raise OracleError("ReduceMean: mean_axis of an empty axis")
+    sequential = 1 if (x.ndim > 1 and a != x.ndim - 1) else 0
+    y = np.empty((outer, inner), np.float32)
+    lib.orc_reduce_mean(_ptr(x), outer, alen, inner, sequential, _ptr(y))
+    shape = list(x.shape)
+    if keepdims:
+        shape[a] = 1
+    else:
+        del shape[a]
+    return y.reshape(shape)
+
+
+def pow(x, e):
+    """Pow::forward (src/operators/pow.rs:18-45): the exponent broadcast to the base's shape
+    (the reference panics when it does not broadcast), powf per element."""
+    x, e = _f32(x), _f32(e)
+    try:
+        eb = np.ascontiguousarray(np.broadcast_to(e, x.shape))
+    except ValueError:
+        raise OracleError("Pow: exponent %s does not broadcast to base %s"
+                          % (list(e.shape), list(x.shape)))
+    y = np.empty_like(x)
+    _load().orc_pow_f32(_ptr(x), _ptr(eb), x.size, _ptr(y))
+    return y
+
+
+def sqrt(x):
+    """Sqrt::forward (src/operators/sqrt.rs:18-30)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    _load().orc_sqrt_f32(_ptr(x), x.size, _ptr(y))
+    return y
+
+
+def layer_norm_decomposed(x, scale, bias, eps, residual=None, square=False):
+    """The LayerNorm an export below opset 17 writes, run node by node as the reference's
+    GraphExecutor runs it (src/graph_executor.rs:356-432): [x = Add(x, residual)];
+    mean = ReduceMean(x, [-1]); c = Sub(x, mean); v = ReduceMean(Pow(c, 2), [-1]);
+    y = Div(c, Sqrt(Add(v, eps))) [; Mul(y, scale)] [; Add(y, bias)] (scale / bias None:
+    absent).  ``square=True`` replaces Pow(c, 2) by Mul(c, c), the correctly rounded square
+    (the LayerNormalization operator's arithmetic)."""
+    x = _f32(x)
+    if residual is not None:
+        x = add(x, residual)
+    mean = reduce_mean(x, [-1])
+    c = sub(x, mean)
+    sq = mul(c, c) if square else pow(c, np.float32(2.0))
+    v = reduce_mean(sq, [-1])
+    y = div(c, sqrt(add(v, np.float32(eps))))
+    if scale is not None:
+        y = mul(y, scale)
+    if bias is not None:
+        y = add(y, bias)
     return y
 
 

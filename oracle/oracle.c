@@ -214,6 +214,36 @@ void orc_softmax_last(const float* x, size_t rows, size_t cols, float* y) {
     }
 }
 
+void orc_reduce_mean(const float* x, size_t outer, size_t axis_len, size_t inner,
+                     int sequential, float* y) {
+    /* reduce_mean.rs:64-72: data.mean() = sum() / n, data.mean_axis(Axis(a)) = sum_axis / n,
+     * n converted by A::from_usize (one rounding above 2^24); ndarray 0.16 sum_axis walks the
+     * min-stride axis lane by lane with unrolled_fold, any other by adding sub-views into a
+     * zero array in axis order. */
+    const float fn = (float)axis_len;
+    for (size_t o = 0; o < outer; ++o)
+        for (size_t i = 0; i < inner; ++i) {
+            float acc;
+            if (!sequential) {
+                acc = orc_sum_unrolled8(x + o * axis_len, axis_len);
+            } else {
+                acc = 0.0f;
+                for (size_t a = 0; a < axis_len; ++a) acc = acc + x[(o * axis_len + a) * inner + i];
+            }
+            y[o * inner + i] = acc / fn;
+        }
+}
+
+void orc_pow_f32(const float* x, const float* e, size_t n, float* y) {
+    /* pow.rs:27-35: b.powf(e) per element of the broadcast exponent */
+    for (size_t i = 0; i < n; ++i) y[i] = powf(x[i], e[i]);
+}
+
+void orc_sqrt_f32(const float* x, size_t n, float* y) {
+    /* sqrt.rs:26-29: x.sqrt() */
+    for (size_t i = 0; i < n; ++i) y[i] = sqrtf(x[i]);
+}
+
 static float erf1(float x) {
     /* erf.rs:21-31: sign * (1 - poly(t) * t * exp(-a*a)), t = 1 / (1 + 0.3275911 a) */
     const float sign = isnan(x) ? x : (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : copysignf(1.0f, x)));

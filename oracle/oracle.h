@@ -88,6 +88,21 @@ void orc_erf(const float* x, size_t n, float* y);
 void orc_matmul_f32(const float* a, const float* b, size_t batch, int b_broadcast, size_t M,
                     size_t K, size_t N, float* c);
 
+/* ReduceMean (src/operators/reduce_mean.rs:19-105) of x viewed as [outer, axis_len, inner]
+ * over its middle axis: y[outer, inner] = sum / (axis_len as f32).  ndarray 0.16's
+ * sum_axis: the least-strided axis (the last one of a standard-layout array, or all of x as
+ * one slice for data.mean()) lane by lane with unrolled_fold (sequential == 0, inner must be
+ * 1); any other axis as res = 0 + x[.., 0, ..] + x[.., 1, ..] + ... (sequential != 0). */
+void orc_reduce_mean(const float* x, size_t outer, size_t axis_len, size_t inner,
+                     int sequential, float* y);
+
+/* Pow (src/operators/pow.rs:18-45): y[i] = powf(x[i], e[i]) — Rust's f32::powf is the C
+ * library's powf (glibc on Linux); e already broadcast to x's shape by the caller. */
+void orc_pow_f32(const float* x, const float* e, size_t n, float* y);
+
+/* Sqrt (src/operators/sqrt.rs:18-30): y = sqrtf(x) (f32::sqrt, correctly rounded). */
+void orc_sqrt_f32(const float* x, size_t n, float* y);
+
 /* Transpose (src/operators/transpose.rs:10-40): y = x.permuted_axes(perm) in standard
  * layout; elem bytes 1, 4 or 8; rank <= 8. */
 void orc_transpose(const void* x, size_t elem, int rank, const size_t* dims, const int* perm,

@@ -465,3 +465,66 @@ def test_dequantize_linear_along_a_non_last_axis_stays_unfused():
     entries, _ = ex.plan()
     assert heads(entries) == [] or all(h.op_type != "MatMulInteger" for h in heads(entries))
     assert by_node(entries)["dq.dequant"].kind == "Regular"
+
+
+# ---- the node-by-node LayerNorm (ReduceMean / Sub / Pow / Sqrt / Div ...) --------------------
+LN_NODES = ("mean", "sub", "pow", "var", "add_eps", "sqrt", "div", "mul_gamma", "add_beta")
+
+
+def _decomposed_ln(residual=True, affine=True, axes_attr=False, outputs=None, exponent=2.0,
+                   hidden=768):
+    ex = GpuGraphExecutor()
+    ex.add_input("a", [None, None, hidden])
+    ex.add_input("b", [None, None, hidden])
+    g = np.ones(hidden, np.float32) if affine else None
+    y = graphs.add_layer_norm_decomposed(ex, "a", "b" if residual else None, g, g, 1e-12, "ln",
+                                         axes_attr=axes_attr)
+    if exponent != 2.0:
+        ex.add_initializer("ln.two", np.array(exponent, np.float32))
+    for o in outputs or [y]:
+        ex.add_output(o)
+    return ex, y
+
+
+@pytest.mark.parametrize("axes_attr", [False, True])
+@pytest.mark.parametrize("residual", [False, True])
+@pytest.mark.parametrize("affine", [False, True])
+def test_decomposed_layer_norm_is_one_head(axes_attr, residual, affine):
+    ex, y = _decomposed_ln(residual, affine, axes_attr)
+    entries, _ = ex.plan()
+    (h,) = heads(entries)
+    assert h.pattern == "DecomposedLayerNorm" and h.op_type == "ReduceMean" and h.out == y
+    kinds = by_node(entries)
+    expect = [n for n in LN_NODES if affine or n not in ("mul_gamma", "add_beta")]
+    for n in expect[1:] + (["residual"] if residual else []):
+        assert kinds["ln." + n].kind == "Skip", n
+    assert len([e for e in entries if e.kind != "Skip"]) == 1
+
+
+def test_decomposed_layer_norm_stops_where_an_intermediate_is_requested():
+    ex, y = _decomposed_ln(outputs=["ln.out", "ln.c"])
+    entries, _ = ex.plan()
+    assert not any(e.pattern == "DecomposedLayerNorm" for e in entries)
+    ops = [e.op_type for e in entries if e.kind != "Skip"]
+    for op in ("ReduceMean", "Pow", "Sqrt"):
+        assert op in ops  # run node by node
+
+
+def test_decomposed_layer_norm_needs_exponent_two():
+    ex, y = _decomposed_ln(exponent=3.0)
+    entries, _ = ex.plan()
+    assert not any(e.pattern == "DecomposedLayerNorm" for e in entries)
+
+
+def test_encoder_with_decomposed_layer_norms_plans_like_the_fused_one():
+    plans = []
+    for ln in ("fused", "decomposed"):
+        ex = GpuGraphExecutor()
+        out, _, _ = graphs.encoder_graph(ex, layers=2, layer_norm=ln)
+        ex.add_output(out)
+        entries, rowsums = ex.plan()
+        plans.append([(e.pattern, e.steps) for e in entries if e.kind != "Skip"])
+    norm = {"AddLayerNorm": "LN", "DecomposedLayerNorm": "LN"}
+    a, b = ([(norm.get(p, p), s) for p, s in pl] for pl in plans)
+    assert a == b
+    assert sum(p == "DecomposedLayerNorm" for p, _ in plans[1]) == 4

@@ -10,6 +10,8 @@
   f64-vs-f32 divergence (reference f64 semantics give 25 where the file says 26).
 * Synthetic configs written as .onnx files and read back execute bit-identically to the
   same graphs built directly.
+* ReduceMean / Pow / Sqrt (the node-by-node LayerNorm's ops): ReduceMean and Sqrt bit-exact
+  against the oracle; Pow within two ulps of the oracle's C-library powf (device powf).
 """
 import glob
 import os
@@ -75,12 +77,23 @@ def oracle_of(op, ins, attrs):
         return oracle.matmul_f32(*v)
     if op == "Gather":
         return oracle.gather(*v, axis=attrs.get("axis", 0))
+    if op == "ReduceMean":
+        y = oracle.reduce_mean(v[0], list(v[1].reshape(-1)), keepdims=attrs.get("keepdims", 1) == 1)
+        if v[1].size == 0:  # the reference's full reduction is rank 0; ONNX keeps every axis as 1
+            y = y.reshape([1] * v[0].ndim if attrs.get("keepdims", 1) == 1 else [])
+        return y
+    if op == "Pow":
+        return oracle.pow(*v)
+    if op == "Sqrt":
+        return oracle.sqrt(v[0])
     return None
 
 
 # (op -> how the GPU result must relate to the file's expected output)
-EXACT_VS_FILE = {"Add", "Sub", "Mul", "Div", "MatMulInteger", "DequantizeLinear", "Transpose", "Gather"}
-TOL_VS_FILE = {"LayerNormalization": 1e-5, "Softmax": 1e-6, "Erf": 5e-7, "MatMul": 1e-6}
+EXACT_VS_FILE = {"Add", "Sub", "Mul", "Div", "MatMulInteger", "DequantizeLinear", "Transpose", "Gather",
+                 "Sqrt"}
+TOL_VS_FILE = {"LayerNormalization": 1e-5, "Softmax": 1e-6, "Erf": 5e-7, "MatMul": 1e-6,
+               "ReduceMean": 2e-7, "Pow": 1e-6}
 
 
 @pytest.mark.parametrize("d", MODELS, ids=[os.path.basename(d) for d in MODELS])
@@ -111,6 +124,10 @@ def test_vendored_onnx_model_executes(d):
         # device exp / erf and fp32 MFMA summation order: close to the oracle
         scale = max(float(np.max(np.abs(ref))), 1e-30)
         assert float(np.max(np.abs(got.astype(np.float64) - ref))) / scale < 1e-6
+    elif op == "Pow":
+        # the device powf against the C library's: within two ulps (exponent 2: the square)
+        d = np.abs(bits(got).astype(np.int64) - bits(ref).astype(np.int64))
+        assert int(d.max()) <= 2, op
     elif got.dtype == np.float32:
         assert np.array_equal(bits(got), bits(ref)), op
     else:
