@@ -32,6 +32,11 @@ class ChainOp(ctypes.Structure):
                 ("p0", ctypes.c_void_p), ("p1", ctypes.c_void_p)]
 
 
+class OpProfile(ctypes.Structure):
+    _fields_ = [("label", ctypes.c_char * 48), ("node", ctypes.c_char * 80),
+                ("gpu_us", ctypes.c_float), ("cpu_us", ctypes.c_float)]
+
+
 class Chain(ctypes.Structure):
     _fields_ = [("n_ops", ctypes.c_int32), ("reserved", ctypes.c_int32),
                 ("ops", ChainOp * MAX_CHAIN)]
@@ -90,6 +95,8 @@ SIGNATURES = {
     "icx_graph_compile": ([P, P], I),
     "icx_graph_set_input": ([P, C, I, I, P, P, I], I),
     "icx_graph_run": ([P, P], I),
+    "icx_graph_run_profiled": ([P, P, ctypes.POINTER(OpProfile), I, ctypes.POINTER(I),
+                                ctypes.POINTER(ctypes.c_float)], I),
     "icx_graph_get_output": ([P, C, ctypes.POINTER(I), ctypes.POINTER(I), P, ctypes.POINTER(P)], I),
     "icx_graph_pool_stats": ([P, P, P, P], I),
     "icx_graph_capture": ([P, P], I),

@@ -257,7 +257,7 @@ constexpr int kExchangeMaxBlocks = 128;  // inputs up to 128 * 1024 (+ 3) elemen
 __global__ void __launch_bounds__(kThreads)
 dql_exchange_kernel(const float* __restrict__ x, size_t n4, int tail, uint8_t* __restrict__ y,
                     float* __restrict__ y_scale, uint8_t* __restrict__ y_zp, unsigned* sync,
-                    unsigned poison, int spin) {
+                    unsigned poison, unsigned long long wait) {
     const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
     const float4 v = i < n4 ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     const bool has_tail = blockIdx.x == gridDim.x - 1 && (int)threadIdx.x < tail;
@@ -271,7 +271,7 @@ dql_exchange_kernel(const float* __restrict__ x, size_t n4, int tail, uint8_t* _
     const unsigned tag = s_tag;
     if (threadIdx.x == 0) icx::qx::publish(sync, tag, mn, mx);
     bool ok;
-    const DqlParams p = icx::qx::gather<kThreads>(sync, tag ^ poison, spin, ok);
+    const DqlParams p = icx::qx::gather<kThreads>(sync, tag ^ poison, wait, ok);
     if (i < n4) reinterpret_cast<uint32_t*>(y)[i] = ok ? quant4(v, p) : 0u;
     if (has_tail) y[n4 * 4 + threadIdx.x] = ok ? (uint8_t)quant1(xt, p) : (uint8_t)0;
     if (threadIdx.x == 0) icx::qx::finish(sync, ok, p, y_scale, y_zp);
@@ -302,14 +302,14 @@ int icx::dql_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float
     if (per_cu[d] < 0 || G > (size_t)per_cu[d] * icx::num_cus())
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: %zu blocks exceed the %d resident ones", G,
                  per_cu[d] * icx::num_cus());
-    int spin = 1 << 22;
+    unsigned long long wait = icx::wall_ticks(icx::kExchangeWaitUs);
     unsigned poison = 0;
     if (const int f = icx::qout_fault_spin()) {  // test hook
-        spin = f;
+        wait = icx::wall_ticks((unsigned)f);
         poison = 0x80000000u;
     }
     hipLaunchKernelGGL(dql_exchange_kernel, dim3((unsigned)G), dim3(kThreads), 0, s, x, n4, (int)(n % 4), y,
-                       y_scale, y_zp, sync, poison, spin);
+                       y_scale, y_zp, sync, poison, wait);
     ICX_LAUNCH_CHECK("dql_exchange_kernel");
     return ICX_OK;
 }

@@ -24,7 +24,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <exception>
 #include <map>
@@ -204,6 +206,8 @@ class Pool {
    public:
     ~Pool() { release_all(); }
     void* get(size_t bytes, size_t* cls_out) {
+        *cls_out = 0;
+        if (bytes > (SIZE_MAX >> 1) + 1) return nullptr;  // no power-of-two class holds it
         size_t c = 256;
         while (c < bytes) c <<= 1;
         *cls_out = c;
@@ -278,12 +282,14 @@ struct icx_graph {
     hipGraph_t hip_graph = nullptr;
     hipGraphExec_t hip_exec = nullptr;
     std::map<std::string, DevTensor> captured_values;
+    std::vector<hipEvent_t> prof_events;  // icx_graph_run_profiled's events, created once
 
     ~icx_graph() {
         if (ran && last_stream) (void)hipStreamSynchronize(last_stream);
         drop_capture();
         clear_run();
         free_weights();
+        for (hipEvent_t e : prof_events) (void)hipEventDestroy(e);
     }
     void drop_capture() {
         if (hip_exec) (void)hipGraphExecDestroy(hip_exec);
@@ -2525,7 +2531,36 @@ extern "C" int icx_graph_set_input(icx_graph* g, const char* name, int dtype, in
     return ICX_OK;
 }
 
-static int icx_graph_run_impl(icx_graph* g, icx_stream_t stream) {
+// Per-op timing of one eager run (icx_graph_run_profiled): the reference's GpuEventTimer
+// (src/cuda/inference/gpu_event_timer.rs:61-117) — an event after the input uploads, then one
+// after each executed op, so op k's GPU time is the interval between events k and k + 1 —
+// and the host time each op's validation and enqueue took (Executor::run_with_profiling,
+// src/cuda/executor/variants.rs:415-515).
+struct RunProfile {
+    std::vector<std::pair<std::string, std::string>> ops;  // (label, node) per executed op
+    std::vector<double> cpu_us;
+};
+
+// The reference's op_label (src/cuda/executor/variants.rs:35-56): a fused head is
+// "Fused_<pattern>", any other op its type.
+static std::string op_label(const PlannedOp& op) {
+    return op.kind == Kind::FusedHead ? std::string("Fused_") + pattern_name(op.pattern) : op.node.op;
+}
+
+static int prof_event(icx_graph* g, size_t k, hipStream_t s) {
+    while (g->prof_events.size() <= k) {
+        // no system-scope fence: an ordinary event's cache write-back and invalidate would
+        // add a few microseconds to every op it brackets; the run ends with a stream
+        // synchronisation before anything is read
+        hipEvent_t e;
+        ICX_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
+        g->prof_events.push_back(e);
+    }
+    ICX_HIP_CHECK(hipEventRecord(g->prof_events[k], s));
+    return ICX_OK;
+}
+
+static int icx_graph_run_impl(icx_graph* g, icx_stream_t stream, RunProfile* prof = nullptr) {
     if (!g) ICX_FAIL(ICX_ERR_INVALID_ARG, "run: null graph");
     int rc = icx_graph_compile_impl(g, stream);
     if (rc) return rc;
@@ -2548,20 +2583,73 @@ static int icx_graph_run_impl(icx_graph* g, icx_stream_t stream) {
     g->last_stream = s;
     g->ran = true;
     Runner r(*g, s);
+    if (prof && (rc = prof_event(g, 0, s))) return rc;
     rc = r.bind_inputs();
     if (rc) return rc;
+    if (prof && (rc = prof_event(g, 1, s))) return rc;
     for (size_t i = 0; i < g->plan.size(); ++i) {
         const PlannedOp& op = g->plan[i];
         if (op.kind == Kind::Skip) continue;
+        const auto t0 = std::chrono::steady_clock::now();
         rc = r.dispatch(op);
         if (rc) {
             const std::string msg = icx_last_error();
             set_error("node '%s' (%s): %s", op.node.name.c_str(), op.node.op.c_str(), msg.c_str());
             return rc;
         }
+        if (prof) {
+            prof->cpu_us.push_back(
+                std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count());
+            prof->ops.emplace_back(op_label(op), op.node.name);
+            if ((rc = prof_event(g, prof->ops.size() + 1, s))) return rc;
+        }
         r.release_dead(i);
     }
     return ICX_OK;
+}
+
+static int icx_graph_run_profiled_impl(icx_graph* g, icx_stream_t stream, icx_op_profile* ops, int capacity,
+                                       int* n_ops, float* upload_us) {
+    if (!g || !n_ops || capacity < 0 || (capacity && !ops))
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "run_profiled: bad arguments");
+    *n_ops = 0;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    ICX_HIP_CHECK(hipStreamIsCapturing(reinterpret_cast<hipStream_t>(stream), &cap));
+    if (cap != hipStreamCaptureStatusNone)
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "run_profiled: the stream is being captured (profile an eager run)");
+    RunProfile prof;
+    int rc = icx_graph_run_impl(g, stream, &prof);
+    if (rc) return rc;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    ICX_HIP_CHECK(hipStreamSynchronize(s));  // one synchronisation for every event (finalize)
+    float ms = 0.0f;
+    if (upload_us) {
+        ICX_HIP_CHECK(hipEventElapsedTime(&ms, g->prof_events[0], g->prof_events[1]));
+        *upload_us = 1000.0f * ms;
+    }
+    const int n = (int)prof.ops.size();
+    *n_ops = n;
+    for (int k = 0; k < n && k < capacity; ++k) {
+        icx_op_profile& o = ops[k];
+        std::memset(&o, 0, sizeof o);
+        std::snprintf(o.label, sizeof o.label, "%s", prof.ops[k].first.c_str());
+        std::snprintf(o.node, sizeof o.node, "%s", prof.ops[k].second.c_str());
+        ICX_HIP_CHECK(hipEventElapsedTime(&ms, g->prof_events[k + 1], g->prof_events[k + 2]));
+        o.gpu_us = 1000.0f * ms;
+        o.cpu_us = (float)prof.cpu_us[k];
+    }
+    return ICX_OK;
+}
+
+extern "C" int icx_graph_run_profiled(icx_graph* g, icx_stream_t stream, icx_op_profile* ops, int capacity,
+                                      int* n_ops, float* upload_us) {
+    icx::clear_error();
+    try {
+        return icx_graph_run_profiled_impl(g, stream, ops, capacity, n_ops, upload_us);
+    } catch (const std::exception& e) {
+        set_error("icx_graph_run_profiled: %s", e.what());
+        return ICX_ERR_INVALID_ARG;
+    }
 }
 
 // Capture: a warm-up run sizes the pool and the workspace, so that a second run reaches no
@@ -2640,6 +2728,8 @@ extern "C" int icx_graph_status(icx_graph* g, icx_stream_t stream) {
     icx::clear_error();
     if (!g) ICX_FAIL(ICX_ERR_INVALID_ARG, "status: null graph");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // the last run may have gone to another stream than the one given here: wait for it too
+    if (g->ran && g->last_stream && g->last_stream != s) ICX_HIP_CHECK(hipStreamSynchronize(g->last_stream));
     if (!g->qsync) {
         ICX_HIP_CHECK(hipStreamSynchronize(s));
         return ICX_OK;

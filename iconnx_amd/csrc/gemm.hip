@@ -77,7 +77,7 @@ struct GemmArgs {
     float* q_scale;
     uint8_t* q_zp;
     unsigned* q_sync;
-    int q_spin;
+    unsigned long long q_wait;  // exchange wait limit, wall-clock ticks
     unsigned q_poison;  // 0; the fault test hook makes every wait expect tag ^ q_poison
 };
 
@@ -642,7 +642,7 @@ gemm_i8_dma_kernel(GemmArgs g) {
 // For a GEMM whose f32 output is read only by a DynamicQuantizeLinear: the chain runs on the
 // accumulators in their MFMA layout (lane = column), every block publishes the (min, max) of
 // its tile, waits for all the others' (every block is resident — the host launches no more
-// than fit — and each wait is bounded by q_spin polls), folds them into the DQL's scale and
+// than fit — and each wait is bounded in time, q_wait wall-clock ticks), folds them into the DQL's scale and
 // zero point exactly as the DQL launch would (dql_core.hpp) and writes its tile as u8
 // through an LDS byte tile with 16-byte row stores.  The f32 output is never written.  No
 // row term: the host requires an int8 weight whose zero point was folded away.
@@ -715,7 +715,7 @@ __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM 
     icx::dql::block_minmax<NT>(mn, mx);
     if (t == 0) icx::qx::publish(g.q_sync, tag, mn, mx);
     bool ok;
-    const icx::dql::DqlParams p = icx::qx::gather<NT>(g.q_sync, tag ^ g.q_poison, g.q_spin, ok);
+    const icx::dql::DqlParams p = icx::qx::gather<NT>(g.q_sync, tag ^ g.q_poison, g.q_wait, ok);
     // quantize into the LDS byte tile [BM][QS]
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
@@ -1757,10 +1757,10 @@ int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp
     g.q_scale = y_scale;
     g.q_zp = y_zp;
     g.q_sync = sync;
-    g.q_spin = 1 << 22;
+    g.q_wait = icx::wall_ticks(icx::kExchangeWaitUs);
     g.q_poison = 0;
     if (const int f = icx::qout_fault_spin()) {  // test hook
-        g.q_spin = f;
+        g.q_wait = icx::wall_ticks((unsigned)f);
         g.q_poison = 0x80000000u;
     }
     if (icx::chain_mode(g.chain) == 2) return launch_qout<CH_COL_EXT>(blocks, s, g);

@@ -72,8 +72,27 @@ int dql_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_s
                  unsigned* sync);
 
 // The fault test hook of the exchange launches (icx_debug_qout_fault): 0 normally, else the
-// number of polls after which a wait gives up, every wait expecting a tag nobody publishes.
+// microseconds after which a wait gives up, every wait expecting a tag nobody publishes.
 int qout_fault_spin();
+
+// How long a block of an exchange launch waits for the other blocks' ranges before it gives
+// up (the launch then reports ICX_ERR_KERNEL through icx_graph_status).  A wait normally
+// ends within microseconds: every block is resident and publishes right after its own work.
+constexpr unsigned kExchangeWaitUs = 20000;
+
+// `us` microseconds in ticks of the current device's wall clock (wall_clock64; the rate is
+// queried once per device, 100 MHz assumed if the query fails).
+inline unsigned long long wall_ticks(unsigned us) {
+    static int khz[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return (unsigned long long)us * 100;
+    if (!khz[dev]) {
+        int r = 0;
+        if (hipDeviceGetAttribute(&r, hipDeviceAttributeWallClockRate, dev) != hipSuccess || r <= 0) r = 100000;
+        khz[dev] = r;
+    }
+    return (unsigned long long)us * (unsigned long long)khz[dev] / 1000ull;
+}
 
 // icx_dynamic_quantize_linear's two launches; `nt_y` writes a flat (no row sums) y with
 // non-temporal stores (the C entry point); the graph executor passes false.

@@ -19,6 +19,7 @@
 // reference's single stream gives by construction.
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <map>
 #include <new>
 #include <unordered_map>
@@ -34,6 +35,10 @@ struct icx_pool {
 };
 
 namespace {
+// The largest size class, 2^63 bytes: a request above it has no power-of-two class (the
+// doubling would wrap to 0), e.g. (size_t)-1 from a bad size computation.
+constexpr size_t kMaxClass = (SIZE_MAX >> 1) + 1;
+
 size_t size_class(size_t bytes) {
     size_t c = 256;
     while (c < bytes) c <<= 1;
@@ -77,6 +82,7 @@ extern "C" int icx_pool_alloc(icx_pool* p, size_t bytes, void** out) {
     icx::clear_error();
     if (!p || !out) ICX_FAIL(ICX_ERR_INVALID_ARG, "pool_alloc: null pool or output");
     *out = nullptr;
+    if (bytes > kMaxClass) ICX_FAIL(ICX_ERR_INVALID_ARG, "pool_alloc: %zu bytes exceeds the largest size class", bytes);
     const size_t c = size_class(bytes);
     auto it = p->free_.find(c);
     if (it != p->free_.end() && !it->second.empty()) {

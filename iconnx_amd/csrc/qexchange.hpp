@@ -14,8 +14,9 @@
 // Every block reads E before it publishes, and the last block past the exchange increments
 // E, so all blocks of a launch agree on it.  Every access is a device-scope atomic (they
 // bypass the per-XCD L2s); no release / acquire fences, whose per-block L2 write-back and
-// invalidate cost more than the exchange.  Waits are bounded: a block whose wait runs out
-// must write its part of y as 0, and the last block past the exchange then writes the scale
+// invalidate cost more than the exchange.  Waits are bounded in time (the constant-rate
+// wall clock, kExchangeWaitUs microseconds from the start of a block's wait): a block whose
+// wait runs out must write its part of y as 0, and the last block past the exchange then writes the scale
 // as NaN, so that every consumer shows the failure, and counts the launch in word 2.
 //
 // All blocks of a launch must be resident together for the waits to end in time.  The host
@@ -56,20 +57,25 @@ __device__ __forceinline__ void publish(unsigned* sync, unsigned tag, float mn, 
 
 // Every thread of a block of NT threads: wait for all gridDim.x blocks' pairs (thread t polls
 // blocks t, t + NT, ...), fold them as the DQL launch does and return its parameters.
-// `ok` is false in every thread if any wait of this block ran out.  `tag` is the value
-// published (read_tag); a test hook passes a tag that no block publishes instead.
+// `ok` is false in every thread if any wait of this block ran out: a thread gives up on the
+// slots still untagged once `limit` ticks of the wall clock (wall_clock64, a constant-rate
+// counter; the host converts microseconds with the device's rate) have passed since its
+// wait began.  `tag` is the value published (read_tag); a test hook passes a tag that no
+// block publishes instead.
 template <int NT>
-__device__ __forceinline__ dql::DqlParams gather(unsigned* sync, unsigned tag, int spin, bool& ok) {
+__device__ __forceinline__ dql::DqlParams gather(unsigned* sync, unsigned tag, unsigned long long limit,
+                                                 bool& ok) {
     const unsigned long long* s = slots(sync);
     float mn = 0.0f, mx = 0.0f;
     int late = 0;
+    const unsigned long long t0 = wall_clock64();
     for (int b = threadIdx.x; b < (int)gridDim.x; b += NT) {
         unsigned long long lo, hi;
-        for (int it = 0;; ++it) {
+        for (;;) {
             lo = __hip_atomic_load(s + 2 * b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             hi = __hip_atomic_load(s + 2 * b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if ((unsigned)(lo >> 32) == tag && (unsigned)(hi >> 32) == tag) break;
-            if (it >= spin) {
+            if (late || wall_clock64() - t0 > limit) {
                 late = 1;
                 break;
             }

@@ -25,7 +25,7 @@ from collections import namedtuple
 
 import numpy as np
 
-from ._lib import ICX_F32, ICX_I8, ICX_I32, ICX_I64, ICX_U8, IconnxError, check, lib
+from ._lib import ICX_F32, ICX_I8, ICX_I32, ICX_I64, ICX_U8, IconnxError, OpProfile, check, lib
 
 _NP_DT = {np.dtype(np.int8): ICX_I8, np.dtype(np.uint8): ICX_U8,
           np.dtype(np.int32): ICX_I32, np.dtype(np.float32): ICX_F32,
@@ -75,6 +75,38 @@ def _hip_memcpy_d2d(dst, src, nbytes, stream):
         raise IconnxError(5, "hipMemcpyAsync of an output failed (hipError %d)" % rc)
 
 
+class ProfileData:
+    """Result of :meth:`GpuGraphExecutor.run_with_profiling` — the reference's ProfileData
+    (src/cuda/inference/mod.rs:89-164).  Times are microseconds, as floats (the reference
+    truncates to whole microseconds, which rounds short kernels to 0).
+
+    * ``gpu_op_times`` {label: (us, calls)}: device time between the hipEvents that bracket
+      each op on the stream;
+    * ``op_times`` {label: (us, calls)}: host time to validate and enqueue each op;
+    * ``ops``: (node, label, gpu_us, cpu_us) per executed op, in execution order;
+    * ``input_upload_us`` (device time of the input copies), ``node_execution_us`` (host
+      enqueue time of all ops), ``output_download_us``, ``total_us``."""
+
+    def __init__(self):
+        self.input_upload_us = self.node_execution_us = 0.0
+        self.output_download_us = self.total_us = 0.0
+        self.op_times, self.gpu_op_times, self.ops = {}, {}, []
+
+    def summary(self, top=15):
+        """The reference's print_summary as a string: the labels by GPU time."""
+        lines = ["=== GPU Inference Profile ===",
+                 "  Input upload:     %10.1f us" % self.input_upload_us,
+                 "  Node execution:   %10.1f us (host enqueue)" % self.node_execution_us,
+                 "  Output download:  %10.1f us" % self.output_download_us,
+                 "  TOTAL:            %10.1f us" % self.total_us,
+                 "=== Top Operators by GPU-Side Time (HIP events) ==="]
+        for label, (us, calls) in sorted(self.gpu_op_times.items(), key=lambda kv: -kv[1][0])[:top]:
+            cpu = self.op_times.get(label, (0.0, 0))[0]
+            lines.append("  %-28s gpu=%10.1f us cpu=%9.1f us (%4d calls, %8.2f us/call)"
+                         % (label, us, cpu, calls, us / max(calls, 1)))
+        return "\n".join(lines)
+
+
 def constant_value(node):
     """The static tensor of a promotable ``Constant`` node (one non-empty output), else None:
     the ``value`` tensor, else ``value_int`` / ``value_ints`` as Int64, ``value_float`` /
@@ -106,6 +138,7 @@ class GpuGraphExecutor:
             raise IconnxError(1, "icx_graph_create failed")
         self._outputs = []
         self._keep = []  # device inputs bound in place, alive until the next run
+        self._n_nodes = 0
 
     def __del__(self):
         g, self._g = getattr(self, "_g", None), None
@@ -166,6 +199,7 @@ class GpuGraphExecutor:
         check(self._L.icx_graph_add_node(
             self._g, name.encode(), op_type.encode(), len(inputs), _cstrs(list(inputs)),
             len(outputs), _cstrs(list(outputs)), len(keys), _cstrs(keys), vals))
+        self._n_nodes += 1
         for k, v in attributes.items():
             if isinstance(v, (float, np.floating)):
                 check(self._L.icx_graph_set_node_attr_float(self._g, name.encode(), k.encode(),
@@ -276,6 +310,10 @@ class GpuGraphExecutor:
         self._bind(inputs)
         stream = torch.cuda.current_stream().cuda_stream
         check(self._L.icx_graph_run(self._g, ctypes.c_void_p(stream)))
+        return self._fetch(output_names, stream)
+
+    def _fetch(self, output_names, stream):
+        torch = _torch()
         out = {}
         for n in output_names:
             dt, rank = ctypes.c_int(), ctypes.c_int()
@@ -298,6 +336,43 @@ class GpuGraphExecutor:
         out = {k: v.cpu().numpy() for k, v in dev.items()}
         self.check_status()
         return out
+
+    def run_with_profiling(self, inputs, output_names):
+        """``run`` with per-op timing (GpuGraphExecutor::run_with_profiling,
+        src/cuda/inference/mod.rs:649-658): every executed op of one eager run is bracketed by
+        hipEvents on the launch stream.  Returns (host outputs, :class:`ProfileData`), whose
+        ``gpu_op_times`` / ``op_times`` map each label — the op type, or ``Fused_<pattern>``
+        for a fused head, as the reference labels them — to (microseconds, calls)."""
+        import time
+
+        torch = _torch()
+        t0 = time.perf_counter()
+        for n in output_names:
+            self.add_output(n)
+        self._bind(inputs)
+        stream = torch.cuda.current_stream().cuda_stream
+        cap = self._n_nodes + 8  # at most one executed op per node
+        recs = (OpProfile * cap)()
+        n_ops, up = ctypes.c_int(), ctypes.c_float()
+        check(self._L.icx_graph_run_profiled(self._g, ctypes.c_void_p(stream), recs, cap,
+                                             ctypes.byref(n_ops), ctypes.byref(up)))
+        t1 = time.perf_counter()
+        dev = self._fetch(output_names, stream)
+        out = {k: v.cpu().numpy() for k, v in dev.items()}
+        self.check_status()
+        t2 = time.perf_counter()
+        prof = ProfileData()
+        prof.input_upload_us = float(up.value)
+        for r in recs[:min(n_ops.value, cap)]:
+            label, node = r.label.decode(), r.node.decode()
+            prof.ops.append((node, label, float(r.gpu_us), float(r.cpu_us)))
+            for m, v in ((prof.gpu_op_times, r.gpu_us), (prof.op_times, r.cpu_us)):
+                us, calls = m.get(label, (0.0, 0))
+                m[label] = (us + float(v), calls + 1)
+        prof.node_execution_us = sum(o[3] for o in prof.ops)
+        prof.output_download_us = (t2 - t1) * 1e6
+        prof.total_us = (t2 - t0) * 1e6
+        return out, prof
 
     def check_status(self):
         """Synchronise the current stream, then raise IconnxError (ICX_ERR_KERNEL) if a

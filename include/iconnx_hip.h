@@ -332,6 +332,23 @@ int icx_graph_run(icx_graph* g, icx_stream_t stream);
 /* Device pointer / dtype / shape of an output after run (valid until the next run). */
 int icx_graph_get_output(icx_graph* g, const char* name, int* dtype, int* rank, int64_t* dims,
                          const void** device_ptr);
+/* One eager run with per-op timing (GpuGraphExecutor::run_with_profiling,
+ * src/cuda/inference/mod.rs:649-658; Executor::run_with_profiling,
+ * src/cuda/executor/variants.rs:415-515; GpuEventTimer, src/cuda/inference/gpu_event_timer.rs:
+ * 61-117): a hipEvent is recorded after the input uploads and after each executed op, the
+ * stream is synchronised once, and op k's gpu_us is the interval between its event and the
+ * previous one.  Records go to ops[0 .. min(capacity, n) - 1] in execution order; *n_ops =
+ * the number of executed ops; *upload_us (may be NULL) = the input uploads' GPU time.  Not
+ * for a captured graph (the events would be recorded into it): it runs eagerly like
+ * icx_graph_run, with the same outputs. */
+typedef struct icx_op_profile {
+    char label[48]; /* the op type, or "Fused_<pattern>" for a fused head (the reference's op_label) */
+    char node[80];  /* the planned op's node name (truncated) */
+    float gpu_us;   /* device time of its kernels */
+    float cpu_us;   /* host time to validate and enqueue it */
+} icx_op_profile;
+int icx_graph_run_profiled(icx_graph* g, icx_stream_t stream, icx_op_profile* ops, int capacity,
+                           int* n_ops, float* upload_us);
 /* Memory pool statistics: allocations from hipMalloc, pool hits, bytes held. */
 int icx_graph_pool_stats(icx_graph* g, int64_t* hipmallocs, int64_t* hits, int64_t* bytes_held);
 /* Record one run into a HIP graph for repeated inference (no counterpart in the reference,
@@ -359,11 +376,12 @@ int icx_graph_replay(icx_graph* g, icx_stream_t stream);
 int icx_graph_status(icx_graph* g, icx_stream_t stream);
 
 /* ---- test hooks ------------------------------------------------------------------------
- * No counterpart in the reference.  icx_debug_qout_fault(spin): with spin > 0, every later
- * quantized-output launch of this process waits for a tag that no block publishes and gives
- * up after `spin` polls, so every block takes the failure path and exits normally (for
- * testing icx_graph_status); 0 restores normal launches. */
-void icx_debug_qout_fault(int spin);
+ * No counterpart in the reference.  icx_debug_qout_fault(us): with us > 0, every later
+ * exchange launch of this process (quantized-output GEMM, single-launch DQL) waits for a tag
+ * that no block publishes and gives up after `us` microseconds (instead of the normal
+ * 20 ms), so every block takes the failure path and exits normally (for testing
+ * icx_graph_status); 0 restores normal launches. */
+void icx_debug_qout_fault(int us);
 
 #ifdef __cplusplus
 }

@@ -80,3 +80,17 @@ def test_pool_bookkeeping_is_host_only(L):
     assert b"not handed out" in L.icx_last_error()
     assert L.icx_pool_free(p, None) == 0
     L.icx_pool_destroy(p)
+
+
+def test_pool_rejects_a_size_without_a_size_class(L):
+    """A request above the largest power-of-two class (2^63 bytes), e.g. (size_t)-1 from a bad
+    size computation, is ICX_ERR_INVALID_ARG before any device call, not an endless doubling."""
+    p = L.icx_pool_create()
+    out = ctypes.c_void_p(0)
+    try:
+        for n in ((1 << 64) - 1, (1 << 63) + 1):
+            assert L.icx_pool_alloc(p, n, ctypes.byref(out)) == 1
+            assert out.value is None
+            assert b"largest size class" in L.icx_last_error()
+    finally:
+        L.icx_pool_destroy(p)

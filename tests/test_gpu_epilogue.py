@@ -58,12 +58,46 @@ def test_cfg1_single_linear_all_rows():
     run_linear_config("cfg1", lambda M: [(0, M)])
 
 
+def full_epilogue_check(cfg):
+    """The fused quantized linear of a config on every output element.  The int32
+    accumulators come from the GEMM without epilogue (every element of which
+    tests/test_gpu_mmi.py checks against an exact float64 product; here sampled rows against
+    the oracle), the DQL outputs are checked whole against the oracle, and the oracle's
+    Cast -> Mul(x_scale * w_scale) -> Add(bias) -> chain, run over all of them, must equal the
+    fused output bit for bit."""
+    d = configs.make(cfg)
+    x = d["x"].reshape(-1, d["x"].shape[-1])
+    M, K = x.shape
+    xq, xs, xzp, rs = ops.gpu_dynamic_quantize_linear(dev(x), rowsum_row_len=K)
+    w = ops.PackedWeight(dev(d["w"]))
+    epi = [("Mul", (xs, dev(d["w_scale"])), False), ("Add", dev(d["bias"]), False)]
+    epi += [(op, dev(c), False) for op, c in d["chain"]]
+    y = ops.gpu_qlinear(xq, w, xzp, dev(d["w_zp"]), epilogue=epi, a_rowsum=rs)
+    acc = ops.gpu_matmul_integer(xq, w, xzp, dev(d["w_zp"]), a_rowsum=rs)
+    torch.cuda.synchronize()
+    xq_h, xs_h, xzp_h = xq.cpu().numpy(), xs.cpu().numpy(), xzp.cpu().numpy()
+    yq, ys, yz = oracle.dynamic_quantize_linear(x)
+    assert np.array_equal(xq_h, yq) and bits(xs_h) == bits(np.float32(ys)) and int(xzp_h) == int(yz)
+    acc = acc.cpu().numpy()
+    per_col = np.asarray(d["w_zp"]).ndim == 1 and np.asarray(d["w_zp"]).size > 1
+    for r0 in (0, M // 2 + 1, M - 2):
+        want = oracle.matmul_integer(xq_h[r0:r0 + 2], d["w"], xzp_h, d["w_zp"], per_column_b_zp=per_col)
+        assert np.array_equal(acc[r0:r0 + 2], want), "%s accumulators rows %d:%d" % (cfg, r0, r0 + 2)
+    want = oracle.add(oracle.mul(oracle.cast_i32_f32(acc), oracle.mul(xs_h, d["w_scale"])), d["bias"])
+    del acc
+    for op, c in d["chain"]:
+        want = {"Mul": oracle.mul, "Add": oracle.add, "Div": oracle.div, "Sub": oracle.sub}[op](want, c)
+    assert_f32_equal(y.cpu().numpy(), want, "%s fused epilogue, every element" % cfg)
+
+
 def test_cfg2_ffn_up_with_chain():
     run_linear_config("cfg2", lambda M: [(0, 40), (M // 2, M // 2 + 8), (M - 24, M)])
+    full_epilogue_check("cfg2")
 
 
 def test_cfg4_per_channel():
     run_linear_config("cfg4", lambda M: [(0, 16), (M // 3, M // 3 + 8), (M - 16, M)])
+    full_epilogue_check("cfg4")
 
 
 def test_cfg5a_fused_dequant_full_size():
@@ -216,13 +250,11 @@ def test_ffn_down_shape_fused_epilogue():
 
 
 def test_division_fast_path_edge_values():
-    """The GEMM epilogues divide by a column operand d as q0 = RN(v * RN(1/d)) plus one FMA
-    correction when v and d lie in [2^-60, 2^60) in magnitude, and by the IEEE division
-    otherwise.  cfg2's shape (one 256x192 tile per CU) with a Mul before the Div that makes
-    the numerators of chosen columns exactly +-0, subnormal, tiny, huge, inf or NaN, and
-    divisors that are 0, tiny, huge, negative or have an all-ones significand (blocks holding
-    an out-of-range divisor take the IEEE division for the whole step): bit-exact against the
-    oracle's op-by-op graph on every sampled row."""
+    """The GEMM epilogues divide by a column operand d with the correctly rounded IEEE
+    division (__fdiv_rn), whatever the operands.  cfg2's shape (one 256x192 tile per CU) with
+    a Mul before the Div that makes the numerators of chosen columns exactly +-0, subnormal,
+    tiny, huge, inf or NaN, and divisors that are 0, tiny, huge, negative or have an all-ones
+    significand: bit-exact against the oracle's op-by-op graph on every sampled row."""
     rng = np.random.default_rng(41)
     M, K, N = 4096, 768, 3072
     x = rng.standard_normal((M, K)).astype(np.float32)

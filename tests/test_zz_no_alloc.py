@@ -30,12 +30,13 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def noalloc(a, b, azp, bzp, packed=None):
+def noalloc(a, b, azp, bzp, packed=None, out=None):
     """icx_matmul_integer_noalloc; ``packed``: an ops.PackedWeight of ``b`` or None."""
     L = lib()
     M, K = a.shape
     N = b.shape[1]
-    out = torch.full((M, N), -7, dtype=torch.int32, device="cuda")
+    if out is None:
+        out = torch.full((M, N), -7, dtype=torch.int32, device="cuda")
     bp = packed.packed if packed is not None else b
     cs = packed.colsum if packed is not None else None
     check(L.icx_matmul_integer_noalloc(_stream(), _p(a), _DT[a.dtype], _p(bp), _DT[b.dtype],
@@ -78,3 +79,24 @@ def test_noalloc_rejects_a_workspace_beyond_its_array():
         check(L.icx_matmul_integer_noalloc(_stream(), _p(t), ICX_I8, _p(t), ICX_I8, 0, None, 16, K, N,
                                            None, None, 1, None, _p(t)))
     assert e.value.status == 4 and "static scratch" in str(e.value)
+
+
+def test_noalloc_allocates_nothing():
+    """After a warm-up call (which resolves the static array's device address once and loads
+    the kernels), further calls leave the device's free memory exactly as it was: no
+    hipMalloc, no allocating library routine — for the packed and the unpacked weight."""
+    rng = np.random.default_rng(72)
+    a, b, azp, bzp = case(rng, 1024, 768, 3072, np.uint8, np.int8, True)
+    pw = ops.PackedWeight(b)
+    out = torch.empty((1024, 3072), dtype=torch.int32, device="cuda")
+    want = ops.gpu_matmul_integer(a, pw, azp, bzp)
+    for packed in (pw, None):  # warm-up of both forms
+        noalloc(a, b, azp, bzp, packed, out)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        for packed in (pw, None):
+            noalloc(a, b, azp, bzp, packed, out)
+            torch.cuda.synchronize()
+            assert torch.cuda.mem_get_info()[0] == free0, "packed=%s" % (packed is not None)
+    assert torch.equal(out, want)
