@@ -54,6 +54,31 @@ __device__ __forceinline__ float erf_ref(float x) {
     return (x != x) ? x : __fmul_rn(sign, y);
 }
 
+// erf inside the erf-GELU x * (1 + erf(x / sqrt(2))) / 2 of a GEMM epilogue, of an argument
+// given pre-scaled as w = u * sqrt(log2 e) (the column factor 1/sqrt(2) times sqrt(log2 e),
+// formed once per operand): the same Abramowitz-Stegun 7.1.26 formula with d = 1 +
+// (0.3275911 / sqrt(log2 e)) |w|, the polynomial as four FMAs, t = 1/d the hardware
+// reciprocal alone (<= 1 ulp), e^(-u^2) = 2^(-w^2) and 1 - p t e as one FMA; NaN and +-inf
+// need no special case (NaN propagates through every step; |w| = inf gives t = 0, e = 0,
+// y = +-1).  About 11 instructions per element against erf_ref's 26.  It is within 1e-6 of
+// erf_ref — the largest differences lie at |u| < 0.06, from the reciprocal's last bit — and
+// there the GELU multiplies erf by x itself: with the rest of the GELU as in the chain, its
+// output stays within 4e-7 of the op-by-op reference relative to its largest value, as
+// close as with erf_ref (modelled on the CPU with the reciprocal and the exponential off by
+// one ulp either way).
+constexpr float kSqrtLog2e = 1.20112240878f;       // sqrt(log2 e)
+constexpr float kErfP = 0.27273747f;               // 0.3275911 / sqrt(log2 e)
+__device__ __forceinline__ float erf_gelu_scaled(float w) {
+    const float b = fabsf(w);
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(kErfP, b, 1.0f));
+    float p = __builtin_fmaf(1.0614054f, t, -1.4531521f);
+    p = __builtin_fmaf(p, t, 1.4214138f);
+    p = __builtin_fmaf(p, t, -0.28449672f);
+    p = __builtin_fmaf(p, t, 0.2548296f);
+    const float e = __builtin_amdgcn_exp2f(__fmul_rn(-b, b));
+    return copysignf(__builtin_fmaf(-__fmul_rn(p, t), e, 1.0f), w);
+}
+
 __device__ __forceinline__ float chain_operand(const icx_chain_op& op, size_t r, size_t c,
                                                size_t cols) {
     if (!op_takes_operand(op.op)) return 0.0f;
@@ -167,37 +192,49 @@ inline int chain_mode(const icx_chain& ch) {
         { float& x = v[u].w; float& z = sv[u].w; stmt; }                \
     }
 
+// The op codes of the dequantized erf-GELU of an FFN projection (Mul, Add, Save, Mul, Erf,
+// Add, MulSaved, Mul; the operand-side bits ignored) — run as straight-line code below.
+__host__ __device__ inline bool is_gelu8(uint32_t codes, int n_ops) {
+    return n_ops == 8 && (codes & 0x77777777u) == 0x26042502u;
+}
+
 // MODE 0: the four binary ops only (no extra registers, no erf code); MODE 2: also the
-// operand-free steps (erf, save, multiply by the saved value).  The host picks the mode
-// with chain_mode(), so kernels without a GELU-style chain do not pay for it.
+// operand-free steps (erf, save, multiply by the saved value); MODE 3: only the straight-line
+// erf-GELU (is_gelu8 must hold; for a kernel whose register budget has no room for the
+// per-op loop's saved values).  The host picks the mode with chain_mode(), so kernels
+// without a GELU-style chain do not pay for it.
 template <int MODE, int NV, typename OpndFn>
 __device__ __forceinline__ void run_chain4(uint32_t codes, int n_ops, float4 (&v)[NV],
                                            OpndFn opnd) {
-    if constexpr (MODE == 2) {
+    if constexpr (MODE >= 2) {
         // The dequantized erf-GELU of an FFN projection — Mul, Add, Save, Mul (the Div by
         // sqrt(2) as the product with its reciprocal), Erf, Add, Mul by the saved value, Mul —
-        // as straight-line code: the same operations in the same order as the loop below
-        // (Add and Mul commute exactly, so the operand-side bit is ignored), without its per-op
-        // dispatch and the register copies that dispatch costs (about 2 instructions per
-        // element and op against 1).
-        if (n_ops == 8 && (codes & 0x77777777u) == 0x26042502u) {
+        // as straight-line code, without the loop's per-op dispatch and the register copies
+        // that dispatch costs: the dequant Mul and bias Add as in the loop (one rounding each),
+        // then erf_gelu_scaled of x * (c3 sqrt(log2 e)) and x * (erf * c7 + c5 c7) — the
+        // last three ops as one FMA and a product — with the two column factors formed once
+        // per operand.
+        if (MODE == 3 || is_gelu8(codes, n_ops)) {
             const float4 o0 = opnd(0), o1 = opnd(1), o3 = opnd(3), o5 = opnd(5), o7 = opnd(7);
-            auto gelu = [](float x, float a0, float a1, float a3, float a5, float a7) {
+            const float4 w3 = make_float4(__fmul_rn(o3.x, kSqrtLog2e), __fmul_rn(o3.y, kSqrtLog2e),
+                                          __fmul_rn(o3.z, kSqrtLog2e), __fmul_rn(o3.w, kSqrtLog2e));
+            const float4 h57 = make_float4(__fmul_rn(o5.x, o7.x), __fmul_rn(o5.y, o7.y), __fmul_rn(o5.z, o7.z),
+                                           __fmul_rn(o5.w, o7.w));
+            auto gelu = [](float x, float a0, float a1, float c3, float c7, float c57) {
                 x = __fadd_rn(__fmul_rn(x, a0), a1);
-                const float z = x;
-                x = __fadd_rn(erf_ref(__fmul_rn(x, a3)), a5);
-                return __fmul_rn(__fmul_rn(z, x), a7);
+                return __fmul_rn(x, __builtin_fmaf(erf_gelu_scaled(__fmul_rn(x, c3)), c7, c57));
             };
 #pragma unroll
             for (int u = 0; u < NV; ++u) {
-                v[u].x = gelu(v[u].x, o0.x, o1.x, o3.x, o5.x, o7.x);
-                v[u].y = gelu(v[u].y, o0.y, o1.y, o3.y, o5.y, o7.y);
-                v[u].z = gelu(v[u].z, o0.z, o1.z, o3.z, o5.z, o7.z);
-                v[u].w = gelu(v[u].w, o0.w, o1.w, o3.w, o5.w, o7.w);
+                v[u].x = gelu(v[u].x, o0.x, o1.x, w3.x, o7.x, h57.x);
+                v[u].y = gelu(v[u].y, o0.y, o1.y, w3.y, o7.y, h57.y);
+                v[u].z = gelu(v[u].z, o0.z, o1.z, w3.z, o7.z, h57.z);
+                v[u].w = gelu(v[u].w, o0.w, o1.w, w3.w, o7.w, h57.w);
             }
             return;
         }
     }
+    if constexpr (MODE == 3) return;
     // The dequant (Mul) and bias (Add) that head every quantized linear's chain, straight-line
     // for the same reason; the ops after them, if any, go through the loop.  Binary-only
     // chains (MODE 0) only: in the GELU kernels the extra code costs registers.

@@ -488,6 +488,16 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
                  : "memory", "m0");
 }
 
+// The same copy from a wave-uniform base in SGPRs plus a 32-bit per-lane byte offset (the
+// saddr form): a copy's source costs one VGPR instead of a 64-bit address, and advancing
+// along K is a scalar add on the base.  The host keeps every operand below 4 GiB for it.
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_addr)
+                 : "memory", "m0");
+}
+
 __device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -536,28 +546,29 @@ gemm_i8_dma_kernel(GemmArgs g) {
     const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds_addr_of(smem) + cw * PA * 16 * ROWB);
     const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds_addr_of(smem) + BM * ROWB + cw * PB * 16 * ROWB);
 
-    // This lane's source rows / chunks for each of its copies (fixed across K steps).
-    const int8_t* srcA[PA];
-    const int8_t* srcB[PB];
+    // This lane's source rows / chunks for each of its copies (fixed across K steps), as
+    // byte offsets from the operand's base.
+    uint32_t offA[PA], offB[PB];
 #pragma unroll
     for (int i = 0; i < PA; ++i) {
         const int row = (cw * PA + i) * 16 + (lane >> 2);
         const int kc = (lane & 3) ^ ((row >> 2) & 3);
-        srcA[i] = g.A + (size_t)min(m0 + row, g.M - 1) * g.K + 16 * kc;
+        offA[i] = (uint32_t)((size_t)min(m0 + row, g.M - 1) * g.K + 16 * kc);
     }
 #pragma unroll
     for (int i = 0; i < PB; ++i) {
         const int row = (cw * PB + i) * 16 + (lane >> 2);
         const int kc = (lane & 3) ^ ((row >> 2) & 3);
-        srcB[i] = g.Bp + (size_t)min(n0 + row, g.N - 1) * g.K + 16 * kc;
+        offB[i] = (uint32_t)((size_t)min(n0 + row, g.N - 1) * g.K + 16 * kc);
     }
     auto issue = [&](int buf, int kt) {
         if (!copier) return;
-        const int k0 = kt * ROWB;
+        const int8_t* a = g.A + kt * ROWB;
+        const int8_t* b = g.Bp + kt * ROWB;
 #pragma unroll
-        for (int i = 0; i < PA; ++i) dma16(srcA[i] + k0, lds_a + buf * STAGE + i * 16 * ROWB);
+        for (int i = 0; i < PA; ++i) dma16s(a, offA[i], lds_a + buf * STAGE + i * 16 * ROWB);
 #pragma unroll
-        for (int i = 0; i < PB; ++i) dma16(srcB[i] + k0, lds_b + buf * STAGE + i * 16 * ROWB);
+        for (int i = 0; i < PB; ++i) dma16s(b, offB[i], lds_b + buf * STAGE + i * 16 * ROWB);
     };
 
     v16i acc[TI][TJ];
@@ -655,7 +666,9 @@ __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM 
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
     constexpr int NT = 64 * WGM * WGN;
-    constexpr int MODE = CH == CH_COL_EXT ? 2 : 0;
+    // operand-free chains: only the straight-line erf-GELU (the host checks is_gelu8), whose
+    // registers fit the three waves per SIMD
+    constexpr int MODE = CH == CH_COL_EXT ? 3 : 0;
     constexpr int QS = BN + 16;                          // bytes per staged u8 row
     constexpr int SOP_BYTES = ICX_MAX_CHAIN * BN * 4;
     constexpr int COLT_OFF = SOP_BYTES + BM * QS;        // column terms after the byte tile
@@ -786,20 +799,20 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
     const int cw = copier ? wid : 0;
     const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds_addr_of(smem) + cw * PA * 8 * ROWB);
     const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds_addr_of(smem) + BM * ROWB + cw * PB * 8 * ROWB);
-    // lane l of a copy covers row (l >> 3) of its 8-row group, physical slot l & 7
-    const int8_t* srcA[PA];
-    const int8_t* srcB[PB];
+    // lane l of a copy covers row (l >> 3) of its 8-row group, physical slot l & 7 (byte
+    // offsets from the operand's base)
+    uint32_t offA[PA], offB[PB];
 #pragma unroll
     for (int i = 0; i < PA; ++i) {
         const int row = (cw * PA + i) * 8 + (lane >> 3);
         const int kc = (lane & 7) ^ ((row >> 1) & 7);
-        srcA[i] = g.A + (size_t)min(m0 + row, g.M - 1) * g.K + 16 * kc;
+        offA[i] = (uint32_t)((size_t)min(m0 + row, g.M - 1) * g.K + 16 * kc);
     }
 #pragma unroll
     for (int i = 0; i < PB; ++i) {
         const int row = (cw * PB + i) * 8 + (lane >> 3);
         const int kc = (lane & 7) ^ ((row >> 1) & 7);
-        srcB[i] = g.Bp + (size_t)min(n0 + row, g.N - 1) * g.K + 16 * kc;
+        offB[i] = (uint32_t)((size_t)min(n0 + row, g.N - 1) * g.K + 16 * kc);
     }
     const int KT = g.K / ROWB;
     // the launch number of a quantized-output launch: read by one thread before its first
@@ -810,11 +823,12 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
     if (QOUT != 0 && t == 0) q_tag0 = icx::qx::read_tag(g.q_sync);
     auto issue = [&](int buf, int kt) {
         if (!copier) return;
-        const int k0 = kt * ROWB;
+        const int8_t* a = g.A + kt * ROWB;
+        const int8_t* b = g.Bp + kt * ROWB;
 #pragma unroll
-        for (int i = 0; i < PA; ++i) dma16(srcA[i] + k0, lds_a + buf * STAGE + i * 8 * ROWB);
+        for (int i = 0; i < PA; ++i) dma16s(a, offA[i], lds_a + buf * STAGE + i * 8 * ROWB);
 #pragma unroll
-        for (int i = 0; i < PB; ++i) dma16(srcB[i] + k0, lds_b + buf * STAGE + i * 8 * ROWB);
+        for (int i = 0; i < PB; ++i) dma16s(b, offB[i], lds_b + buf * STAGE + i * 8 * ROWB);
     };
 
     v16i acc[TI][TJ];
@@ -980,30 +994,30 @@ gemm_i8_stream_kernel(GemmArgs g) {
             rowB[i] = (p * PB + i) * 16 + (lane >> 2);
             kcB[i] = 16 * ((lane & 3) ^ ((rowB[i] >> 2) & 3));
         }
-        const int8_t* srcA[PA];
-        const int8_t* srcB[PB];
+        uint32_t offA[PA], offB[PB];  // byte offsets from the operands' bases
         auto set_tile = [&](int ordinal) {
             int tm, tn;
             stream_tile(g, (int)blockIdx.x + ordinal * G, T, tm, tn);
 #pragma unroll
             for (int i = 0; i < PA; ++i)
-                srcA[i] = g.A + (size_t)min(tm * BM + rowA[i], g.M - 1) * g.K + kcA[i];
+                offA[i] = (uint32_t)((size_t)min(tm * BM + rowA[i], g.M - 1) * g.K + kcA[i]);
 #pragma unroll
             for (int i = 0; i < PB; ++i)
-                srcB[i] = g.Bp + (size_t)min(tn * BN + rowB[i], g.N - 1) * g.K + kcB[i];
+                offB[i] = (uint32_t)((size_t)min(tn * BN + rowB[i], g.N - 1) * g.K + kcB[i]);
         };
         // Issue state: the step being issued, as (tile ordinal, K step).
         int it = 0, ik = 0, buf = 0;
         set_tile(0);
         auto issue_next = [&]() {
             const uint32_t off = __builtin_amdgcn_readfirstlane(buf * STAGE);
-            const int k0 = ik * ROWB;
+            const int8_t* a = g.A + __builtin_amdgcn_readfirstlane(ik * ROWB);
+            const int8_t* b = g.Bp + __builtin_amdgcn_readfirstlane(ik * ROWB);
 #pragma unroll
             for (int i = 0; i < PA; ++i)
-                dma16(srcA[i] + k0, __builtin_amdgcn_readfirstlane(ldsA + off + i * 16 * ROWB));
+                dma16s(a, offA[i], __builtin_amdgcn_readfirstlane(ldsA + off + i * 16 * ROWB));
 #pragma unroll
             for (int i = 0; i < PB; ++i)
-                dma16(srcB[i] + k0, __builtin_amdgcn_readfirstlane(ldsB + off + i * 16 * ROWB));
+                dma16s(b, offB[i], __builtin_amdgcn_readfirstlane(ldsB + off + i * 16 * ROWB));
             buf = buf + 1 == NS ? 0 : buf + 1;
             // advance to the next step; past the last one keep re-copying it
             if (it * KT + ik + 1 < S) {
@@ -1542,7 +1556,9 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
     for (int i = 0; i < n_seg; ++i) g.seg[i] = segs[i];
 
     const bool vec = K >= 16 && (K % 16 == 0) && icx::aligned16(A) && icx::aligned16(Bp);
-    const bool dma = vec && K >= 64 && K % 64 == 0;
+    // (the LDS-DMA main loops address each operand as a base plus 32-bit byte offsets)
+    const bool dma = vec && K >= 64 && K % 64 == 0 && (uint64_t)M * K <= 0xffffffffull &&
+                     (uint64_t)N * K <= 0xffffffffull;
     const bool colchain = out_kind == OUT_F32 && icx::chain_is_col_only(g.chain);
     const int ch = !colchain ? CH_GENERAL : (icx::chain_mode(g.chain) == 2 ? CH_COL_EXT : CH_COL);
     // 256x256 tiles (128x128 per wave) when there are enough of them to fill the chip;
@@ -1722,7 +1738,8 @@ int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp
     if (!icx::is_int8_kind(a_dtype) || b_dtype != ICX_I8)
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: needs an Int8 weight (dtypes %d, %d)", a_dtype, b_dtype);
     if (M == 0 || M > 0x7fffffff || K > 0x7fffffff || N > 0x7fffffff || K < 128 || K % 128 != 0 ||
-        N % 192 != 0 || !icx::aligned16(A) || !icx::aligned16(Bp) || !icx::aligned16(y))
+        N % 192 != 0 || (uint64_t)M * K > 0xffffffffull || (uint64_t)N * K > 0xffffffffull ||
+        !icx::aligned16(A) || !icx::aligned16(Bp) || !icx::aligned16(y))
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: shape %zux%zux%zu or alignment outside the 256x192 kernel",
                  M, K, N);
     GemmArgs g{};
@@ -1763,7 +1780,11 @@ int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp
         g.q_wait = icx::wall_ticks((unsigned)f);
         g.q_poison = 0x80000000u;
     }
-    if (icx::chain_mode(g.chain) == 2) return launch_qout<CH_COL_EXT>(blocks, s, g);
+    if (icx::chain_mode(g.chain) == 2) {
+        if (!icx::is_gelu8(g.codes, g.chain.n_ops))
+            ICX_FAIL(ICX_ERR_UNSUPPORTED, "QLinear+DQL: an operand-free chain other than the erf-GELU");
+        return launch_qout<CH_COL_EXT>(blocks, s, g);
+    }
     return launch_qout<CH_COL>(blocks, s, g);
 }
 

@@ -55,6 +55,34 @@ __device__ __forceinline__ void publish(unsigned* sync, unsigned tag, float mn, 
     __hip_atomic_store(s + 1, hi | __float_as_uint(mx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// dql::block_minmax that also ORs `flag` over the block through the same LDS exchange and
+// barrier (__syncthreads_or would add a barrier and, forming the block-linear thread id from
+// all three work-item ids, keep the packed id register alive for the whole kernel).
+template <int NT>
+__device__ __forceinline__ bool block_minmax_any(float& mn, float& mx, int flag) {
+    __shared__ float smn[NT / 64], smx[NT / 64];
+    __shared__ int sfl[NT / 64];
+    dql::wave_minmax(mn, mx);
+    const int any = __any(flag) ? 1 : 0;
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        smn[wid] = mn;
+        smx[wid] = mx;
+        sfl[wid] = any;
+    }
+    __syncthreads();
+    mn = smn[0];
+    mx = smx[0];
+    int f = sfl[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) {
+        dql::acc_minmax(smn[w], mn, mx);
+        dql::acc_minmax(smx[w], mn, mx);
+        f |= sfl[w];
+    }
+    return f != 0;
+}
+
 // Every thread of a block of NT threads: wait for all gridDim.x blocks' pairs (thread t polls
 // blocks t, t + NT, ...), fold them as the DQL launch does and return its parameters.
 // `ok` is false in every thread if any wait of this block ran out: a thread gives up on the
@@ -84,8 +112,7 @@ __device__ __forceinline__ dql::DqlParams gather(unsigned* sync, unsigned tag, u
         dql::acc_minmax(__uint_as_float((uint32_t)lo), mn, mx);
         dql::acc_minmax(__uint_as_float((uint32_t)hi), mn, mx);
     }
-    ok = __syncthreads_or(late) == 0;
-    dql::block_minmax<NT>(mn, mx);
+    ok = !block_minmax_any<NT>(mn, mx, late);
     return dql::make_params(mn, mx);
 }
 

@@ -108,9 +108,12 @@ def test_qlinear_with_gelu_epilogue():
 
 
 def test_gelu_epilogue_straight_line_matches_the_chain_loop():
-    """The 8-op dequant + erf-GELU epilogue runs as straight-line code; the same ops through
-    the per-op loop (the dequant and bias in the GEMM store, then the 6-op GELU chain as a
-    separate launch) give the same bits."""
+    """The 8-op dequant + erf-GELU epilogue runs as straight-line code with the epilogue's
+    erf (erf_gelu_scaled: FMA polynomial, hardware reciprocal) and its last three ops as
+    one FMA and a product; the same ops through the per-op loop (the dequant and bias in the
+    GEMM store, then the 6-op GELU chain as a separate launch, with the reference-order erf)
+    agree within 5e-7 of the output's largest value, and both match the oracle within 1e-6 —
+    the GELU multiplies erf by x where the two erf forms differ most (|x| < 0.06)."""
     rng = np.random.default_rng(5)
     x = rng.standard_normal((512, 768)).astype(np.float32)
     w = rng.integers(-127, 128, (768, 3072)).astype(np.int8)
@@ -124,7 +127,11 @@ def test_gelu_epilogue_straight_line_matches_the_chain_loop():
     y8 = host(ops.gpu_qlinear(xq, pw, xzp, None, epilogue=lin + gelu, a_rowsum=rs))
     t = ops.gpu_qlinear(xq, pw, xzp, None, epilogue=lin, a_rowsum=rs)
     y2 = host(ops.gpu_fused_chain(t, gelu))
-    assert np.array_equal(bits(y8), bits(y2))
+    assert rel_err(y8, y2) < 5e-7
+    th = host(t)
+    want = oracle.mul(oracle.mul(th, oracle.add(oracle.erf(oracle.div(th, np.float32(1.4142135))),
+                                                np.float32(1.0))), np.float32(0.5))
+    assert rel_err(y8, want) < 1e-6 and rel_err(y2, want) < 1e-6
 
 
 def test_qlinear_with_gelu_epilogue_narrow_tile():
