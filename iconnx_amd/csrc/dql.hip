@@ -248,10 +248,10 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
 // Single launch, flat mode: block b holds the float4s [256 b, 256 b + 256) of x in registers
 // (one per lane), the last block also the n % 4 scalar tail.  The block's (min, max) goes
 // through the exchange; once every block's pair is in, each block quantizes its registers
-// and writes y.  A block whose wait ran out writes its part of y as 0 (the last block out
-// then writes the scale as NaN and counts the launch in the exchange buffer's error word).
-// `poison` is 0 but for the fault test hook, which makes every wait expect a tag no block
-// publishes.
+// and writes y.  A block whose wait ran out writes its part of y as 0 and counts itself in
+// the exchange buffer's error word (block 0's, which every block then shares, also makes the
+// scale NaN).  `poison` is 0 but for the fault test hook, which makes block 0's wait expect a
+// tag no block publishes.
 constexpr int kExchangeMaxBlocks = 128;  // inputs up to 128 * 1024 (+ 3) elements
 
 __global__ void __launch_bounds__(kThreads)
@@ -271,7 +271,7 @@ dql_exchange_kernel(const float* __restrict__ x, size_t n4, int tail, uint8_t* _
     const unsigned tag = s_tag;
     if (threadIdx.x == 0) icx::qx::publish(sync, tag, mn, mx);
     bool ok;
-    const DqlParams p = icx::qx::gather<kThreads>(sync, tag ^ poison, wait, ok);
+    const DqlParams p = icx::qx::gather<kThreads>(sync, tag, tag ^ poison, wait, ok);
     if (i < n4) reinterpret_cast<uint32_t*>(y)[i] = ok ? quant4(v, p) : 0u;
     if (has_tail) y[n4 * 4 + threadIdx.x] = ok ? (uint8_t)quant1(xt, p) : (uint8_t)0;
     if (threadIdx.x == 0) icx::qx::finish(sync, ok, p, y_scale, y_zp);

@@ -16,6 +16,7 @@
 #include "chain.hpp"
 #include "icx_common.hpp"
 #include "internal.hpp"
+#include "qexchange.hpp"
 #include <cmath>
 
 #include <algorithm>
@@ -391,6 +392,14 @@ struct AttnArgs {
     float recip;      // 1 / scale when that is exact (a power of two), so x / scale == x * recip
     int recip_exact;  // bit for bit, and the division becomes a multiplication
     int qsplit;       // blocks per (batch, head): 2 when S > 64 (64 queries each), else 1
+    // quantized output (attention_kernel<true>): the DynamicQuantizeLinear of out, written as
+    // u8 (row stride ldo), scale and zero point, through qexchange.hpp's range exchange
+    uint8_t* qy;
+    float* q_scale;
+    uint8_t* q_zp;
+    unsigned* q_sync;
+    unsigned long long q_wait;  // exchange wait limit, wall-clock ticks
+    unsigned q_poison;          // test hook: a tag no block publishes
 };
 
 __device__ __forceinline__ float apply_scale(float x, const AttnArgs& a) {
@@ -402,8 +411,16 @@ __device__ __forceinline__ float f4c(const float4& v, int e) {
     return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
 }
 
+// QOUT: the context is not stored; the blocks (all resident: the host launches no more than
+// fit) trade their (min, max) through the range exchange (qexchange.hpp) and each writes its
+// part of the DynamicQuantizeLinear of the context — y, scale and zero point bit-identical to that op
+// applied to the f32 context (the same fold, parameters and per-element rounding,
+// dql_core.hpp).
+template <bool QOUT>
 __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float lds[ATT_LDS_FLOATS];
+    unsigned tag0 = 0;  // the exchange's tag, read early to hide its latency
+    if (QOUT && threadIdx.x == 0) tag0 = icx::qx::read_tag(a.q_sync);
     // The two halves of a (batch, head) are blocks g and g + 8 of a group of 16, which the
     // hardware places on the same XCD (block i runs on XCD i % 8), so the second half's K and
     // V loads hit that XCD's L2.
@@ -548,6 +565,38 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[dt][r] = __fmul_rn(o[dt][r], inv_r[r]);
     // lane l holds ctx rows (queries) 16 w + 4 lg + r, dims 16 dt + lq
+    if constexpr (QOUT) {
+        __shared__ unsigned s_tag;
+        float qmn = 0.0f, qmx = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (half * ATT_QB + 16 * w + 4 * lg + r >= S) continue;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) icx::range_acc(o[dt][r], qmn, qmx);
+        }
+        if (t == 0) s_tag = tag0;
+        icx::dql::block_minmax<kThreads>(qmn, qmx);  // its barrier also publishes s_tag
+        const unsigned tag = s_tag;
+        if (t == 0) icx::qx::publish(a.q_sync, tag, qmn, qmx);
+        bool ok;
+        const icx::dql::DqlParams p = icx::qx::gather<kThreads>(a.q_sync, tag, tag ^ a.q_poison, a.q_wait, ok);
+        // the block's 64 x 64 bytes go through LDS (free: every wave is past the gather's
+        // barrier), then out as 16-byte row segments, four lanes per row
+        uint8_t* qt = reinterpret_cast<uint8_t*>(lds);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t b4 = ok ? icx::dql::quant4(make_float4(o[0][r], o[1][r], o[2][r], o[3][r]), p) : 0u;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) qt[(16 * w + 4 * lg + r) * ATT_D + 16 * dt + lq] = (uint8_t)(b4 >> (8 * dt));
+        }
+        __syncthreads();
+        const int qrow = half * ATT_QB + (t >> 2);
+        if (qrow < S)
+            *reinterpret_cast<uint4*>(a.qy + ((size_t)b * S + qrow) * a.ldo + h * ATT_D + 16 * (t & 3)) =
+                *reinterpret_cast<const uint4*>(qt + (t >> 2) * ATT_D + 16 * (t & 3));
+        if (t == 0) icx::qx::finish(a.q_sync, ok, p, a.q_scale, a.q_zp);
+        return;
+    }
     float mn = 0.0f, mx = 0.0f;  // DQL range of out (when a.part is given)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -732,37 +781,103 @@ extern "C" int icx_matmul_f32(icx_stream_t stream, const float* a, const float* 
     return ICX_OK;
 }
 
-int icx::attention_f32(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
-                       size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
-                       int scale_div, int scale_q, float* out, float2* part, int* n_part) {
-    if (n_part) *n_part = 0;
-    if (!q || !k || !v || !out) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention: null pointer argument");
+namespace {
+// Shape checks and kernel arguments shared by the f32 and the quantized-output launches.
+int attention_args(const float* q, const float* k, const float* v, size_t B, size_t S, size_t H, size_t D,
+                   size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale, int scale_div, int scale_q,
+                   AttnArgs* a, size_t* blocks) {
+    if (!q || !k || !v) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention: null pointer argument");
     if (D != (size_t)ATT_D || S == 0 || S > (size_t)ATT_S)
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention: head size %zu / sequence %zu unsupported (D = 64, S <= 128)", D, S);
     if (ldq < H * D || ldk < H * D || ldv < H * D || ldo < H * D || (ldq | ldk | ldv) % 4 ||
         !icx::aligned16(q) || !icx::aligned16(k) || !icx::aligned16(v))
         ICX_FAIL(ICX_ERR_SHAPE, "Attention: row strides must cover H*D and keep 16-byte alignment");
-    if (B * H == 0) return ICX_OK;
     if (B * H > 0x3fffffff) ICX_FAIL(ICX_ERR_SHAPE, "Attention: too many (batch, head) pairs");
     // two blocks per (batch, head) when S > 64 (each takes 64 queries), one otherwise
     const size_t per = S > (size_t)ATT_QB ? 2 : 1;
-    const size_t blocks = B * H * per;
-    float2* pp = (part && blocks <= (size_t)icx::kMaxRangeParts) ? part : nullptr;
-    AttnArgs a{q, k, v, out, (int)S, (int)H, (int64_t)ldq, (int64_t)ldk, (int64_t)ldv, (int64_t)ldo,
-               scale, scale_div ? 1 : 0, scale_q ? 1 : 0, pp, 0.0f, 0, (int)per};
-    {
-        // a power-of-two scale whose reciprocal is a normal float: x / scale == x * (1 / scale)
-        int e = 0;
-        const float m = std::frexp(scale, &e);
-        const float r = 1.0f / scale;
-        if (m == 0.5f && std::isnormal(scale) && std::isnormal(r)) {
-            a.recip = r;
-            a.recip_exact = 1;
-        }
+    *blocks = B * H * per;
+    *a = AttnArgs{};
+    a->q = q;
+    a->k = k;
+    a->v = v;
+    a->S = (int)S;
+    a->H = (int)H;
+    a->ldq = (int64_t)ldq;
+    a->ldk = (int64_t)ldk;
+    a->ldv = (int64_t)ldv;
+    a->ldo = (int64_t)ldo;
+    a->scale = scale;
+    a->scale_div = scale_div ? 1 : 0;
+    a->scale_q = scale_q ? 1 : 0;
+    a->qsplit = (int)per;
+    // a power-of-two scale whose reciprocal is a normal float: x / scale == x * (1 / scale)
+    int e = 0;
+    const float m = std::frexp(scale, &e);
+    const float r = 1.0f / scale;
+    if (m == 0.5f && std::isnormal(scale) && std::isnormal(r)) {
+        a->recip = r;
+        a->recip_exact = 1;
     }
-    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
+    return ICX_OK;
+}
+}  // namespace
+
+int icx::attention_f32(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
+                       size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
+                       int scale_div, int scale_q, float* out, float2* part, int* n_part) {
+    if (n_part) *n_part = 0;
+    if (!out) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention: null pointer argument");
+    AttnArgs a;
+    size_t blocks;
+    int rc = attention_args(q, k, v, B, S, H, D, ldq, ldk, ldv, ldo, scale, scale_div, scale_q, &a, &blocks);
+    if (rc) return rc;
+    if (blocks == 0) return ICX_OK;
+    a.out = out;
+    float2* pp = (part && blocks <= (size_t)icx::kMaxRangeParts) ? part : nullptr;
+    a.part = pp;
+    hipLaunchKernelGGL(attention_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
     ICX_LAUNCH_CHECK("attention_kernel");
     if (pp && n_part) *n_part = (int)blocks;
+    return ICX_OK;
+}
+
+int icx::attention_dql(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
+                       size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
+                       int scale_div, int scale_q, uint8_t* y, float* y_scale, uint8_t* y_zp, unsigned* sync) {
+    if (!y || !y_scale || !y_zp || !sync) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention+DQL: null pointer argument");
+    if (ldo % 16 || !icx::aligned16(y))
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention+DQL: the u8 rows must keep 16-byte alignment");
+    AttnArgs a;
+    size_t blocks;
+    int rc = attention_args(q, k, v, B, S, H, D, ldq, ldk, ldv, ldo, scale, scale_div, scale_q, &a, &blocks);
+    if (rc) return rc;
+    if (blocks == 0 || blocks > (size_t)icx::kQoutMaxBlocks)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention+DQL: %zu blocks outside the exchange's 1..%d", blocks,
+                 icx::kQoutMaxBlocks);
+    // every block must be resident at once for the exchange: launch only what fits
+    static int per_cu[64] = {0};
+    int d = 0;
+    ICX_HIP_CHECK(hipGetDevice(&d));
+    if (d < 0 || d >= 64) ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention+DQL: device %d", d);
+    if (!per_cu[d]) {
+        int nb = 0;
+        ICX_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, attention_kernel<true>, kThreads, 0));
+        per_cu[d] = nb > 0 ? nb : -1;
+    }
+    if (per_cu[d] < 0 || blocks > (size_t)per_cu[d] * icx::num_cus())
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention+DQL: %zu blocks exceed the %d resident ones", blocks,
+                 per_cu[d] * icx::num_cus());
+    a.qy = y;
+    a.q_scale = y_scale;
+    a.q_zp = y_zp;
+    a.q_sync = sync;
+    a.q_wait = icx::wall_ticks(icx::kExchangeWaitUs);
+    if (const int f = icx::qout_fault_spin()) {  // test hook
+        a.q_wait = icx::wall_ticks((unsigned)f);
+        a.q_poison = 0x80000000u;
+    }
+    hipLaunchKernelGGL(attention_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
+    ICX_LAUNCH_CHECK("attention_kernel");
     return ICX_OK;
 }
 

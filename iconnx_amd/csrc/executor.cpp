@@ -271,7 +271,7 @@ struct icx_graph {
     std::set<std::string> dql_done;  // DQL outputs already written by their producer's GEMM
     int64_t quant_fused = 0;         // GEMM launches that quantized their own output
     int64_t dql_single = 0;          // DynamicQuantizeLinear runs done as one launch
-    unsigned* qsync = nullptr;       // exchange buffer of both kinds of launch (zeroed once)
+    unsigned* qsync = nullptr;       // range-exchange buffer of every launch that uses one (zeroed once)
     hipStream_t last_stream = nullptr;
     bool ran = false;
     Pool pool;
@@ -471,13 +471,18 @@ class Planner {
             g_.keep.insert(o);
             g_.keep.insert(root_of(o));
         }
-        // a quantized-linear head (Int8 weight without zero point, no sibling group) whose
-        // output only a DynamicQuantizeLinear reads, and whose quantized output no GEMM reads
-        // row sums of: the head's GEMM may write the DQL's outputs itself
+        // a quantized-linear head (Int8 weight without zero point, no sibling group) or an
+        // attention head whose output only a DynamicQuantizeLinear reads, and whose quantized
+        // output no GEMM reads row sums of: the head's kernel may write the DQL's outputs itself
         g_.quant_out.clear();
         for (auto& op : g_.plan) {
-            if (op.kind != Kind::FusedHead || op.pattern != Pattern::QuantizedLinear || !op.group.empty()) continue;
-            if (g_.inits[op.w].dtype != ICX_I8 || !(op.w_zp.empty() || op.w_zp_folded)) continue;
+            if (op.kind != Kind::FusedHead) continue;
+            if (op.pattern == Pattern::QuantizedLinear) {
+                if (!op.group.empty()) continue;
+                if (g_.inits[op.w].dtype != ICX_I8 || !(op.w_zp.empty() || op.w_zp_folded)) continue;
+            } else if (op.pattern != Pattern::Attention) {
+                continue;
+            }
             if (g_.keep.count(op.out) || !g_.range_wanted.count(op.out)) continue;
             auto cs = gi_.consumers.find(op.out);
             if (cs == gi_.consumers.end() || cs->second.size() != 1) continue;
@@ -1640,10 +1645,29 @@ class Runner {
         const std::vector<int64_t> shape = Q->shape;
         const float *q = static_cast<const float*>(Q->ptr), *k = static_cast<const float*>(K->ptr),
                     *v = static_cast<const float*>(V->ptr);
+        const size_t hd = (size_t)shape[2];
+        auto qo = g_.quant_out.find(op.out);
+        if (qo != g_.quant_out.end() && g_.qsync) {  // the context's only reader is a DQL
+            const Node& d = qo->second;
+            DevTensor *QY, *QS, *QZ;
+            rc = alloc(d.out[0], ICX_U8, shape, &QY);
+            if (!rc) rc = alloc(d.out[1], ICX_F32, {}, &QS);
+            if (!rc) rc = alloc(d.out[2], ICX_U8, {}, &QZ);
+            if (rc) return rc;
+            rc = icx::attention_dql(s_, q, k, v, shape[0], shape[1], op.heads, op.head_dim, hd, hd, hd, hd, op.scale,
+                                    op.scale_div ? 1 : 0, op.scale_q ? 1 : 0, static_cast<uint8_t*>(QY->ptr),
+                                    static_cast<float*>(QS->ptr), static_cast<uint8_t*>(QZ->ptr), g_.qsync);
+            if (rc == ICX_OK) {
+                g_.dql_done.insert(d.out[0]);
+                ++g_.quant_fused;
+                return ICX_OK;
+            }
+            if (rc != ICX_ERR_UNSUPPORTED) return rc;
+            icx::clear_error();  // a grid that would not be resident at once: f32 context, then the DQL
+        }
         DevTensor* O;
         rc = alloc(op.out, ICX_F32, shape, &O);
         if (rc) return rc;
-        const size_t hd = (size_t)shape[2];
         float2* part;
         rc = range_parts(op.out, &part);
         if (rc) return rc;
@@ -2388,7 +2412,7 @@ static int icx_graph_compile_impl(icx_graph* g, icx_stream_t stream) {
     if (g->ran && g->last_stream) ICX_HIP_CHECK(hipStreamSynchronize(g->last_stream));
     g->clear_run();
     g->free_weights();
-    // the range-exchange buffer, for quantized-output GEMMs and single-launch DQLs
+    // the range-exchange buffer, for quantized-output GEMMs / attentions and single-launch DQLs
     bool exchange = !g->quant_out.empty();
     for (auto& op : g->plan)
         if (op.kind == Kind::Regular && op.node.op == "DynamicQuantizeLinear") exchange = true;
@@ -2743,10 +2767,10 @@ extern "C" int icx_graph_status(icx_graph* g, icx_stream_t stream) {
         ICX_HIP_CHECK(hipMemsetAsync(word, 0, sizeof failed, s));
         ICX_HIP_CHECK(hipStreamSynchronize(s));
         ICX_FAIL(ICX_ERR_KERNEL,
-                 "DynamicQuantizeLinear range exchange: %u launch(es) since the last status check (quantized-output "
-                 "GEMMs or single-launch DQLs) had a block whose wait for the other blocks' ranges ran out (they "
-                 "were not all resident, e.g. other work held CUs); their quantized outputs are invalid (y = 0, "
-                 "scale = NaN)",
+                 "DynamicQuantizeLinear range exchange: %u failure record(s) since the last status check — a "
+                 "launch that quantizes its own output (quantized-output GEMM or attention, single-launch DQL) had "
+                 "blocks whose wait for the other blocks' ranges ran out (they were not all resident, e.g. other "
+                 "work held CUs); its quantized output is invalid (y = 0, scale = NaN)",
                  failed);
     }
     return ICX_OK;

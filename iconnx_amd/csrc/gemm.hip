@@ -78,7 +78,7 @@ struct GemmArgs {
     uint8_t* q_zp;
     unsigned* q_sync;
     unsigned long long q_wait;  // exchange wait limit, wall-clock ticks
-    unsigned q_poison;  // 0; the fault test hook makes every wait expect tag ^ q_poison
+    unsigned q_poison;  // 0; the fault test hook makes block 0's wait expect tag ^ q_poison
 };
 
 // Output of the tile whose first column is n0: base pointer, row stride and the global
@@ -728,7 +728,7 @@ __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM 
     icx::dql::block_minmax<NT>(mn, mx);
     if (t == 0) icx::qx::publish(g.q_sync, tag, mn, mx);
     bool ok;
-    const icx::dql::DqlParams p = icx::qx::gather<NT>(g.q_sync, tag ^ g.q_poison, g.q_wait, ok);
+    const icx::dql::DqlParams p = icx::qx::gather<NT>(g.q_sync, tag, tag ^ g.q_poison, g.q_wait, ok);
     // quantize into the LDS byte tile [BM][QS]
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {

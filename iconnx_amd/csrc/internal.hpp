@@ -31,6 +31,16 @@ int attention_f32(hipStream_t s, const float* q, const float* k, const float* v,
                   size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
                   int scale_div, int scale_q, float* out, float2* part, int* n_part);
 
+// The attention of icx_attention_f32 followed by a DynamicQuantizeLinear of its output, as
+// one launch: y [B * S, row stride ldo] u8, y_scale, y_zp are what the DQL of the f32
+// context would give, bit for bit, and the context itself is never written.  The blocks
+// trade their ranges through `sync` (qlinear_dql's exchange, same contract and failure
+// reporting).  ICX_ERR_UNSUPPORTED, having launched nothing, for a grid that would not be
+// resident at once.
+int attention_dql(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
+                  size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
+                  int scale_div, int scale_q, uint8_t* y, float* y_scale, uint8_t* y_zp, unsigned* sync);
+
 // icx_qlinear_f32 with the same partial output.
 int qlinear_f32(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype, int b_packed,
                 const int32_t* b_colsum, size_t M, size_t K, size_t N, const void* a_zp, const void* b_zp,
@@ -55,7 +65,8 @@ int qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, in
 // ICX_ERR_UNSUPPORTED, having launched nothing, for a shape outside the kernel or a grid
 // that would not be resident at once.
 constexpr int kQoutMaxBlocks = 1024;  // blocks of one quantized-output launch
-constexpr size_t kQoutSyncBytes = 256 + 16 * (size_t)kQoutMaxBlocks;  // qexchange.hpp's layout
+// qexchange.hpp's layout: words and the launch's result, a tagged pair per block, 9 counters
+constexpr size_t kQoutSyncBytes = 256 + 16 * (size_t)kQoutMaxBlocks + 9 * 128;
 constexpr int kQoutErrWord = 2;  // word of that buffer counting launches whose exchange failed
 // icx_matmul_integer_noalloc's file-scope device scratch (one per GPU, for the process's life)
 constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;

@@ -418,12 +418,14 @@ def test_quantized_output_selection():
 
 
 def test_encoder_ffn_up_quantizes_its_own_output():
-    """The FFN-up's erf-GELU output feeds only the FFN-down's DQL; no other producer."""
+    """The FFN-up's erf-GELU output feeds only the FFN-down's DQL and the attention context
+    only the output projection's DQL: those two producers quantize their own outputs; the
+    LayerNorm outputs (read by a DQL and by the next residual Add) do not."""
     ex = GpuGraphExecutor()
     out, names, _ = graphs.encoder_graph(ex, layers=2)
     ex.add_output(out)
     planned, _ = ex.quantized_outputs()
-    assert set(planned) == {t["h"] for t in names}
+    assert set(planned) == {t["h"] for t in names} | {t["ctx"] for t in names}
     entries, _ = ex.plan()
     dql_of = {e.node: e for e in entries if e.op_type == "DynamicQuantizeLinear"}
     assert all(d in dql_of for d in planned.values())

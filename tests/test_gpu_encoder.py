@@ -140,37 +140,40 @@ def test_full_size_encoder_node_by_node():
     assert np.all(np.isfinite(got[out]))
 
 
-def ff2_names(names):
+def ff2_names(names, tag="ff2"):
     out = []
     for t in names:
         base = t["q"].rsplit(".", 2)[0]
-        out += [base + ".ff2.x_q", base + ".ff2.x_scale", base + ".ff2.x_zp"]
+        out += [base + ".%s.x_q" % tag, base + ".%s.x_scale" % tag, base + ".%s.x_zp" % tag]
     return out
 
 
 def test_full_size_encoder_as_benched():
     """The 6-layer b32 s128 encoder exactly as bench.py runs it: captured with only the final
-    output requested, so every FFN-up GEMM quantizes its own output for the FFN-down's DQL
-    (six fused launches) and every other DQL takes its range from its producer; replayed
-    twice.  The reference run is the same graph run eagerly with every FFN-up f32 output
-    requested, which turns that fusion off (the separate DQL runs on the f32 tensor; the
-    node-by-node test pins that path to the oracle, and its FFN-down DQLs are checked against
-    the oracle here too).  The bar is bit equality of every layer's FFN-down quantized input
-    (x_q, scale, zero point) and of the final output."""
+    output requested, so every FFN-up GEMM quantizes its own output for the FFN-down's DQL and
+    every attention its context for the output projection's DQL (twelve fused launches), and
+    every other DQL takes its range from its producer; replayed twice.  The reference run is
+    the same graph run eagerly with every FFN-up output and every attention context requested
+    as f32, which turns those fusions off (the separate DQLs run on the f32 tensors; the
+    node-by-node test pins that path to the oracle, and those DQLs are checked against the
+    oracle here too).  The bar is bit equality of every layer's FFN-down and output-projection
+    quantized inputs (x_q, scale, zero point) and of the final output."""
     cfg = graphs.ENCODER
     B, S, H, L = cfg["batch"], cfg["seq"], cfg["heads"], cfg["layers"]
     x = torch.from_numpy(graphs.encoder_input(B, S)).cuda()
 
     ref_ex = GpuGraphExecutor()
     out, names, _ = graphs.encoder_graph(ref_ex, layers=L, heads=H)
-    qnames = ff2_names(names)
-    want = ref_ex.run({"x": x}, [out] + [t["h"] for t in names] + qnames)
+    qnames = ff2_names(names) + ff2_names(names, "o")
+    want = ref_ex.run({"x": x}, [out] + [t["h"] for t in names] + [t["ctx"] for t in names] + qnames)
     assert ref_ex.quantized_outputs() == ({}, 0)
-    for l, t in enumerate(names):
-        yq, ys, yz = oracle.dynamic_quantize_linear(want[t["h"]])
-        assert_bits(want[qnames[3 * l]], yq, "L%d ff2 x_q (unfused) vs oracle" % l)
-        assert_bits(want[qnames[3 * l + 1]], np.asarray(ys, np.float32), "L%d ff2 scale (unfused) vs oracle" % l)
-        assert int(want[qnames[3 * l + 2]]) == int(yz)
+    for src, base in (("h", 0), ("ctx", 3 * L)):
+        for l, t in enumerate(names):
+            yq, ys, yz = oracle.dynamic_quantize_linear(want[t[src]])
+            i = base + 3 * l
+            assert_bits(want[qnames[i]], yq, "L%d DQL of %s x_q (unfused) vs oracle" % (l, src))
+            assert_bits(want[qnames[i + 1]], np.asarray(ys, np.float32), "L%d DQL of %s scale vs oracle" % (l, src))
+            assert int(want[qnames[i + 2]]) == int(yz)
 
     # as benched: only the final output
     ex = GpuGraphExecutor()
@@ -178,10 +181,10 @@ def test_full_size_encoder_as_benched():
     xin = x.clone()
     ex.capture({"x": xin}, [out])
     planned, launches = ex.quantized_outputs()
-    assert sorted(planned) == sorted(t["h"] for t in names)
+    assert sorted(planned) == sorted([t["h"] for t in names] + [t["ctx"] for t in names])
     # capture runs the plan twice on the host (the warm-up run, then the recorded one): every
-    # layer's FFN-up launch took the fused form both times
-    assert launches == 2 * L, "%d fused launches for %d layers" % (launches, L)
+    # layer's FFN-up and attention launches took the fused form both times
+    assert launches == 2 * 2 * L, "%d fused launches for %d layers" % (launches, L)
     for rep in range(2):
         ex.replay()
         got = ex.outputs([out])[out].cpu().numpy()
@@ -194,7 +197,7 @@ def test_full_size_encoder_as_benched():
     graphs.encoder_graph(ex2, layers=L, heads=H)
     ex2.capture({"x": xin}, [out] + qnames)
     assert ex2.plan()[0] == ex.plan()[0]
-    assert ex2.quantized_outputs() == (planned, 2 * L)
+    assert ex2.quantized_outputs() == (planned, 2 * 2 * L)
     for rep in range(2):
         ex2.replay()
         got = {k: v.cpu().numpy() for k, v in ex2.outputs([out] + qnames).items()}

@@ -205,7 +205,7 @@ def test_exchange_that_gives_up_is_an_error_status():
             ex.check_status()
     finally:
         L.icx_debug_qout_fault(0)
-    assert e.value.status == 7 and "1 launch" in str(e.value)
+    assert e.value.status == 7 and "range exchange" in str(e.value)
     assert ex.quantized_outputs()[1] == 1
     assert np.isnan(got["hs"].cpu().numpy()) and not got["hq"].cpu().numpy().any()
     ex.check_status()  # cleared
@@ -219,3 +219,131 @@ def test_exchange_that_gives_up_is_an_error_status():
         L.icx_debug_qout_fault(0)
     assert e.value.status == 7
     check_same(ex.run({"x": x}, ["hq", "hs", "hzp"]), want, "normal run after the second failure")
+
+
+# ---- the attention that quantizes its own context ---------------------------------------------
+def build_attention(ex, H):
+    """q, k, v [B, S, H*64] -> the exported self-attention -> DynamicQuantizeLinear(ctx)."""
+    from iconnx_amd import graphs
+
+    for n in "qkv":
+        ex.add_input(n, [None, None, H * 64])
+    ctx = graphs.add_self_attention(ex, "q", "k", "v", H, 64, "att")
+    ex.add_node("dql_ctx", "DynamicQuantizeLinear", [ctx], ["cq", "cs", "czp"])
+    return ctx
+
+
+def qkv(B, S, H, seed):
+    rng = np.random.default_rng(seed)
+    return {n: (rng.standard_normal((B, S, H * 64)) * (1.0 + i)).astype(np.float32) for i, n in enumerate("qkv")}
+
+
+def check_attention_same(fused, ref, what):
+    check_same({"hq": fused["cq"], "hs": fused["cs"], "hzp": fused["czp"]},
+               {"hq": ref["cq"], "hs": ref["cs"], "hzp": ref["czp"]}, what)
+
+
+@pytest.mark.parametrize("B,S,H,fused_launch", [
+    (32, 128, 12, True),   # the encoder's attention: 768 blocks of 64 queries
+    (4, 100, 12, True),    # partial last block of queries
+    (3, 64, 4, True),      # one block per (batch, head)
+    (64, 128, 12, False),  # 1536 blocks: more than the exchange holds -> f32 context + DQL launch
+])
+def test_attention_quantized_output_matches_separate_dql(B, S, H, fused_launch):
+    """The attention whose context only a DynamicQuantizeLinear reads writes that DQL's u8
+    output, scale and zero point itself (the context is never formed); the same graph with the
+    context requested runs the attention and then the DQL, whose result is the oracle's DQL of
+    that context bit for bit.  The fused and the separate results are bit-identical."""
+    feeds = qkv(B, S, H, seed=B * S + H)
+    ref_ex, fused_ex = GpuGraphExecutor(), GpuGraphExecutor()
+    ctx = build_attention(ref_ex, H)
+    build_attention(fused_ex, H)
+    ref = ref_ex.run(feeds, [ctx, "cq", "cs", "czp"])
+    assert ref_ex.quantized_outputs()[0] == {}
+    yq, ys, yz = oracle.dynamic_quantize_linear(ref[ctx])
+    check_attention_same(ref, {"cq": yq, "cs": ys, "czp": yz}, "separate DQL vs oracle")
+    fused = fused_ex.run(feeds, ["cq", "cs", "czp"])
+    planned, launches = fused_ex.quantized_outputs()
+    assert planned == {ctx: "dql_ctx"}
+    assert launches == (1 if fused_launch else 0)
+    check_attention_same(fused, ref, "fused vs separate (B=%d S=%d H=%d)" % (B, S, H))
+
+
+def test_attention_quantized_output_capture_replay_and_failure():
+    """Recorded and replayed with eager work between the replays (bit-identical to eager
+    runs), then the exchange's failure path: with the test hook every wait gives up, the
+    status check reports ICX_ERR_KERNEL, and a normal run afterwards is correct."""
+    from iconnx_amd._lib import IconnxError, lib
+
+    B, S, H = 32, 128, 12
+    ex, ref_ex = GpuGraphExecutor(), GpuGraphExecutor()
+    ctx = build_attention(ex, H)
+    build_attention(ref_ex, H)
+    inputs = [{n: torch.from_numpy(a).cuda() for n, a in qkv(B, S, H, seed=s).items()} for s in (1, 2)]
+    bound = {n: t.clone() for n, t in inputs[0].items()}
+    ex.capture(bound, ["cq", "cs", "czp"])
+    for rep in range(3):
+        src = inputs[rep % 2]
+        for n in bound:
+            bound[n].copy_(src[n])
+        ex.replay()
+        got = {k: v.cpu().numpy() for k, v in ex.outputs(["cq", "cs", "czp"]).items()}
+        ex.check_status()
+        want = ref_ex.run({n: t.cpu().numpy() for n, t in src.items()}, [ctx, "cq", "cs", "czp"])
+        check_attention_same(got, want, "replay %d" % rep)
+        _ = (src["q"] * 2.0).sum().item()  # eager work between the replays
+    run_ex = GpuGraphExecutor()
+    build_attention(run_ex, H)
+    L = lib()
+    L.icx_debug_qout_fault(64)
+    try:
+        bad = run_ex.run_device(inputs[0], ["cq", "cs", "czp"])
+        with pytest.raises(IconnxError) as e:
+            run_ex.check_status()
+    finally:
+        L.icx_debug_qout_fault(0)
+    assert e.value.status == 7
+    assert np.isnan(bad["cs"].cpu().numpy()) and not bad["cq"].cpu().numpy().any()
+    want = ref_ex.run({n: t.cpu().numpy() for n, t in inputs[0].items()}, [ctx, "cq", "cs", "czp"])
+    check_attention_same(run_ex.run(inputs[0], ["cq", "cs", "czp"]), want, "normal run after the failure")
+
+
+def test_attention_quantized_outputs_interleaved_with_gemm_exchanges():
+    """Two attentions that quantize their contexts, with a quantized-output GEMM (the other
+    kind of range exchange, which keeps its own launch numbers in the same buffer) between
+    them, in one graph run three times: every quantized tensor equals the separate DQL's."""
+    from iconnx_amd import graphs
+
+    H, K = 12, 768
+    def make(ex):
+        for n in "qkv":
+            ex.add_input(n, [None, None, H * 64])
+        c1 = graphs.add_self_attention(ex, "q", "k", "v", H, 64, "a1")
+        ex.add_node("dql1", "DynamicQuantizeLinear", [c1], ["c1q", "c1s", "c1z"])
+        rng = np.random.default_rng(4)
+        ex.add_initializer("w", rng.integers(-127, 128, (K, 3072)).astype(np.int8))
+        ex.add_initializer("ws", np.array(0.003, np.float32))
+        ex.add_initializer("b", (0.05 * rng.standard_normal(3072)).astype(np.float32))
+        ex.add_node("mm", "MatMulInteger", ["c1q", "w", "c1z"], ["acc"])
+        ex.add_node("cast", "Cast", ["acc"], ["accf"], {"to": 1})
+        ex.add_node("sc", "Mul", ["c1s", "ws"], ["s"])
+        ex.add_node("deq", "Mul", ["accf", "s"], ["l0"])
+        ex.add_node("bias", "Add", ["l0", "b"], ["lin"])
+        ex.add_node("dqlh", "DynamicQuantizeLinear", ["lin"], ["hq", "hs", "hz"])
+        c2 = graphs.add_self_attention(ex, "k", "v", "q", H, 64, "a2")
+        ex.add_node("dql2", "DynamicQuantizeLinear", [c2], ["c2q", "c2s", "c2z"])
+        return c1, c2
+    ref_ex, ex = GpuGraphExecutor(), GpuGraphExecutor()
+    c1, c2 = make(ref_ex)
+    make(ex)
+    names = ["c1q", "c1s", "c1z", "hq", "hs", "hz", "c2q", "c2s", "c2z"]
+    for s in range(3):
+        feeds = qkv(32, 128, H, seed=40 + s)
+        want = ref_ex.run(feeds, [c1, c2, "lin"] + names)
+        got = ex.run(feeds, names)
+        for n in names:
+            assert got[n].shape == want[n].shape, (s, n)
+            bad = int(np.count_nonzero(bits(got[n]) != bits(want[n])))
+            assert bad == 0, "run %d: %s: %d of %d differ" % (s, n, bad, want[n].size)
+    planned, launches = ex.quantized_outputs()
+    assert sorted(planned) == sorted([c1, c2, "lin"]) and launches == 9
