@@ -89,6 +89,7 @@ SIGNATURES = {
     "icx_graph_add_initializer": ([P, C, I, I, P, P], I),
     "icx_graph_add_node": ([P, C, C, I, CP, I, CP, I, CP, P], I),
     "icx_graph_add_output": ([P, C], I),
+    "icx_graph_set_option": ([P, C, ctypes.c_int64], I),
     "icx_graph_set_node_attr_float": ([P, C, C, ctypes.c_double], I),
     "icx_graph_set_node_attr_ints": ([P, C, C, I, P], I),
     "icx_graph_plan": ([P, P, S], I),

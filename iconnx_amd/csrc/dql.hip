@@ -67,26 +67,35 @@ __device__ __forceinline__ Slice slice_of(size_t units, size_t unit, size_t tail
     return s;
 }
 
-// Reduce the partials of launch 1 (every block of launch 2 does this redundantly).  The
-// first 4 * kThreads partials (all of them for the grids used here) are requested at once;
-// a missing one reads as (0, 0), which never moves a range that starts at (0, 0).
-__device__ __forceinline__ DqlParams fold_partials(const float2* __restrict__ part, int G) {
-    float mn = 0.0f, mx = 0.0f;
+// Reduce the partials of launch 1 (every block of launch 2 does this redundantly).  All
+// partials (at most kMaxPartials: the producers' grids are capped) are requested at once,
+// by load_partials before the kernel requests its own data: a wave's loads complete in
+// issue order, so the fold then waits for the partials alone and overlaps the data loads
+// (requested after them, the fold waited for every data load: +1.6 us on a 4096 x 768
+// quantize).  Both sets of loads are unconditional (clamped in-bounds index), since after
+// a conditional load the compiler cannot count what is in flight and waits for everything:
+// a lane past the last partial reads the last one again, which cannot move a min / max.
+constexpr int kMaxPartials = 4 * kThreads;
+static_assert(kMaxBlocks <= kMaxPartials && icx::kMaxRangeParts <= kMaxPartials,
+              "every partial of a launch-1 grid or a range-leaving kernel is folded");
+struct Partials {
     float2 v[4];
+};
+__device__ __forceinline__ Partials load_partials(const float2* __restrict__ part, int G) {
+    Partials pv;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int i = threadIdx.x + u * kThreads;
-        v[u] = i < G ? part[i] : make_float2(0.0f, 0.0f);
+        pv.v[u] = part[i < G ? i : G - 1];
     }
+    return pv;
+}
+__device__ __forceinline__ DqlParams fold_partials(const Partials& pv) {
+    float mn = 0.0f, mx = 0.0f;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        acc_minmax(v[u].x, mn, mx);
-        acc_minmax(v[u].y, mn, mx);
-    }
-    for (int i = threadIdx.x + 4 * kThreads; i < G; i += kThreads) {
-        const float2 w = part[i];
-        acc_minmax(w.x, mn, mx);
-        acc_minmax(w.y, mn, mx);
+        acc_minmax(pv.v[u].x, mn, mx);
+        acc_minmax(pv.v[u].y, mn, mx);
     }
     block_minmax<kThreads>(mn, mx);
     return make_params(mn, mx);
@@ -121,29 +130,35 @@ dql_minmax_kernel(const float* __restrict__ x, size_t units, size_t unit, size_t
     if (threadIdx.x == 0) part[blockIdx.x] = make_float2(mn, mx);
 }
 
-// Flat quantize of this block's slice: lane-consecutive float4 in, 4 bytes out.
-// `vec`: x 16-byte and y 4-byte aligned (unit == 4).
-template <bool NT>
+// Flat quantize of this block's slice: lane-consecutive float4 in, 4 bytes out (VEC: x
+// 16-byte and y 4-byte aligned, unit == 4), else one element at a time.  (Two kernels, not a
+// branch: with the scalar path beside it, the compiler hoisted the fold's first step above
+// the data loads.)
+template <bool NT, bool VEC>
 __global__ void __launch_bounds__(kThreads)
-dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size_t tail, int vec,
+dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size_t tail,
                     uint8_t* __restrict__ y, const float2* __restrict__ part, int G,
                     float* __restrict__ y_scale, uint8_t* __restrict__ y_zp) {
     const Slice sl = slice_of(units, unit, tail);
     const size_t t = threadIdx.x;
-    size_t scalar_from = sl.e0;
-    if (vec) {
+    const Partials pv = load_partials(part, G);
+    if constexpr (VEC) {
         const float4* x4 = reinterpret_cast<const float4*>(x);
         uint32_t* y4 = reinterpret_cast<uint32_t*>(y);
         const size_t b4 = sl.e0 / 4, end4 = b4 + (sl.e1 - sl.e0) / 4;
         size_t i = b4 + t;
         // the lane's first kU float4 are requested before the partials are folded, so the
-        // fold's loads and barriers overlap them; every batch is guarded per element, so a
-        // short last batch still has all its loads in flight at once
+        // fold's barriers overlap them (a slice holds at least one float4: past its end the
+        // load repeats the last one, which is not stored); every later batch is guarded per
+        // element, so a short last batch still has all its loads in flight at once
         float4 v[kU];
 #pragma unroll
-        for (int j = 0; j < kU; ++j)
-            if (i + j * kThreads < end4) v[j] = x4[i + j * kThreads];
-        const DqlParams p = fold_partials(part, G);
+        for (int j = 0; j < kU; ++j) {
+            const size_t k = i + j * kThreads;
+            v[j] = x4[k < end4 ? k : end4 - 1];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the fold stays after the data loads' issue
+        const DqlParams p = fold_partials(pv);
         if (blockIdx.x == 0 && threadIdx.x == 0) {
             *y_scale = (float)p.s;
             *y_zp = (uint8_t)p.zp;
@@ -159,14 +174,14 @@ dql_quantize_kernel(const float* __restrict__ x, size_t units, size_t unit, size
                 if (i + j * kThreads < end4) v[j] = x4[i + j * kThreads];
         }
         for (size_t j = end4 * 4 + t; j < sl.e1; j += kThreads) y[j] = (uint8_t)quant1(x[j], p);
-        return;
+    } else {
+        const DqlParams p = fold_partials(pv);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            *y_scale = (float)p.s;
+            *y_zp = (uint8_t)p.zp;
+        }
+        for (size_t j = sl.e0 + t; j < sl.e1; j += kThreads) y[j] = (uint8_t)quant1(x[j], p);
     }
-    const DqlParams p = fold_partials(part, G);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        *y_scale = (float)p.s;
-        *y_zp = (uint8_t)p.zp;
-    }
-    for (size_t j = scalar_from + t; j < sl.e1; j += kThreads) y[j] = (uint8_t)quant1(x[j], p);
 }
 
 // Row mode: the slices are whole rows; one wave per row at a time, and the row sums of y
@@ -177,7 +192,7 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
                          uint8_t* __restrict__ y, int32_t* __restrict__ rowsum,
                          const float2* __restrict__ part, int G, float* __restrict__ y_scale,
                          uint8_t* __restrict__ y_zp) {
-    const DqlParams p = fold_partials(part, G);
+    const DqlParams p = fold_partials(load_partials(part, G));
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         *y_scale = (float)p.s;
         *y_zp = (uint8_t)p.zp;
@@ -320,8 +335,9 @@ extern "C" size_t icx_dql_workspace_size(size_t) { return sizeof(float2) * kMaxB
 // and kernels as the second launch below).
 int icx::dql_from_parts(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
                         int32_t* rowsum, size_t row_len, const float2* part, int n_part) {
-    if (!x || !y || !y_scale || !y_zp || !part || n_part <= 0)
-        ICX_FAIL(ICX_ERR_INVALID_ARG, "DynamicQuantizeLinear: null pointer or no partials");
+    if (!x || !y || !y_scale || !y_zp || !part || n_part <= 0 || n_part > kMaxPartials)
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "DynamicQuantizeLinear: null pointer, or %d partials (1..%d)", n_part,
+                 kMaxPartials);
     if (rowsum && (row_len == 0 || n % row_len != 0))
         ICX_FAIL(ICX_ERR_SHAPE, "DynamicQuantizeLinear: row_len %zu does not divide n = %zu", row_len, n);
     const bool x16 = icx::aligned16(x), y4 = (reinterpret_cast<uintptr_t>(y) & 3u) == 0;
@@ -335,8 +351,10 @@ int icx::dql_from_parts(hipStream_t s, const float* x, size_t n, uint8_t* y, flo
         ICX_LAUNCH_CHECK("dql_quantize_rows_kernel");
         return ICX_OK;
     }
+    // float4 units only when there is at least one: the vector kernel's slices (G <= units)
+    // then each hold a float4, which its first, unconditional loads read
     size_t units, unit, tail;
-    if (x16 && y4) {
+    if (x16 && y4 && n >= 4) {
         units = n / 4;
         unit = 4;
         tail = n % 4;
@@ -346,9 +364,14 @@ int icx::dql_from_parts(hipStream_t s, const float* x, size_t n, uint8_t* y, flo
         tail = 0;
     }
     const int G = (int)std::max<size_t>(1, std::min<size_t>({(size_t)kMaxBlocks, icx::cdiv(n, (size_t)kThreads * 16), units}));
-    const int qvec = (x16 && y4 && unit == 4) ? 1 : 0;
-    hipLaunchKernelGGL(dql_quantize_kernel<false>, dim3(G), dim3(kThreads), 0, s, x, units, unit, tail, qvec, y, part,
-                       n_part, y_scale, y_zp);
+    const int qvec = unit == 4 ? 1 : 0;
+    if (qvec && units < (size_t)G) ICX_FAIL(ICX_ERR_INVALID_ARG, "DynamicQuantizeLinear: %d slices of %zu float4", G, units);
+    if (qvec)
+        hipLaunchKernelGGL((dql_quantize_kernel<false, true>), dim3(G), dim3(kThreads), 0, s, x, units, unit, tail, y,
+                           part, n_part, y_scale, y_zp);
+    else
+        hipLaunchKernelGGL((dql_quantize_kernel<false, false>), dim3(G), dim3(kThreads), 0, s, x, units, unit, tail, y,
+                           part, n_part, y_scale, y_zp);
     ICX_LAUNCH_CHECK("dql_quantize_kernel");
     return ICX_OK;
 }
@@ -372,7 +395,7 @@ int icx::dql_two_launch(hipStream_t s, const float* x, size_t n, uint8_t* y, flo
         units = n / row_len;
         unit = row_len;
         tail = 0;
-    } else if (x16 && y4) {
+    } else if (x16 && y4 && n >= 4) {  // as in dql_from_parts: every slice holds a float4
         units = n / 4;
         unit = 4;
         tail = n % 4;
@@ -399,12 +422,15 @@ int icx::dql_two_launch(hipStream_t s, const float* x, size_t n, uint8_t* y, flo
         ICX_LAUNCH_CHECK("dql_quantize_rows_kernel");
     } else {
         const int qvec = (x16 && y4 && unit == 4) ? 1 : 0;
-        if (nt_y)
-            hipLaunchKernelGGL(dql_quantize_kernel<true>, dim3(G), dim3(kThreads), 0, s, x, units, unit,
-                               tail, qvec, y, part, G, y_scale, y_zp);
+        if (!qvec)
+            hipLaunchKernelGGL((dql_quantize_kernel<false, false>), dim3(G), dim3(kThreads), 0, s, x, units, unit,
+                               tail, y, part, G, y_scale, y_zp);
+        else if (nt_y)
+            hipLaunchKernelGGL((dql_quantize_kernel<true, true>), dim3(G), dim3(kThreads), 0, s, x, units, unit,
+                               tail, y, part, G, y_scale, y_zp);
         else
-            hipLaunchKernelGGL(dql_quantize_kernel<false>, dim3(G), dim3(kThreads), 0, s, x, units, unit,
-                               tail, qvec, y, part, G, y_scale, y_zp);
+            hipLaunchKernelGGL((dql_quantize_kernel<false, true>), dim3(G), dim3(kThreads), 0, s, x, units, unit,
+                               tail, y, part, G, y_scale, y_zp);
         ICX_LAUNCH_CHECK("dql_quantize_kernel");
     }
     return ICX_OK;

@@ -137,18 +137,17 @@ layer_norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ re
     if (t < 8 * ROWS) {
         const int r = t >> 3, j = t & 7;
         if (r < nr) {  // whole 8-lane groups
+            // both passes read the row from LDS (a register copy of the lane's PER values
+            // would cost PER VGPRs in every wave of the block, and with them occupancy)
             const float* tr = tile + r * STRIDE + j;
-            float v[PER];
-#pragma unroll
-            for (int k = 0; k < PER; ++k) v[k] = tr[8 * k];
             float p = 0.0f;
-#pragma unroll
-            for (int k = 0; k < PER; ++k) p = __fadd_rn(p, v[k]);
+#pragma unroll 16
+            for (int k = 0; k < PER; ++k) p = __fadd_rn(p, tr[8 * k]);
             const float mean = __fdiv_rn(combine8(p), (float)cols);
             p = 0.0f;
-#pragma unroll
+#pragma unroll 16
             for (int k = 0; k < PER; ++k) {
-                const float c = __fsub_rn(v[k], mean);
+                const float c = __fsub_rn(tr[8 * k], mean);
                 p = __fadd_rn(p, __fmul_rn(c, c));
             }
             const float var = __fdiv_rn(combine8(p), (float)cols);

@@ -251,14 +251,16 @@ struct icx_graph {
 
     // plan
     bool planned = false, compiled = false;
+    bool quant_out_on = true;  // option "quantized_outputs"
     std::vector<PlannedOp> plan;
     std::vector<std::string> live_outputs;     // requested outputs, or the sinks
     std::set<std::string> keep;                // tensors that stay until the next run
     std::map<std::string, size_t> last_use;    // tensor -> plan index of its last reader
     std::set<std::string> rowsum_wanted;       // DQL outputs whose row sums a GEMM reads
     std::set<std::string> range_wanted;        // DQL inputs whose producer leaves their range
-    // quantized-linear head output -> the DynamicQuantizeLinear that is its only reader: the
-    // head's GEMM writes the DQL's outputs itself when the shape allows (icx::qlinear_dql)
+    // head output -> the DynamicQuantizeLinear that is its only reader, whose outputs the
+    // head's kernel writes itself when the shape allows (the f32 output is never formed): a
+    // quantized linear's GEMM (icx::qlinear_dql) or an attention (icx::attention_dql)
     std::map<std::string, Node> quant_out;
 
     // device state
@@ -269,7 +271,7 @@ struct icx_graph {
     std::map<std::string, std::string> rowsum_of;  // DQL y -> its row-sum tensor
     std::map<std::string, std::pair<std::string, int>> range_of;  // DQL x -> (partials tensor, count)
     std::set<std::string> dql_done;  // DQL outputs already written by their producer's GEMM
-    int64_t quant_fused = 0;         // GEMM launches that quantized their own output
+    int64_t quant_fused = 0;         // head launches that quantized their own output
     int64_t dql_single = 0;          // DynamicQuantizeLinear runs done as one launch
     unsigned* qsync = nullptr;       // range-exchange buffer of every launch that uses one (zeroed once)
     hipStream_t last_stream = nullptr;
@@ -476,7 +478,7 @@ class Planner {
         // output no GEMM reads row sums of: the head's kernel may write the DQL's outputs itself
         g_.quant_out.clear();
         for (auto& op : g_.plan) {
-            if (op.kind != Kind::FusedHead) continue;
+            if (op.kind != Kind::FusedHead || !g_.quant_out_on) continue;
             if (op.pattern == Pattern::QuantizedLinear) {
                 if (!op.group.empty()) continue;
                 if (g_.inits[op.w].dtype != ICX_I8 || !(op.w_zp.empty() || op.w_zp_folded)) continue;
@@ -2355,6 +2357,20 @@ extern "C" int icx_graph_set_node_attr_ints(icx_graph* g, const char* node, cons
     n->iattrs[attr] = std::vector<int64_t>(values, values + count);
     g->invalidate();
     return ICX_OK;
+}
+
+extern "C" int icx_graph_set_option(icx_graph* g, const char* name, int64_t value) {
+    icx::clear_error();
+    if (!g || !name) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_option: bad arguments");
+    if (std::strcmp(name, "quantized_outputs") == 0) {
+        if (value != 0 && value != 1) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_option: quantized_outputs is 0 or 1");
+        if (g->quant_out_on != (value != 0)) {
+            g->quant_out_on = value != 0;
+            g->invalidate();
+        }
+        return ICX_OK;
+    }
+    ICX_FAIL(ICX_ERR_INVALID_ARG, "set_option: no option '%s'", name);
 }
 
 extern "C" int icx_graph_add_output(icx_graph* g, const char* name) {

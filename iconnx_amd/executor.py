@@ -214,6 +214,12 @@ class GpuGraphExecutor:
             self._outputs.append(name)
         check(self._L.icx_graph_add_output(self._g, name.encode()))
 
+    def set_option(self, name, value):
+        """Planner option; ``"quantized_outputs"``: True (default) lets a head whose output
+        only a DynamicQuantizeLinear reads write that DQL's outputs in the same launch, False
+        runs every DQL as its own launch (bit-identical results).  Replans at the next run."""
+        check(self._L.icx_graph_set_option(self._g, name.encode(), int(value)))
+
     # ---- lowering -------------------------------------------------------------------------
     def plan(self):
         """Fusion decision and op order (host only, no GPU work): a list of PlanEntry, plus
@@ -256,9 +262,10 @@ class GpuGraphExecutor:
         return entries, rowsums
 
     def quantized_outputs(self):
-        """Quantized-linear outputs read only by a DynamicQuantizeLinear, mapped to that
-        node: the GEMM writes the DQL's outputs itself when the shape allows, and the f32
-        tensor is never formed.  Second value: how many GEMM launches so far did that."""
+        """Head outputs (quantized linear, attention) read only by a DynamicQuantizeLinear,
+        mapped to that node: the head's kernel writes the DQL's outputs itself when the shape
+        allows, and the f32 tensor is never formed.  Second value: how many head launches so
+        far did that."""
         self.plan()
         return dict(self._quant_out), self._quant_launches
 

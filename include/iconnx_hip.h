@@ -317,6 +317,13 @@ int icx_graph_set_node_attr_float(icx_graph* g, const char* node, const char* at
 int icx_graph_set_node_attr_ints(icx_graph* g, const char* node, const char* attr, int count,
                                  const int64_t* values);
 int icx_graph_add_output(icx_graph* g, const char* name);
+/* A planner option (no counterpart in the reference, whose nodes always run one by one):
+ *   "quantized_outputs" 1 (default) / 0 — whether a head whose output only a
+ *   DynamicQuantizeLinear reads (quantized linear, attention) may write that DQL's outputs
+ *   itself in the same launch; 0 runs every DQL as its own launch (the results are
+ *   bit-identical either way; the option isolates the fused kernels when checking that).
+ * ICX_ERR_INVALID_ARG for an unknown name or value.  Takes effect at the next plan. */
+int icx_graph_set_option(icx_graph* g, const char* name, int64_t value);
 /* Host passes only (topological sort, fusion decision, zero-point folding); no GPU work.
  * Writes a text summary into buf (may be NULL): one "<node> <op> <kind> <pattern> [k=v...]"
  * line per executed op in order (kind Regular or FusedHead; a head's fused nodes follow it as

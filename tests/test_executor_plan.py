@@ -417,18 +417,27 @@ def test_quantized_output_selection():
     assert ex.quantized_outputs()[0] == {}
 
 
-def test_encoder_ffn_up_quantizes_its_own_output():
+def test_encoder_heads_quantize_their_own_outputs():
     """The FFN-up's erf-GELU output feeds only the FFN-down's DQL and the attention context
-    only the output projection's DQL: those two producers quantize their own outputs; the
-    LayerNorm outputs (read by a DQL and by the next residual Add) do not."""
+    only the output projection's DQL: those producers quantize their own outputs; the
+    LayerNorm outputs (read by a DQL and by the next residual Add) do not.  The option
+    "quantized_outputs" off plans none of them."""
     ex = GpuGraphExecutor()
     out, names, _ = graphs.encoder_graph(ex, layers=2)
     ex.add_output(out)
     planned, _ = ex.quantized_outputs()
-    assert set(planned) == {t["h"] for t in names} | {t["ctx"] for t in names}
+    assert set(planned) == {t[k] for k in ("h", "ctx") for t in names}
     entries, _ = ex.plan()
     dql_of = {e.node: e for e in entries if e.op_type == "DynamicQuantizeLinear"}
     assert all(d in dql_of for d in planned.values())
+    ex.set_option("quantized_outputs", False)
+    assert ex.quantized_outputs()[0] == {}
+    ex.set_option("quantized_outputs", True)
+    assert set(ex.quantized_outputs()[0]) == set(planned)
+    with pytest.raises(IconnxError):
+        ex.set_option("quantized_outputs", 2)
+    with pytest.raises(IconnxError):
+        ex.set_option("no_such_option", 1)
 
 
 def _dq_graph(rank, scale_n, axis, zp):

@@ -151,29 +151,38 @@ def ff2_names(names, tag="ff2"):
 def test_full_size_encoder_as_benched():
     """The 6-layer b32 s128 encoder exactly as bench.py runs it: captured with only the final
     output requested, so every FFN-up GEMM quantizes its own output for the FFN-down's DQL and
-    every attention its context for the output projection's DQL (twelve fused launches), and
+    every attention its context for the output projection's DQL (2L fused launches), and
     every other DQL takes its range from its producer; replayed twice.  The reference run is
-    the same graph run eagerly with every FFN-up output and every attention context requested
-    as f32, which turns those fusions off (the separate DQLs run on the f32 tensors; the
-    node-by-node test pins that path to the oracle, and those DQLs are checked against the
-    oracle here too).  The bar is bit equality of every layer's FFN-down and output-projection
-    quantized inputs (x_q, scale, zero point) and of the final output."""
+    the same graph run eagerly with those fusions turned off (the planner option
+    "quantized_outputs": every DQL a launch of its own on the f32 tensor, which the
+    node-by-node test pins to the oracle; those DQLs are checked against the oracle here
+    too).  The bar is bit equality of every layer's quantized GEMM inputs (x_q, scale, zero
+    point) and of the final output."""
     cfg = graphs.ENCODER
     B, S, H, L = cfg["batch"], cfg["seq"], cfg["heads"], cfg["layers"]
     x = torch.from_numpy(graphs.encoder_input(B, S)).cuda()
 
     ref_ex = GpuGraphExecutor()
     out, names, _ = graphs.encoder_graph(ref_ex, layers=L, heads=H)
-    qnames = ff2_names(names) + ff2_names(names, "o")
-    want = ref_ex.run({"x": x}, [out] + [t["h"] for t in names] + [t["ctx"] for t in names] + qnames)
+    ref_ex.set_option("quantized_outputs", False)
+    qnames = ff2_names(names) + ff2_names(names, "o") + ff2_names(names, "ff1") + ff2_names(names, "qkv")
+    srcs = [t[k] for k in ("h", "ctx", "x1", "out") for t in names]
+    want = ref_ex.run({"x": x}, list(dict.fromkeys([out] + srcs + qnames)))
     assert ref_ex.quantized_outputs() == ({}, 0)
-    for src, base in (("h", 0), ("ctx", 3 * L)):
+    for j, (src, base) in enumerate((("h", 0), ("ctx", 3 * L), ("x1", 6 * L), ("out", 9 * L))):
         for l, t in enumerate(names):
+            if src == "out":  # the Q/K/V DQL of layer l + 1 reads layer l's output
+                if l == L - 1:
+                    continue
+                i = base + 3 * (l + 1)
+            else:
+                i = base + 3 * l
             yq, ys, yz = oracle.dynamic_quantize_linear(want[t[src]])
-            i = base + 3 * l
             assert_bits(want[qnames[i]], yq, "L%d DQL of %s x_q (unfused) vs oracle" % (l, src))
             assert_bits(want[qnames[i + 1]], np.asarray(ys, np.float32), "L%d DQL of %s scale vs oracle" % (l, src))
             assert int(want[qnames[i + 2]]) == int(yz)
+    fused = sorted([t[k] for k in ("h", "ctx") for t in names])
+    n_fused = 2 * L
 
     # as benched: only the final output
     ex = GpuGraphExecutor()
@@ -181,10 +190,10 @@ def test_full_size_encoder_as_benched():
     xin = x.clone()
     ex.capture({"x": xin}, [out])
     planned, launches = ex.quantized_outputs()
-    assert sorted(planned) == sorted([t["h"] for t in names] + [t["ctx"] for t in names])
+    assert sorted(planned) == fused
     # capture runs the plan twice on the host (the warm-up run, then the recorded one): every
-    # layer's FFN-up and attention launches took the fused form both times
-    assert launches == 2 * 2 * L, "%d fused launches for %d layers" % (launches, L)
+    # planned head launch took the fused form both times
+    assert launches == 2 * n_fused, "%d fused launches for %d layers" % (launches, L)
     for rep in range(2):
         ex.replay()
         got = ex.outputs([out])[out].cpu().numpy()
@@ -197,7 +206,7 @@ def test_full_size_encoder_as_benched():
     graphs.encoder_graph(ex2, layers=L, heads=H)
     ex2.capture({"x": xin}, [out] + qnames)
     assert ex2.plan()[0] == ex.plan()[0]
-    assert ex2.quantized_outputs() == (planned, 2 * 2 * L)
+    assert ex2.quantized_outputs() == (planned, 2 * n_fused)
     for rep in range(2):
         ex2.replay()
         got = {k: v.cpu().numpy() for k, v in ex2.outputs([out] + qnames).items()}
