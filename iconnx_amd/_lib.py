@@ -12,6 +12,9 @@ LIB_PATH = os.path.join(HERE, "libiconnx_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "iconnx_hip.h")
 
 ICX_I8, ICX_U8, ICX_I32, ICX_F32, ICX_I64 = 0, 1, 2, 3, 4
+# status codes (include/iconnx_hip.h)
+ICX_OK, ICX_ERR_INVALID_ARG, ICX_ERR_SHAPE, ICX_ERR_DTYPE, ICX_ERR_WORKSPACE, ICX_ERR_HIP = 0, 1, 2, 3, 4, 5
+ICX_ERR_UNSUPPORTED, ICX_ERR_KERNEL = 6, 7
 OP_ADD, OP_SUB, OP_MUL, OP_DIV = 0, 1, 2, 3
 OP_ERF, OP_SAVE, OP_MUL_SAVED = 4, 5, 6
 BCAST_SCALAR, BCAST_COL, BCAST_ROW, BCAST_FULL = 0, 1, 2, 3
@@ -89,6 +92,9 @@ SIGNATURES = {
     "icx_graph_add_initializer": ([P, C, I, I, P, P], I),
     "icx_graph_add_node": ([P, C, C, I, CP, I, CP, I, CP, P], I),
     "icx_graph_add_output": ([P, C], I),
+    "icx_exchange_buffer_size": ([], ctypes.c_size_t),
+    "icx_dynamic_quantize_linear_exchange": ([P, P, ctypes.c_size_t, P, P, P, P], I),
+    "icx_exchange_status": ([P, P], I),
     "icx_graph_set_option": ([P, C, ctypes.c_int64], I),
     "icx_graph_set_node_attr_float": ([P, C, C, ctypes.c_double], I),
     "icx_graph_set_node_attr_ints": ([P, C, C, I, P], I),

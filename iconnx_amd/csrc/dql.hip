@@ -10,13 +10,12 @@
 //   Block b of both launches runs on the same XCD (b mod 8) and reads the same bytes, so
 //   launch 2 re-reads x from that XCD's L2 (small tensors) or the Infinity Cache.
 //
-// The graph executor also has a single-launch form for small inputs (icx::dql_exchange, flat
-// mode, at most kExchangeMaxBlocks blocks): every block keeps its 1024 elements of x in
-// registers, the blocks trade their (min, max) pairs through the tagged-slot exchange of
-// qexchange.hpp, and each block quantizes from its registers.  Measured on MI355X (kernel
-// durations): 7.1 us against 3.2 + 4.9 us for the two launches at 98304 elements, but 9.2
-// against 8.3 us at 393216 and 13.0 against 10.6 us at 3.1M — the exchange's agent-scope
-// round trips cost ~4 us, which only beats a second launch while the pass itself is short.
+// A single-launch form (icx::dql_exchange, flat mode, no row sums; the graph executor's DQLs
+// and icx_dynamic_quantize_linear_exchange): every block keeps 1, 2 or 4 float4 per lane of
+// x in registers (up to 1024 resident blocks, 4 Mi elements), the blocks trade their
+// (min, max) pairs through the range exchange of qexchange.hpp, and each block quantizes
+// from its registers.  Kernel durations on MI355X: 9.1 us against 4.2 + 6.4 us for the two
+// launches at 3.1 M elements, 8.3 against 3.3 + 4.8 us at 1 M, and one launch boundary less.
 //
 // Semantics and per-element rounding: dql_core.hpp (DynamicQuantizeLinear::forward,
 // src/operators/dynamic_quantize_linear.rs:32-112).
@@ -260,36 +259,80 @@ dql_quantize_rows_kernel(const float* __restrict__ x, size_t rows, size_t row_le
     }
 }
 
-// Single launch, flat mode: block b holds the float4s [256 b, 256 b + 256) of x in registers
-// (one per lane), the last block also the n % 4 scalar tail.  The block's (min, max) goes
-// through the exchange; once every block's pair is in, each block quantizes its registers
-// and writes y.  A block whose wait ran out writes its part of y as 0 and counts itself in
-// the exchange buffer's error word (block 0's, which every block then shares, also makes the
-// scale NaN).  `poison` is 0 but for the fault test hook, which makes block 0's wait expect a
-// tag no block publishes.
-constexpr int kExchangeMaxBlocks = 128;  // inputs up to 128 * 1024 (+ 3) elements
-
+// Single launch, flat mode: block b holds the float4s [256 U b, 256 U (b + 1)) of x in
+// registers (U per lane, lane t the float4s 256 U b + 256 u + t), the last block also the
+// n % 4 scalar tail.  The block's (min, max) goes through the exchange; once every block's
+// pair is in, each block quantizes its registers and writes y.  A block whose wait ran out
+// writes its part of y as 0 and counts itself in the exchange buffer's error word (block
+// 0's, which every block then shares, also makes the scale NaN).  `poison` is 0 but for the
+// fault test hook, which makes block 0's wait expect a tag no block publishes.
+template <int U>
 __global__ void __launch_bounds__(kThreads)
 dql_exchange_kernel(const float* __restrict__ x, size_t n4, int tail, uint8_t* __restrict__ y,
                     float* __restrict__ y_scale, uint8_t* __restrict__ y_zp, unsigned* sync,
                     unsigned poison, unsigned long long wait) {
-    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
-    const float4 v = i < n4 ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const size_t i0 = (size_t)blockIdx.x * kThreads * U + threadIdx.x;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const size_t i = i0 + (size_t)u * kThreads;
+        v[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);  // 0.0 never moves the range
+    }
     const bool has_tail = blockIdx.x == gridDim.x - 1 && (int)threadIdx.x < tail;
-    const float xt = has_tail ? x[n4 * 4 + threadIdx.x] : 0.0f;  // 0.0 never moves the range
+    const float xt = has_tail ? x[n4 * 4 + threadIdx.x] : 0.0f;
     __shared__ unsigned s_tag;
     if (threadIdx.x == 0) s_tag = icx::qx::read_tag(sync);
     float mn = 0.0f, mx = 0.0f;
-    acc4(v, mn, mx);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc4(v[u], mn, mx);
     acc_minmax(xt, mn, mx);
     block_minmax<kThreads>(mn, mx);  // (its barrier also shares s_tag)
     const unsigned tag = s_tag;
     if (threadIdx.x == 0) icx::qx::publish(sync, tag, mn, mx);
     bool ok;
     const DqlParams p = icx::qx::gather<kThreads>(sync, tag, tag ^ poison, wait, ok);
-    if (i < n4) reinterpret_cast<uint32_t*>(y)[i] = ok ? quant4(v, p) : 0u;
+    uint32_t* y4 = reinterpret_cast<uint32_t*>(y);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const size_t i = i0 + (size_t)u * kThreads;
+        if (i < n4) y4[i] = ok ? quant4(v[u], p) : 0u;
+    }
     if (has_tail) y[n4 * 4 + threadIdx.x] = ok ? (uint8_t)quant1(xt, p) : (uint8_t)0;
     if (threadIdx.x == 0) icx::qx::finish(sync, ok, p, y_scale, y_zp);
+}
+
+// Launch with U float4 per lane if the grid fits the exchange and is resident at once
+// (occupancy per CU computed once per device): *launched tells whether it did; the return
+// value is an ICX status.
+template <int U>
+int try_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                 unsigned* sync, bool* launched) {
+    *launched = false;
+    const size_t n4 = n / 4;
+    const size_t G = icx::cdiv(std::max<size_t>(n4, 1), (size_t)kThreads * U);
+    if (G > (size_t)icx::kQoutMaxBlocks) return ICX_OK;
+    static int per_cu[64] = {0};
+    int d = 0;
+    ICX_HIP_CHECK(hipGetDevice(&d));
+    if (d < 0 || d >= 64) return ICX_OK;
+    if (!per_cu[d]) {
+        int nb = 0;
+        ICX_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, dql_exchange_kernel<U>, kThreads, 0));
+        per_cu[d] = nb > 0 ? nb : -1;
+    }
+    if (per_cu[d] < 0 || G > (size_t)per_cu[d] * icx::num_cus()) return ICX_OK;
+    unsigned long long wait = icx::wall_ticks(icx::kExchangeWaitUs);
+    unsigned poison = 0;
+    if (const int f = icx::qout_fault_spin()) {  // test hook
+        wait = icx::wall_ticks((unsigned)f);
+        poison = 0x80000000u;
+    }
+    hipLaunchKernelGGL(dql_exchange_kernel<U>, dim3((unsigned)G), dim3(kThreads), 0, s, x, n4, (int)(n % 4), y,
+                       y_scale, y_zp, sync, poison, wait);
+    ICX_LAUNCH_CHECK("dql_exchange_kernel");
+    *launched = true;
+    return ICX_OK;
 }
 
 }  // namespace
@@ -300,33 +343,49 @@ int icx::dql_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float
         ICX_FAIL(ICX_ERR_INVALID_ARG, "DQL exchange: null pointer");
     if (n == 0 || !icx::aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 3u) != 0)
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: empty or unaligned operands");
-    const size_t n4 = n / 4;
-    const size_t G = icx::cdiv(std::max<size_t>(n4, 1), (size_t)kThreads);
-    if (G > (size_t)kExchangeMaxBlocks)
-        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: %zu elements need %zu blocks, more than %d", n, G,
-                 kExchangeMaxBlocks);
-    static int per_cu[64] = {0};
-    int d = 0;
-    ICX_HIP_CHECK(hipGetDevice(&d));
-    if (d < 0 || d >= 64) ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: device index %d", d);
-    if (!per_cu[d]) {
-        int nb = 0;
-        ICX_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, dql_exchange_kernel, kThreads, 0));
-        per_cu[d] = nb > 0 ? nb : -1;
-    }
-    if (per_cu[d] < 0 || G > (size_t)per_cu[d] * icx::num_cus())
-        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: %zu blocks exceed the %d resident ones", G,
-                 per_cu[d] * icx::num_cus());
-    unsigned long long wait = icx::wall_ticks(icx::kExchangeWaitUs);
-    unsigned poison = 0;
-    if (const int f = icx::qout_fault_spin()) {  // test hook
-        wait = icx::wall_ticks((unsigned)f);
-        poison = 0x80000000u;
-    }
-    hipLaunchKernelGGL(dql_exchange_kernel, dim3((unsigned)G), dim3(kThreads), 0, s, x, n4, (int)(n % 4), y,
-                       y_scale, y_zp, sync, poison, wait);
-    ICX_LAUNCH_CHECK("dql_exchange_kernel");
+    // the fewest float4 per lane whose grid fits: more blocks, more loads in flight
+    bool done = false;
+    int rc = try_exchange<1>(s, x, n, y, y_scale, y_zp, sync, &done);
+    if (!rc && !done) rc = try_exchange<2>(s, x, n, y, y_scale, y_zp, sync, &done);
+    if (!rc && !done) rc = try_exchange<4>(s, x, n, y, y_scale, y_zp, sync, &done);
+    if (rc) return rc;
+    if (!done)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL exchange: %zu elements need more than %d resident blocks of %d", n,
+                 icx::kQoutMaxBlocks, kThreads * 16);
     return ICX_OK;
+}
+
+int icx::exchange_status(hipStream_t s, unsigned* sync) {
+    if (!sync) ICX_FAIL(ICX_ERR_INVALID_ARG, "exchange status: null buffer");
+    unsigned* word = sync + icx::kQoutErrWord;
+    unsigned failed = 0;
+    ICX_HIP_CHECK(hipMemcpyAsync(&failed, word, sizeof failed, hipMemcpyDeviceToHost, s));
+    ICX_HIP_CHECK(hipStreamSynchronize(s));
+    if (failed) {
+        ICX_HIP_CHECK(hipMemsetAsync(word, 0, sizeof failed, s));
+        ICX_HIP_CHECK(hipStreamSynchronize(s));
+        ICX_FAIL(ICX_ERR_KERNEL,
+                 "DynamicQuantizeLinear range exchange: %u failure record(s) since the last status check — a "
+                 "launch that quantizes its own output (quantized-output GEMM or attention, single-launch DQL) had "
+                 "blocks whose wait for the other blocks' ranges ran out (they were not all resident, e.g. other "
+                 "work held CUs); its quantized output is invalid (y = 0, scale = NaN)",
+                 failed);
+    }
+    return ICX_OK;
+}
+
+extern "C" size_t icx_exchange_buffer_size(void) { return icx::kQoutSyncBytes; }
+
+extern "C" int icx_dynamic_quantize_linear_exchange(icx_stream_t stream, const float* x, size_t n, uint8_t* y,
+                                                    float* y_scale, uint8_t* y_zp, void* sync) {
+    icx::clear_error();
+    return icx::dql_exchange(reinterpret_cast<hipStream_t>(stream), x, n, y, y_scale, y_zp,
+                             static_cast<unsigned*>(sync));
+}
+
+extern "C" int icx_exchange_status(icx_stream_t stream, void* sync) {
+    icx::clear_error();
+    return icx::exchange_status(reinterpret_cast<hipStream_t>(stream), static_cast<unsigned*>(sync));
 }
 
 extern "C" size_t icx_dql_workspace_size(size_t) { return sizeof(float2) * kMaxBlocks; }

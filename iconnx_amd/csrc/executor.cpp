@@ -2774,22 +2774,7 @@ extern "C" int icx_graph_status(icx_graph* g, icx_stream_t stream) {
         ICX_HIP_CHECK(hipStreamSynchronize(s));
         return ICX_OK;
     }
-    // the exchange buffer's sticky word: launches whose range exchange gave up
-    unsigned* word = g->qsync + icx::kQoutErrWord;
-    unsigned failed = 0;
-    ICX_HIP_CHECK(hipMemcpyAsync(&failed, word, sizeof failed, hipMemcpyDeviceToHost, s));
-    ICX_HIP_CHECK(hipStreamSynchronize(s));
-    if (failed) {
-        ICX_HIP_CHECK(hipMemsetAsync(word, 0, sizeof failed, s));
-        ICX_HIP_CHECK(hipStreamSynchronize(s));
-        ICX_FAIL(ICX_ERR_KERNEL,
-                 "DynamicQuantizeLinear range exchange: %u failure record(s) since the last status check — a "
-                 "launch that quantizes its own output (quantized-output GEMM or attention, single-launch DQL) had "
-                 "blocks whose wait for the other blocks' ranges ran out (they were not all resident, e.g. other "
-                 "work held CUs); its quantized output is invalid (y = 0, scale = NaN)",
-                 failed);
-    }
-    return ICX_OK;
+    return icx::exchange_status(s, g->qsync);
 }
 
 extern "C" int icx_graph_get_output(icx_graph* g, const char* name, int* dtype, int* rank,

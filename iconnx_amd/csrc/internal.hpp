@@ -79,6 +79,9 @@ int qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int
 // qlinear_dql's).  Needs 16-byte aligned x, 4-byte aligned y and n <= 128 * 1024 + 3 (it is
 // slower than the two launches beyond that); otherwise ICX_ERR_UNSUPPORTED, having launched
 // nothing.  y, y_scale, y_zp equal icx_dynamic_quantize_linear's bit for bit.
+// Synchronise `s`, then read and clear the exchange buffer's sticky error word:
+// ICX_ERR_KERNEL (with a message) if any launch since the last check gave up waiting.
+int exchange_status(hipStream_t s, unsigned* sync);
 int dql_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
                  unsigned* sync);
 

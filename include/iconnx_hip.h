@@ -95,6 +95,24 @@ int icx_dynamic_quantize_linear(icx_stream_t stream, const float* x, size_t n, u
                                 float* y_scale, uint8_t* y_zp, int32_t* opt_rowsum,
                                 size_t row_len, void* ws, size_t ws_bytes);
 
+/* The same op as one launch (no counterpart in the reference, whose op runs as its two
+ * kernels; for callers that keep one buffer per stream): every block keeps its slice of x in
+ * registers and the blocks trade their (min, max) through `sync`, a buffer of
+ * icx_exchange_buffer_size() bytes that the caller zeroes once before its first use and
+ * keeps for later calls (it carries a launch number from call to call; calls sharing a
+ * buffer must not overlap).  Same outputs, bit for bit, as icx_dynamic_quantize_linear
+ * without row sums.  Up to 4 Mi elements (1024 resident blocks of 256 lanes with 4 float4
+ * each), x 16-byte and y 4-byte aligned: otherwise ICX_ERR_UNSUPPORTED with nothing
+ * launched.  All blocks must run at once: if other work keeps some from being scheduled,
+ * the waiting blocks give up after a bounded time, write y as 0 and the scale as NaN, and
+ * the next icx_exchange_status on the buffer returns ICX_ERR_KERNEL. */
+size_t icx_exchange_buffer_size(void);
+int icx_dynamic_quantize_linear_exchange(icx_stream_t stream, const float* x, size_t n, uint8_t* y,
+                                         float* y_scale, uint8_t* y_zp, void* sync);
+/* Synchronise the stream, then report (ICX_ERR_KERNEL) and clear the failures recorded in
+ * an exchange buffer since the last check. */
+int icx_exchange_status(icx_stream_t stream, void* sync);
+
 /* ---- weight packing (once per weight; part of initializer upload in the reference,
  * src/ir/lowering.rs:292-297) -----------------------------------------------------------
  * B [K,N] row-major (i8 or u8) -> packed [N,K] i8 (u8 shifted by -128) + colsum[N] of the

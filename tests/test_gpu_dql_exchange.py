@@ -1,14 +1,15 @@
-"""GPU parity of the single-launch DynamicQuantizeLinear the graph executor runs for a small
-input (up to 128 blocks of 1024 elements, e.g. a batch-1 sequence of 128 x 768) when no
-producer left the input's range and no GEMM reads row sums of its output: the blocks keep
-x in registers and trade their (min, max) through the graph's exchange buffer.
+"""GPU parity of the single-launch DynamicQuantizeLinear the graph executor runs for an input
+of up to 1024 resident blocks of 256 lanes holding 1, 2 or 4 float4 each (4 Mi elements,
+e.g. the encoder's [32, 128, 768] activation) when no producer left the input's range and
+no GEMM reads row sums of its output: the blocks keep x in registers and trade their
+(min, max) through the graph's exchange buffer.
 
 The bar is the two-launch path's: y, scale and zero point bit-exact against the oracle
 (DynamicQuantizeLinear::forward, src/operators/dynamic_quantize_linear.rs:32-112; the
 reference's own test is tests/dynamic_quantize_linear_test.rs:28-136), over sizes that
-take one to 128 blocks, the scalar tail, the edge values the two-launch tests cover, inputs
-past the limit (two-launch fallback), captured replays, and the failure path of the
-exchange.
+take one to 1024 blocks at each of the three widths, the scalar tail, the edge values the
+two-launch tests cover, inputs past the limit (two-launch fallback), captured replays, and
+the failure path of the exchange.
 """
 import numpy as np
 import pytest
@@ -37,9 +38,11 @@ def check_oracle(got, x, what):
     assert int(got["zp"]) == int(ezp), what
 
 
-# one float4 per lane, 256 lanes per block: 1 to 128 blocks, with and without a scalar tail
+# 256 lanes per block holding 1 float4 each up to 1024 blocks (1 Mi elements), then 2, then 4
+# (4 Mi elements); with and without a scalar tail, and each width's first and last grid
 @pytest.mark.parametrize("n", [1, 3, 4, 5, 1000, 1024, 1025, 65536 + 7, 128 * 768, 128 * 1024,
-                               128 * 1024 + 3])
+                               128 * 1024 + 3, 128 * 1024 + 4, (1 << 20) + 3, (1 << 20) + 4,
+                               (2 << 20) + 3, (2 << 20) + 5, 4096 * 768, (4 << 20) + 3])
 def test_single_launch_matches_oracle(n):
     x = (np.random.default_rng(n).standard_normal(n) * 3.0).astype(np.float32)
     ex = dql_graph()
@@ -94,16 +97,16 @@ def test_consecutive_runs_of_different_sizes():
     rest for the next (the launch number advances, the counter is back at 0)."""
     ex = dql_graph()
     rng = np.random.default_rng(5)
-    for i, n in enumerate((128 * 768, 1000, 128 * 1024 + 3, 3, 128 * 768)):
+    for i, n in enumerate((128 * 768, 1000, 4096 * 768, 128 * 1024 + 3, 3, (2 << 20) + 5, 128 * 768)):
         x = (rng.standard_normal(n) * (1.0 + i)).astype(np.float32)
         check_oracle(ex.run({"x": x}, ["y", "s", "zp"]), x, "run %d (n=%d)" % (i, n))
-    assert ex.single_launch_dqls() == 5
+    assert ex.single_launch_dqls() == 7
 
 
-@pytest.mark.parametrize("n", [128 * 1024 + 4, 4096 * 768])
+@pytest.mark.parametrize("n", [(4 << 20) + 4, 24576 * 1024])
 def test_larger_inputs_take_two_launches(n):
-    """Past 128 blocks (one element more than the limit; cfg2's activation) the DQL runs as
-    two launches, which are faster there; the results are the same."""
+    """Past 1024 blocks of 4 float4 per lane (one float4 more than the limit; cfg4's
+    activation) the DQL runs as two launches; the results are the same."""
     x = (np.random.default_rng(n).standard_normal(n) * 3.0).astype(np.float32)
     ex = dql_graph()
     got = ex.run({"x": x}, ["y", "s", "zp"])
@@ -151,3 +154,51 @@ def test_exchange_that_gives_up_is_an_error_status():
     ex.check_status()  # cleared
     check_oracle(ex.run({"x": x}, ["y", "s", "zp"]), x, "normal run after the failure")
     assert ex.single_launch_dqls() == 2
+
+
+def test_c_abi_single_launch_op():
+    """icx_dynamic_quantize_linear_exchange on one zeroed buffer kept across calls (what a
+    per-op caller does): calls of six sizes in a row, each bit-exact against the oracle and
+    checked clean by icx_exchange_status; an input past the limit is ICX_ERR_UNSUPPORTED
+    with nothing launched; with the test hook every block's wait gives up, the status check
+    reports ICX_ERR_KERNEL once (y = 0, scale NaN), and the next call is correct again."""
+    import ctypes
+
+    from iconnx_amd._lib import ICX_ERR_KERNEL, ICX_ERR_UNSUPPORTED
+
+    L = lib()
+    P = ctypes.c_void_p
+    sync = torch.zeros(L.icx_exchange_buffer_size(), dtype=torch.uint8, device="cuda")
+    stream = P(torch.cuda.current_stream().cuda_stream)
+
+    def call(x):
+        xd = torch.from_numpy(x).cuda()
+        y = torch.empty(x.size, dtype=torch.uint8, device="cuda")
+        s = torch.empty((), dtype=torch.float32, device="cuda")
+        zp = torch.empty((), dtype=torch.uint8, device="cuda")
+        rc = L.icx_dynamic_quantize_linear_exchange(stream, P(xd.data_ptr()), x.size, P(y.data_ptr()),
+                                                    P(s.data_ptr()), P(zp.data_ptr()), P(sync.data_ptr()))
+        return rc, {"y": y, "s": s, "zp": zp}
+
+    rng = np.random.default_rng(21)
+    for n in (3, 1000, 128 * 1024 + 3, (1 << 20) + 4, 4096 * 768, 4 << 20):
+        x = (rng.standard_normal(n) * 2.5).astype(np.float32)
+        rc, out = call(x)
+        assert rc == 0, L.icx_last_error()
+        assert L.icx_exchange_status(stream, P(sync.data_ptr())) == 0
+        check_oracle({k: v.cpu().numpy() for k, v in out.items()}, x, "C ABI n=%d" % n)
+    rc, _ = call(np.ones((4 << 20) + 4, np.float32))
+    assert rc == ICX_ERR_UNSUPPORTED
+    x = (rng.standard_normal(4096 * 768)).astype(np.float32)
+    L.icx_debug_qout_fault(64)
+    try:
+        rc, bad = call(x)
+        assert rc == 0
+        assert L.icx_exchange_status(stream, P(sync.data_ptr())) == ICX_ERR_KERNEL
+    finally:
+        L.icx_debug_qout_fault(0)
+    assert np.isnan(bad["s"].cpu().numpy()) and not bad["y"].cpu().numpy().any()
+    assert L.icx_exchange_status(stream, P(sync.data_ptr())) == 0  # cleared by the check
+    rc, out = call(x)
+    assert rc == 0 and L.icx_exchange_status(stream, P(sync.data_ptr())) == 0
+    check_oracle({k: v.cpu().numpy() for k, v in out.items()}, x, "C ABI after the give-up")
