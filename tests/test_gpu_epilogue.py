@@ -249,7 +249,7 @@ def test_ffn_down_shape_fused_epilogue():
         assert_f32_equal(y[r0:r1], ref["y"][r0:r1], "rows %d:%d" % (r0, r1))
 
 
-def test_division_fast_path_edge_values():
+def test_division_edge_values():
     """The GEMM epilogues divide by a column operand d with the correctly rounded IEEE
     division (__fdiv_rn), whatever the operands.  cfg2's shape (one 256x192 tile per CU) with
     a Mul before the Div that makes the numerators of chosen columns exactly +-0, subnormal,
