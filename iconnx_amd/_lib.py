@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libiconnx_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "iconnx_hip.h")
 
-ICX_I8, ICX_U8, ICX_I32, ICX_F32, ICX_I64 = 0, 1, 2, 3, 4
+ICX_I8, ICX_U8, ICX_I32, ICX_F32, ICX_I64, ICX_BOOL = 0, 1, 2, 3, 4, 5
 # status codes (include/iconnx_hip.h)
 ICX_OK, ICX_ERR_INVALID_ARG, ICX_ERR_SHAPE, ICX_ERR_DTYPE, ICX_ERR_WORKSPACE, ICX_ERR_HIP = 0, 1, 2, 3, 4, 5
 ICX_ERR_UNSUPPORTED, ICX_ERR_KERNEL = 6, 7

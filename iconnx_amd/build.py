@@ -27,7 +27,7 @@ HIP_FLAGS = [
 ]
 # host-only C++ (the graph executor) goes through hipcc for the HIP runtime headers
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall"]
-SOURCES = ["dql.hip", "gemm.hip", "elementwise.hip", "encoder.hip", "executor.cpp", "memory.cpp"]
+SOURCES = ["dql.hip", "gemm.hip", "elementwise.hip", "encoder.hip", "layout.hip", "executor.cpp", "memory.cpp"]
 
 
 def _compile(src):

@@ -14,13 +14,16 @@
 //              DecomposedLayerNorm  [Add(a, b) ->] ReduceMean -> Sub -> Pow(2) -> ReduceMean
 //                               -> Add(eps) -> Sqrt -> Div [-> Mul(gamma)] [-> Add(beta)]
 //              MulAdd / AddMul / SubMul / DivMul / ElementwiseChain / Gelu
-//            weight zero-point folding; Reshape outputs alias their input; last use of
-//            every tensor
+//            weight zero-point folding; Reshape / Unsqueeze / Squeeze / Identity outputs
+//            alias their input; last use of every tensor
 //   compile: upload initializers, pack MatMulInteger weights once (icx_pack_weight)
 //   run:     input shape guard, then every planned op on the caller's stream; intermediate
 //            tensors come from a size-class pool on hipMalloc and return to it at their
 //            last use (stream order makes the reuse safe).  A fused head whose runtime
 //            shapes fall outside its kernel runs its member nodes one by one instead.
+//            Shape results and the integer arithmetic on them (an exported model's reshape
+//            targets, Slice bounds, Expand shapes) are computed on the host and uploaded
+//            only where a device op or the caller reads them.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -45,7 +48,8 @@ using icx::set_error;
 size_t dtype_size(int dt) {
     switch (dt) {
         case ICX_I8:
-        case ICX_U8: return 1;
+        case ICX_U8:
+        case ICX_BOOL: return 1;
         case ICX_I64: return 8;
         default: return 4;
     }
@@ -58,6 +62,7 @@ const char* dtype_name(int dt) {
         case ICX_I32: return "Int32";
         case ICX_F32: return "Float32";
         case ICX_I64: return "Int64";
+        case ICX_BOOL: return "Bool";
         default: return "?";
     }
 }
@@ -268,6 +273,7 @@ struct icx_graph {
     std::map<std::string, PackedW> packed;         // packed MatMulInteger weights
     std::map<std::string, BoundInput> bound;       // inputs for the next run
     std::map<std::string, DevTensor> values;       // tensors of the current / last run
+    std::map<std::string, HostTensor> hv;          // tensors of this run known on the host
     std::map<std::string, std::string> rowsum_of;  // DQL y -> its row-sum tensor
     std::map<std::string, std::pair<std::string, int>> range_of;  // DQL x -> (partials tensor, count)
     std::set<std::string> dql_done;  // DQL outputs already written by their producer's GEMM
@@ -318,6 +324,7 @@ struct icx_graph {
         for (auto& kv : values)
             if (kv.second.pooled) pool.put(kv.second.ptr, kv.second.cls);
         values.clear();
+        hv.clear();
         rowsum_of.clear();
         range_of.clear();
         dql_done.clear();
@@ -350,6 +357,11 @@ struct GraphIndex {
         }
     }
 };
+
+// Ops whose output, for a device tensor, names the input's buffer with another shape.
+bool is_view(const std::string& op) {
+    return op == "Reshape" || op == "Unsqueeze" || op == "Squeeze" || op == "Identity";
+}
 
 int op_code(const std::string& op) {
     if (op == "Add") return ICX_OP_ADD;
@@ -439,7 +451,7 @@ class Planner {
                     heads_out.count(op.node.in[0]))
                     g_.range_wanted.insert(op.node.in[0]);
         }
-        // last readers; a Reshape output aliases its input's buffer, so uses of the alias
+        // last readers; a view's output (Reshape, Unsqueeze, ...) aliases its input's buffer, so uses of the alias
         // extend the buffer's life, and a live alias keeps it until the next run
         g_.last_use.clear();
         std::map<std::string, std::string> root;
@@ -463,10 +475,10 @@ class Planner {
                     g_.last_use[u] = i;
                     g_.last_use[root_of(u)] = i;
                 }
-            if (op.kind == Kind::Regular && op.node.op == "Reshape" && !op.node.out.empty())
+            if (op.kind == Kind::Regular && is_view(op.node.op) && !op.node.out.empty() && !op.node.in.empty())
                 root[op.node.out[0]] = root_of(op.node.in[0]);
             for (auto& m : op.sub)  // a fused head run node by node creates the same aliases
-                if (m.op == "Reshape" && !m.out.empty()) root[m.out[0]] = root_of(m.in[0]);
+                if (is_view(m.op) && !m.out.empty()) root[m.out[0]] = root_of(m.in[0]);
         }
         g_.keep.clear();
         for (auto& o : g_.live_outputs) {
@@ -1242,6 +1254,146 @@ int reshape_target(const std::vector<int64_t>& in, const std::vector<int64_t>& s
     return ICX_OK;
 }
 
+// ---- tensors known on the host ------------------------------------------------------------
+// An exported encoder computes its reshape targets, Slice bounds and Expand shapes from Shape
+// results: small integer tensors.  The reference reads such Int64 tensors on the host and
+// caches them (cache_i64 / get_or_fetch_i64, src/cuda/executor/layout.rs:136-146, 345-445),
+// while each op of the shape arithmetic still runs as a GPU kernel.  Here an op whose inputs
+// are all known on the host (computed on the host this run, a small initializer, or a small
+// input bound from host memory) and whose output is small is computed on the host, and its
+// output reaches device memory only if a device op or the caller reads it.
+constexpr int64_t kHostFoldMax = 1024;  // elements
+
+std::vector<int64_t> dense_strides(const std::vector<int64_t>& sh) {
+    std::vector<int64_t> st(sh.size());
+    int64_t s = 1;
+    for (size_t i = sh.size(); i-- > 0;) {
+        st[i] = s;
+        s *= sh[i];
+    }
+    return st;
+}
+
+// Element strides with which a dense tensor of shape `in` is read over `out` (numpy rules,
+// aligned at the right): 0 on a broadcast dimension.
+std::vector<int64_t> bcast_strides(const std::vector<int64_t>& in, const std::vector<int64_t>& out) {
+    std::vector<int64_t> st(out.size(), 0);
+    const std::vector<int64_t> ds = dense_strides(in);
+    const size_t off = out.size() - in.size();
+    for (size_t i = 0; i < in.size(); ++i) st[off + i] = in[i] == 1 ? 0 : ds[i];
+    return st;
+}
+
+// f(e, off) for every flat index e of `dims` in row-major order, off[k] = the element offset
+// of operand k (base[k] + sum of index * st[k]).
+template <typename F>
+void for_each_offset(const std::vector<int64_t>& dims, const std::vector<std::vector<int64_t>>& st,
+                     const std::vector<int64_t>& base, F f) {
+    const int64_t total = numel(dims);
+    const size_t r = dims.size();
+    std::vector<int64_t> idx(r, 0), off = base;
+    for (int64_t e = 0; e < total; ++e) {
+        f(e, off);
+        for (size_t d = r; d-- > 0;) {
+            ++idx[d];
+            for (size_t k = 0; k < st.size(); ++k) off[k] += st[k][d];
+            if (idx[d] < dims[d]) break;
+            for (size_t k = 0; k < st.size(); ++k) off[k] -= st[k][d] * dims[d];
+            idx[d] = 0;
+        }
+    }
+}
+
+bool int_dtype(int dt) { return dt == ICX_I64 || dt == ICX_I32 || dt == ICX_I8 || dt == ICX_U8 || dt == ICX_BOOL; }
+
+int64_t int_at(const HostTensor& t, int64_t i) {
+    const uint8_t* p = t.data.data();
+    switch (t.dtype) {
+        case ICX_I64: return reinterpret_cast<const int64_t*>(p)[i];
+        case ICX_I32: return reinterpret_cast<const int32_t*>(p)[i];
+        case ICX_I8: return reinterpret_cast<const int8_t*>(p)[i];
+        default: return p[i];  // UInt8, Bool
+    }
+}
+
+void put_int(HostTensor& t, int64_t i, int64_t v) {
+    uint8_t* p = t.data.data();
+    switch (t.dtype) {
+        case ICX_I64: reinterpret_cast<int64_t*>(p)[i] = v; break;
+        case ICX_I32: reinterpret_cast<int32_t*>(p)[i] = (int32_t)v; break;
+        case ICX_I8: reinterpret_cast<int8_t*>(p)[i] = (int8_t)v; break;
+        case ICX_BOOL: p[i] = v != 0; break;
+        default: p[i] = (uint8_t)v; break;
+    }
+}
+
+HostTensor host_tensor(int dtype, const std::vector<int64_t>& shape) {
+    HostTensor t;
+    t.dtype = dtype;
+    t.shape = shape;
+    t.data.assign((size_t)numel(shape) * dtype_size(dtype), 0);
+    return t;
+}
+
+// Slice parameters as the reference's GPU Slice normalises them (gpu_slice_nd,
+// src/cuda/ops/layout/mod.rs:2849-2935; starts / ends of different lengths broadcast or
+// truncate first, layout.rs:386-401; axes or steps of another length are ignored,
+// layout.rs:403-445): per dimension the first index, the step and the output length.
+int slice_params(const std::vector<int64_t>& shape, std::vector<int64_t> starts, std::vector<int64_t> ends,
+                 const std::vector<int64_t>* axes_in, const std::vector<int64_t>* steps_in,
+                 std::vector<int64_t>* first, std::vector<int64_t>* step, std::vector<int64_t>* len) {
+    if (starts.size() != ends.size()) {
+        if (starts.size() == 1 && ends.size() > 1) starts.assign(ends.size(), starts[0]);
+        else if (ends.size() == 1 && starts.size() > 1) ends.assign(starts.size(), ends[0]);
+        else {
+            const size_t n = std::min(starts.size(), ends.size());
+            starts.resize(n);
+            ends.resize(n);
+        }
+    }
+    const size_t ns = starts.size();
+    std::vector<int64_t> axes, steps(ns, 1);
+    if (axes_in && axes_in->size() == ns) axes = *axes_in;
+    else for (size_t i = 0; i < ns; ++i) axes.push_back((int64_t)i);
+    if (steps_in && steps_in->size() == ns) steps = *steps_in;
+    const int64_t nd = (int64_t)shape.size();
+    first->assign(nd, 0);
+    step->assign(nd, 1);
+    len->assign(shape.begin(), shape.end());
+    std::vector<int64_t> end(shape.begin(), shape.end());
+    for (size_t i = 0; i < ns; ++i) {
+        const int64_t ax = axes[i] < 0 ? nd + axes[i] : axes[i];
+        if (ax < 0 || ax >= nd) {
+            set_error("Slice: axis %lld out of bounds for ndim %lld", (long long)axes[i], (long long)nd);
+            return ICX_ERR_SHAPE;
+        }
+        if (steps[i] == 0) {
+            set_error("Slice: step cannot be 0");
+            return ICX_ERR_INVALID_ARG;
+        }
+        const int64_t dim = shape[ax];
+        int64_t s = starts[i] < 0 ? std::max<int64_t>(dim + starts[i], 0) : std::min(starts[i], dim);
+        int64_t e = ends[i] < 0 ? std::max<int64_t>(dim + ends[i], 0) : std::min(ends[i], dim);
+        if (steps[i] < 0) {
+            s = std::min(s, dim - 1);
+            e = std::max<int64_t>(e, -1);
+        } else {
+            s = std::max<int64_t>(s, 0);
+            e = std::max<int64_t>(e, 0);
+        }
+        (*first)[ax] = s;
+        (*step)[ax] = steps[i];
+        end[ax] = e;
+    }
+    for (int64_t d = 0; d < nd; ++d) {
+        const int64_t s = (*first)[d], e = end[d], st = (*step)[d];
+        // the reference's output length (layout/mod.rs:2931-2939)
+        const int64_t n = st > 0 ? (e - s + st - 1) / st : (s - e - st - 1) / (-st);
+        (*len)[d] = std::max<int64_t>(n, 0);
+    }
+    return ICX_OK;
+}
+
 class Runner {
    public:
     Runner(icx_graph& g, hipStream_t s) : g_(g), s_(s) {}
@@ -1334,6 +1486,13 @@ class Runner {
         if (t == "ReduceMean") return run_reduce_mean(n);
         if (t == "Pow") return run_pow(n);
         if (t == "Sqrt") return run_sqrt(n);
+        if (t == "Shape") return run_shape(n);
+        if (t == "Unsqueeze" || t == "Squeeze" || t == "Identity") return run_view(n);
+        if (t == "Concat") return run_concat(n);
+        if (t == "Slice") return run_slice(n);
+        if (t == "Expand") return run_expand(n);
+        if (t == "Equal") return run_equal(n);
+        if (t == "Where") return run_where(n);
         if (op_code(t) >= 0) return run_binary(n);
         set_error("op '%s' is not on the quantized-linear path", t.c_str());
         return ICX_ERR_UNSUPPORTED;
@@ -1349,8 +1508,118 @@ class Runner {
     int need(const std::string& name, const DevTensor** out, const char* who) const {
         *out = find(name);
         if (*out) return ICX_OK;
+        if (g_.hv.count(name)) return materialize(name, out);
         set_error("%s: input tensor '%s' is missing", who, name.c_str());
         return ICX_ERR_INVALID_ARG;
+    }
+    // A tensor computed on the host, uploaded for a device reader (through kernel arguments,
+    // so a captured run replays the copy); it stays a host value too.
+    int materialize(const std::string& name, const DevTensor** out) const {
+        const HostTensor& h = g_.hv.at(name);
+        DevTensor t;
+        t.dtype = h.dtype;
+        t.shape = h.shape;
+        t.bytes = h.data.size();
+        t.ptr = g_.pool.get(std::max<size_t>(t.bytes, 1), &t.cls);
+        if (!t.ptr) {
+            set_error("memory pool: hipMalloc of %zu bytes for '%s' failed", t.bytes, name.c_str());
+            return ICX_ERR_HIP;
+        }
+        t.pooled = true;
+        DevTensor& d = g_.values[name] = t;
+        *out = &d;
+        return icx::upload_bytes(s_, h.data.data(), h.data.size(), d.ptr);
+    }
+    // The host copy of `name` if it is known on the host without reading device memory.
+    const HostTensor* host_known(const std::string& name) const {
+        auto h = g_.hv.find(name);
+        if (h != g_.hv.end()) return &h->second;
+        auto it = g_.inits.find(name);
+        if (it != g_.inits.end()) return numel(it->second.shape) <= kHostFoldMax ? &it->second : nullptr;
+        auto b = g_.bound.find(name);
+        if (b != g_.bound.end() && !b->second.dev && numel(b->second.shape) <= kHostFoldMax) {
+            HostTensor t;
+            t.dtype = b->second.dtype;
+            t.shape = b->second.shape;
+            t.data = b->second.host;
+            return &(g_.hv[name] = std::move(t));
+        }
+        return nullptr;
+    }
+    // Integer values of `name` on the host (Float32 truncated, as the reference's Slice and
+    // ReduceMean read their parameters): a host-known tensor, else read from the device
+    // (synchronising the stream, as the reference's get_or_fetch_i64 does; refused while
+    // the stream is being captured) and kept for later readers.
+    int host_ints(const std::string& name, std::vector<int64_t>* v, const char* who) const {
+        const HostTensor* h = host_known(name);
+        if (!h) {
+            const DevTensor* d = find(name);
+            if (!d) {
+                set_error("%s: input tensor '%s' is missing", who, name.c_str());
+                return ICX_ERR_INVALID_ARG;
+            }
+            if (!int_dtype(d->dtype) && d->dtype != ICX_F32) {
+                set_error("%s: '%s' must be an integer tensor, got %s", who, name.c_str(), dtype_name(d->dtype));
+                return ICX_ERR_DTYPE;
+            }
+            if (numel(d->shape) > kHostFoldMax) {
+                set_error("%s: '%s' has %lld elements, too many to read on the host", who, name.c_str(),
+                          (long long)numel(d->shape));
+                return ICX_ERR_SHAPE;
+            }
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            ICX_HIP_CHECK(hipStreamIsCapturing(s_, &cs));
+            if (cs != hipStreamCaptureStatusNone) {
+                set_error("%s: '%s' would have to be read on the host while the run is captured", who, name.c_str());
+                return ICX_ERR_UNSUPPORTED;
+            }
+            HostTensor t;
+            t.dtype = d->dtype;
+            t.shape = d->shape;
+            t.data.resize(d->bytes);
+            if (d->bytes) {
+                ICX_HIP_CHECK(hipMemcpyAsync(t.data.data(), d->ptr, d->bytes, hipMemcpyDeviceToHost, s_));
+                ICX_HIP_CHECK(hipStreamSynchronize(s_));
+            }
+            h = &(g_.hv[name] = std::move(t));
+        }
+        v->resize((size_t)numel(h->shape));
+        for (size_t i = 0; i < v->size(); ++i)  // (Float32 as the reference's Slice / ReduceMean take it)
+            (*v)[i] = h->dtype == ICX_F32 ? (int64_t)reinterpret_cast<const float*>(h->data.data())[i]
+                                          : int_at(*h, (int64_t)i);
+        return ICX_OK;
+    }
+    // Shape and dtype of a tensor wherever it lives (no upload).
+    bool shape_of(const std::string& name, std::vector<int64_t>* sh, int* dt) const {
+        if (const DevTensor* d = find(name)) {
+            *sh = d->shape;
+            *dt = d->dtype;
+            return true;
+        }
+        auto h = g_.hv.find(name);
+        if (h == g_.hv.end()) return false;
+        *sh = h->second.shape;
+        *dt = h->second.dtype;
+        return true;
+    }
+    // Every non-empty input of the first n_inputs an integer or Bool tensor known on the
+    // host: the op is shape arithmetic and is computed on the host (Float32 tensors, the
+    // model's activations and constants, always take the device kernels).
+    bool all_host(const Node& n, size_t n_inputs, std::vector<const HostTensor*>* hs) const {
+        hs->assign(n_inputs, nullptr);
+        for (size_t i = 0; i < n_inputs && i < n.in.size(); ++i) {
+            if (n.in[i].empty()) continue;
+            (*hs)[i] = host_known(n.in[i]);
+            if (!(*hs)[i] || !int_dtype((*hs)[i]->dtype)) return false;
+        }
+        return true;
+    }
+    // (a host route returns kHostTooLarge, having done nothing, for an output of more than
+    // kHostFoldMax elements: the op then runs on the device)
+    static constexpr int kHostTooLarge = -1;
+    int set_host(const std::string& name, HostTensor t) const {
+        g_.hv[name] = std::move(t);
+        return ICX_OK;
     }
     int alloc(const std::string& name, int dtype, const std::vector<int64_t>& shape, DevTensor** out) {
         auto old = g_.values.find(name);
@@ -1784,12 +2053,23 @@ class Runner {
             set_error("Reshape requires 2 inputs, got %zu", n.in.size());
             return ICX_ERR_INVALID_ARG;
         }
-        const DevTensor* X;
-        int rc = need(n.in[0], &X, "Reshape");
+        std::vector<int64_t> xs, spec, tgt;
+        int xdt;
+        if (!shape_of(n.in[0], &xs, &xdt)) {
+            set_error("Reshape: input tensor '%s' is missing", n.in[0].c_str());
+            return ICX_ERR_INVALID_ARG;
+        }
+        int rc = host_ints(n.in[1], &spec, "Reshape");
+        if (!rc) rc = reshape_target(xs, spec, n.attr_or("allowzero", 0) != 0, &tgt);
         if (rc) return rc;
-        std::vector<int64_t> spec, tgt;
-        rc = shape_init(n.in[1], &spec);
-        if (!rc) rc = reshape_target(X->shape, spec, n.attr_or("allowzero", 0) != 0, &tgt);
+        const HostTensor* h = host_known(n.in[0]);
+        if (h && int_dtype(h->dtype)) {
+            HostTensor t = *h;
+            t.shape = tgt;
+            return set_host(n.out[0], std::move(t));
+        }
+        const DevTensor* X;
+        rc = need(n.in[0], &X, "Reshape");
         if (rc) return rc;
         DevTensor t = *X;
         t.shape = tgt;
@@ -1960,45 +2240,6 @@ class Runner {
                                    row_len, g_.ws, g_.ws_bytes, false);
     }
 
-    // Values of a small integer tensor known on the host: an Int64 (or, as the reference's
-    // ReduceMean also takes, Float32) initializer, or a graph input bound from host memory.
-    int host_ints(const std::string& name, std::vector<int64_t>* v, const char* who) const {
-        v->clear();
-        const uint8_t* data = nullptr;
-        int dt = -1;
-        int64_t cnt = 0;
-        auto it = g_.inits.find(name);
-        if (it != g_.inits.end()) {
-            data = it->second.data.data();
-            dt = it->second.dtype;
-            cnt = numel(it->second.shape);
-        } else {
-            auto b = g_.bound.find(name);
-            if (b != g_.bound.end() && !b->second.dev) {
-                data = b->second.host.data();
-                dt = b->second.dtype;
-                cnt = numel(b->second.shape);
-            }
-        }
-        if (dt != ICX_I64 && dt != ICX_F32) {
-            set_error("%s: '%s' must be an Int64 (or Float32) initializer or input bound from host memory", who,
-                      name.c_str());
-            return ICX_ERR_UNSUPPORTED;
-        }
-        for (int64_t i = 0; i < cnt; ++i) {
-            if (dt == ICX_I64) {
-                int64_t a;
-                std::memcpy(&a, data + 8 * i, 8);
-                v->push_back(a);
-            } else {
-                float f;
-                std::memcpy(&f, data + 4 * i, 4);
-                v->push_back((int64_t)f);
-            }
-        }
-        return ICX_OK;
-    }
-
     // ReduceMean (src/operators/reduce_mean.rs:19-105): axes from the second input (opset 18)
     // or the `axes` attribute (earlier opsets; the reference's CPU forward reads the input
     // only, its GPU dispatch always reduces the last axis, src/cuda/executor/reduction.rs:
@@ -2112,11 +2353,18 @@ class Runner {
         return icx_fused_chain_f32(s_, x, rows, cols, &ch, static_cast<float*>(Y->ptr));
     }
 
-    // Mul / Add / Sub / Div outside a chain: the output must have one operand's shape.
+    // Mul / Add / Sub / Div outside a chain: the chain kernel when the output has one
+    // operand's shape and the other broadcasts as a chain operand, else a general broadcast
+    // kernel; integer operands known on the host are shape arithmetic, done on the host.
     int run_binary(const Node& n) {
         if (n.in.size() != 2 || n.out.size() != 1) {
             set_error("%s: expected 2 inputs and 1 output", n.op.c_str());
             return ICX_ERR_INVALID_ARG;
+        }
+        std::vector<const HostTensor*> hs;
+        if (all_host(n, 2, &hs)) {
+            int rc = host_binary(n, *hs[0], *hs[1]);
+            if (rc != kHostTooLarge) return rc;
         }
         const DevTensor *A, *B;
         int rc = need(n.in[0], &A, n.op.c_str());
@@ -2129,46 +2377,75 @@ class Runner {
                       shape_str(B->shape).c_str());
             return ICX_ERR_SHAPE;
         }
+        if (A->dtype != ICX_F32 || B->dtype != ICX_F32) {
+            set_error("%s: device operands of dtypes %s and %s (Float32 only; integer arithmetic runs on host-known "
+                      "shape tensors)", n.op.c_str(), dtype_name(A->dtype), dtype_name(B->dtype));
+            return ICX_ERR_DTYPE;
+        }
         Step st;
         st.op = op_code(n.op);
-        if (A->shape == out) {
+        if (A->shape == out && bcast_kind(B->shape, out) >= 0) {
             st.opnd0 = n.in[1];
             return run_chain(n.in[0], {st}, n.out[0], n.op.c_str());
         }
-        if (B->shape == out) {
+        if (B->shape == out && bcast_kind(A->shape, out) >= 0) {
             st.lhs = true;
             st.opnd0 = n.in[0];
             return run_chain(n.in[1], {st}, n.out[0], n.op.c_str());
         }
-        set_error("%s: broadcast of %s and %s to a new shape %s is not on this path", n.op.c_str(),
-                  shape_str(A->shape).c_str(), shape_str(B->shape).c_str(), shape_str(out).c_str());
-        return ICX_ERR_UNSUPPORTED;
+        // any other numpy broadcast (e.g. [1, S, D] over [B, S, D])
+        const std::vector<int64_t> ast = bcast_strides(A->shape, out), bst = bcast_strides(B->shape, out);
+        const float *a = static_cast<const float*>(A->ptr), *b = static_cast<const float*>(B->ptr);
+        DevTensor* Y;
+        rc = alloc(n.out[0], ICX_F32, out, &Y);
+        if (rc) return rc;
+        return icx::binary_f32(s_, st.op, a, ast.data(), b, bst.data(), (int)out.size(), out.data(),
+                               static_cast<float*>(Y->ptr));
     }
 
+    // Cast (src/operators/cast.rs; GPU dispatch src/cuda/executor/layout.rs:148-172) to
+    // FLOAT / INT32 / INT64 / BOOL, with Rust's `as` semantics.
     int run_cast(const Node& n) {
+        const int64_t to = n.attr_or("to", -1);
+        int dst;
+        switch (to) {
+            case 1: dst = ICX_F32; break;
+            case 6: dst = ICX_I32; break;
+            case 7: dst = ICX_I64; break;
+            case 9: dst = ICX_BOOL; break;
+            default:
+                set_error("Cast to ONNX dtype %lld is not on this path (FLOAT, INT32, INT64, BOOL)", (long long)to);
+                return ICX_ERR_UNSUPPORTED;
+        }
+        std::vector<const HostTensor*> hs;
+        if (all_host(n, 1, &hs)) {
+            const HostTensor& x = *hs[0];
+            HostTensor y = host_tensor(dst, x.shape);
+            const int64_t cnt = numel(x.shape);
+            for (int64_t i = 0; i < cnt; ++i) {  // integer / Bool source (all_host)
+                const int64_t v = int_at(x, i);
+                if (dst == ICX_F32) reinterpret_cast<float*>(y.data.data())[i] = (float)v;  // RNE
+                else put_int(y, i, v);
+            }
+            return set_host(n.out[0], std::move(y));
+        }
         const DevTensor* X;
         int rc = need(n.in[0], &X, "Cast");
         if (rc) return rc;
-        if (n.attr_or("to", -1) != 1) {
-            set_error("Cast to ONNX dtype %lld is not on this path (FLOAT only)", (long long)n.attr_or("to", -1));
-            return ICX_ERR_UNSUPPORTED;
-        }
-        if (X->dtype != ICX_I32 && X->dtype != ICX_F32) {
-            set_error("Cast from %s to Float32 is not on this path", dtype_name(X->dtype));
-            return ICX_ERR_UNSUPPORTED;
-        }
         const std::vector<int64_t> shape = X->shape;
         const void* x = X->ptr;
-        const int dt = X->dtype;
+        const int src = X->dtype;
         const size_t cnt = (size_t)numel(shape);
         DevTensor* Y;
-        rc = alloc(n.out[0], ICX_F32, shape, &Y);
+        rc = alloc(n.out[0], dst, shape, &Y);
         if (rc) return rc;
-        if (dt == ICX_F32) {
-            if (cnt) ICX_HIP_CHECK(hipMemcpyAsync(Y->ptr, x, cnt * 4, hipMemcpyDeviceToDevice, s_));
+        if (src == dst) {
+            if (cnt) ICX_HIP_CHECK(hipMemcpyAsync(Y->ptr, x, cnt * dtype_size(dst), hipMemcpyDeviceToDevice, s_));
             return ICX_OK;
         }
-        return icx_cast_i32_f32(s_, static_cast<const int32_t*>(x), cnt, static_cast<float*>(Y->ptr));
+        if (src == ICX_I32 && dst == ICX_F32)
+            return icx_cast_i32_f32(s_, static_cast<const int32_t*>(x), cnt, static_cast<float*>(Y->ptr));
+        return icx::cast_any(s_, src, x, dst, Y->ptr, cnt);
     }
 
     // DequantizeLinear (src/operators/dequantize_linear.rs:32-180): per-tensor or per-axis.
@@ -2180,6 +2457,11 @@ class Runner {
         if (n.in.size() != 2 || n.out.size() != 1) {
             set_error("Gather requires [data, indices] and one output");
             return ICX_ERR_INVALID_ARG;
+        }
+        std::vector<const HostTensor*> hs;
+        if (all_host(n, 2, &hs)) {
+            int rc = host_gather(n, *hs[0], *hs[1]);
+            if (rc != kHostTooLarge) return rc;
         }
         const DevTensor *D, *I;
         int rc = need(n.in[0], &D, "Gather");
@@ -2271,6 +2553,466 @@ class Runner {
         if (rc) return rc;
         return icx_dequantize_linear_f32(s_, x, x_dt, sc, zp, cnt, axis_size, inner, static_cast<float*>(Y->ptr));
     }
+
+    // ---- the shape / mask plumbing of an exported encoder ----------------------------------
+    // Shape (src/operators/shape.rs; GPU layout.rs:136-146): always on the host, Int64 [n],
+    // with opset 15's start / end clamped as the reference does.
+    int run_shape(const Node& n) {
+        std::vector<int64_t> xs;
+        int xdt;
+        if (n.in.empty() || !shape_of(n.in[0], &xs, &xdt)) {
+            set_error("Shape: input tensor '%s' is missing", n.in.empty() ? "" : n.in[0].c_str());
+            return ICX_ERR_INVALID_ARG;
+        }
+        const int64_t r = (int64_t)xs.size();
+        const int64_t s0 = n.attr_or("start", 0);
+        const int64_t start = s0 < 0 ? std::max<int64_t>(r + s0, 0) : std::min(s0, r);
+        int64_t end = r;
+        if (n.attr.count("end")) {
+            const int64_t e0 = n.attr.at("end");
+            end = e0 < 0 ? std::max<int64_t>(r + e0, 0) : std::min(e0, r);
+        }
+        end = std::max(end, start);
+        HostTensor t = host_tensor(ICX_I64, {end - start});
+        for (int64_t i = start; i < end; ++i) put_int(t, i - start, xs[(size_t)i]);
+        return set_host(n.out[0], std::move(t));
+    }
+
+    // Unsqueeze / Squeeze / Identity (GPU layout.rs:579-662): a new shape over the same
+    // elements — a view of a device tensor (as Reshape), a copy of a host one.  Axes come
+    // from the input (opset 13) or the attribute, negative ones counted from the output rank
+    // (Unsqueeze) or the input rank (Squeeze); Squeeze without axes drops every unit dim, and
+    // with axes drops the listed ones that are 1.
+    int run_view(const Node& n) {
+        std::vector<int64_t> xs;
+        int xdt;
+        if (n.in.empty() || !shape_of(n.in[0], &xs, &xdt)) {
+            set_error("%s: input tensor '%s' is missing", n.op.c_str(), n.in.empty() ? "" : n.in[0].c_str());
+            return ICX_ERR_INVALID_ARG;
+        }
+        std::vector<int64_t> oshape, axes;
+        bool have = false;
+        if (n.in.size() > 1 && !n.in[1].empty()) {
+            int rc = host_ints(n.in[1], &axes, n.op.c_str());
+            if (rc) return rc;
+            have = true;
+        } else if (n.iattrs.count("axes")) {
+            axes = n.iattrs.at("axes");
+            have = true;
+        }
+        if (n.op == "Identity") {
+            oshape = xs;
+        } else if (n.op == "Unsqueeze") {
+            if (!have) {
+                set_error("Unsqueeze requires an 'axes' attribute or input");
+                return ICX_ERR_INVALID_ARG;
+            }
+            const int64_t r = (int64_t)(xs.size() + axes.size());
+            std::vector<char> ins((size_t)r, 0);
+            for (int64_t a : axes) {
+                const int64_t ax = a < 0 ? a + r : a;
+                if (ax < 0 || ax >= r || ins[(size_t)ax]) {
+                    set_error("Unsqueeze: axis %lld is out of range or repeated for output rank %lld", (long long)a,
+                              (long long)r);
+                    return ICX_ERR_SHAPE;
+                }
+                ins[(size_t)ax] = 1;
+            }
+            size_t k = 0;
+            for (int64_t d = 0; d < r; ++d) oshape.push_back(ins[(size_t)d] ? 1 : xs[k++]);
+        } else {  // Squeeze
+            const int64_t r = (int64_t)xs.size();
+            std::vector<char> drop((size_t)r, have ? 0 : 1);
+            for (int64_t a : axes) {
+                const int64_t ax = a < 0 ? a + r : a;
+                if (ax < 0 || ax >= r) {
+                    set_error("Squeeze: axis %lld out of range for rank %lld", (long long)a, (long long)r);
+                    return ICX_ERR_SHAPE;
+                }
+                drop[(size_t)ax] = 1;
+            }
+            for (int64_t d = 0; d < r; ++d)
+                if (!(drop[(size_t)d] && xs[(size_t)d] == 1)) oshape.push_back(xs[(size_t)d]);
+        }
+        const HostTensor* h = host_known(n.in[0]);
+        if (h && int_dtype(h->dtype)) {
+            HostTensor t = *h;
+            t.shape = oshape;
+            return set_host(n.out[0], std::move(t));
+        }
+        const DevTensor* X;
+        int rc = need(n.in[0], &X, n.op.c_str());
+        if (rc) return rc;
+        DevTensor t = *X;
+        t.shape = oshape;
+        t.pooled = false;  // the buffer belongs to the input
+        g_.values[n.out[0]] = t;
+        return ICX_OK;
+    }
+
+    // Concat (src/operators/concat.rs; GPU gpu_concat via layout.rs:664-667): one strided
+    // copy per non-empty input into its slot of the output.
+    int run_concat(const Node& n) {
+        if (n.in.empty() || n.out.size() != 1) {
+            set_error("Concat requires at least one input and one output");
+            return ICX_ERR_INVALID_ARG;
+        }
+        std::vector<std::vector<int64_t>> shapes(n.in.size());
+        int dt = -1;
+        for (size_t i = 0; i < n.in.size(); ++i) {
+            int d;
+            if (!shape_of(n.in[i], &shapes[i], &d)) {
+                set_error("Concat: input tensor '%s' is missing", n.in[i].c_str());
+                return ICX_ERR_INVALID_ARG;
+            }
+            if (i && d != dt) {
+                set_error("Concat: inputs of dtypes %s and %s", dtype_name(dt), dtype_name(d));
+                return ICX_ERR_DTYPE;
+            }
+            dt = d;
+        }
+        const int64_t r = (int64_t)shapes[0].size();
+        const int64_t a0 = n.attr_or("axis", 0);
+        const int64_t ax = a0 < 0 ? a0 + r : a0;
+        if (ax < 0 || ax >= r) {
+            set_error("Concat: axis %lld out of range for rank %lld", (long long)a0, (long long)r);
+            return ICX_ERR_SHAPE;
+        }
+        std::vector<int64_t> oshape = shapes[0];
+        oshape[(size_t)ax] = 0;
+        for (auto& sh : shapes) {
+            bool ok = (int64_t)sh.size() == r;
+            for (int64_t d = 0; ok && d < r; ++d) ok = d == ax || sh[(size_t)d] == shapes[0][(size_t)d];
+            if (!ok) {
+                set_error("Concat: input shape %s does not match %s off axis %lld", shape_str(sh).c_str(),
+                          shape_str(shapes[0]).c_str(), (long long)ax);
+                return ICX_ERR_SHAPE;
+            }
+            oshape[(size_t)ax] += sh[(size_t)ax];
+        }
+        const std::vector<int64_t> ost = dense_strides(oshape);
+        std::vector<const HostTensor*> hs;
+        if (all_host(n, n.in.size(), &hs) && numel(oshape) <= kHostFoldMax) {
+            HostTensor y = host_tensor(dt, oshape);
+            const size_t es = dtype_size(dt);
+            int64_t at = 0;
+            for (size_t i = 0; i < n.in.size(); ++i) {
+                const std::vector<int64_t> ist = dense_strides(shapes[i]);
+                for_each_offset(shapes[i], {ost, ist}, {at * ost[(size_t)ax], 0}, [&](int64_t, const std::vector<int64_t>& o) {
+                    std::memcpy(&y.data[(size_t)o[0] * es], &hs[i]->data[(size_t)o[1] * es], es);
+                });
+                at += shapes[i][(size_t)ax];
+            }
+            return set_host(n.out[0], std::move(y));
+        }
+        std::vector<const DevTensor*> xs(n.in.size());
+        for (size_t i = 0; i < n.in.size(); ++i) {
+            int rc = need(n.in[i], &xs[i], "Concat");
+            if (rc) return rc;
+        }
+        std::vector<const void*> ptrs;
+        for (auto* x : xs) ptrs.push_back(x->ptr);
+        DevTensor* Y;
+        int rc = alloc(n.out[0], dt, oshape, &Y);
+        if (rc) return rc;
+        int64_t at = 0;
+        for (size_t i = 0; i < n.in.size(); ++i) {
+            const std::vector<int64_t> ist = dense_strides(shapes[i]);
+            rc = icx::strided_copy(s_, ptrs[i], Y->ptr, dtype_size(dt), (int)r, shapes[i].data(), ist.data(), 0,
+                                   ost.data(), at * ost[(size_t)ax]);
+            if (rc) return rc;
+            at += shapes[i][(size_t)ax];
+        }
+        return ICX_OK;
+    }
+
+    // Slice (GPU gpu_slice_nd via layout.rs:345-456; CPU src/operators/slice.rs): starts /
+    // ends / axes / steps read on the host, one strided copy.
+    int run_slice(const Node& n) {
+        if (n.in.size() < 3 || n.out.size() != 1) {
+            set_error("Slice requires at least 3 inputs: data, starts, ends");
+            return ICX_ERR_INVALID_ARG;
+        }
+        std::vector<int64_t> xs, starts, ends, axes, steps, first, step, len;
+        int dt;
+        if (!shape_of(n.in[0], &xs, &dt)) {
+            set_error("Slice: input tensor '%s' is missing", n.in[0].c_str());
+            return ICX_ERR_INVALID_ARG;
+        }
+        int rc = host_ints(n.in[1], &starts, "Slice");
+        if (!rc) rc = host_ints(n.in[2], &ends, "Slice");
+        const bool has_axes = n.in.size() > 3 && !n.in[3].empty(), has_steps = n.in.size() > 4 && !n.in[4].empty();
+        if (!rc && has_axes) rc = host_ints(n.in[3], &axes, "Slice");
+        if (!rc && has_steps) rc = host_ints(n.in[4], &steps, "Slice");
+        if (!rc)
+            rc = slice_params(xs, starts, ends, has_axes ? &axes : nullptr, has_steps ? &steps : nullptr, &first, &step,
+                              &len);
+        if (rc) return rc;
+        const std::vector<int64_t> ist = dense_strides(xs);
+        std::vector<int64_t> xst(xs.size());
+        int64_t x_off = 0;
+        for (size_t d = 0; d < xs.size(); ++d) {
+            xst[d] = step[d] * ist[d];
+            if (len[d] > 0) x_off += first[d] * ist[d];
+        }
+        const std::vector<int64_t> ost = dense_strides(len);
+        std::vector<const HostTensor*> hs;
+        if (all_host(n, 1, &hs) && numel(len) <= kHostFoldMax) {
+            HostTensor y = host_tensor(dt, len);
+            const size_t es = dtype_size(dt);
+            if (numel(len) > 0)
+                for_each_offset(len, {ost, xst}, {0, x_off}, [&](int64_t, const std::vector<int64_t>& o) {
+                    std::memcpy(&y.data[(size_t)o[0] * es], &hs[0]->data[(size_t)o[1] * es], es);
+                });
+            return set_host(n.out[0], std::move(y));
+        }
+        const DevTensor* X;
+        rc = need(n.in[0], &X, "Slice");
+        if (rc) return rc;
+        const void* x = X->ptr;
+        DevTensor* Y;
+        rc = alloc(n.out[0], dt, len, &Y);
+        if (rc) return rc;
+        return icx::strided_copy(s_, x, Y->ptr, dtype_size(dt), (int)len.size(), len.data(), xst.data(), x_off,
+                                 ost.data(), 0);
+    }
+
+    // Expand (GPU gpu_expand, src/cuda/ops/layout/mod.rs:1624-1670): bidirectional
+    // broadcast of the input and the target shape, one strided copy with stride 0 on the
+    // broadcast dimensions.
+    int run_expand(const Node& n) {
+        if (n.in.size() != 2 || n.out.size() != 1) {
+            set_error("Expand requires [input, shape] and one output");
+            return ICX_ERR_INVALID_ARG;
+        }
+        std::vector<int64_t> xs, target;
+        int dt;
+        if (!shape_of(n.in[0], &xs, &dt)) {
+            set_error("Expand: input tensor '%s' is missing", n.in[0].c_str());
+            return ICX_ERR_INVALID_ARG;
+        }
+        int rc = host_ints(n.in[1], &target, "Expand");
+        if (rc) return rc;
+        bool ok;
+        const std::vector<int64_t> oshape = broadcast_shape(xs, target, &ok);
+        if (!ok) {
+            set_error("Expand: shapes %s and %s are not broadcastable", shape_str(xs).c_str(), shape_str(target).c_str());
+            return ICX_ERR_SHAPE;
+        }
+        const std::vector<int64_t> xst = bcast_strides(xs, oshape), ost = dense_strides(oshape);
+        std::vector<const HostTensor*> hs;
+        if (all_host(n, 1, &hs) && numel(oshape) <= kHostFoldMax) {
+            HostTensor y = host_tensor(dt, oshape);
+            const size_t es = dtype_size(dt);
+            for_each_offset(oshape, {ost, xst}, {0, 0}, [&](int64_t, const std::vector<int64_t>& o) {
+                std::memcpy(&y.data[(size_t)o[0] * es], &hs[0]->data[(size_t)o[1] * es], es);
+            });
+            return set_host(n.out[0], std::move(y));
+        }
+        const DevTensor* X;
+        rc = need(n.in[0], &X, "Expand");
+        if (rc) return rc;
+        const void* x = X->ptr;
+        DevTensor* Y;
+        rc = alloc(n.out[0], dt, oshape, &Y);
+        if (rc) return rc;
+        return icx::strided_copy(s_, x, Y->ptr, dtype_size(dt), (int)oshape.size(), oshape.data(), xst.data(), 0,
+                                 ost.data(), 0);
+    }
+
+    // Equal (src/operators/equal.rs; GPU elementwise.rs:333): numpy broadcasting, Bool out.
+    int run_equal(const Node& n) {
+        if (n.in.size() != 2 || n.out.size() != 1) {
+            set_error("Equal: expected 2 inputs and 1 output");
+            return ICX_ERR_INVALID_ARG;
+        }
+        std::vector<int64_t> as, bs;
+        int adt, bdt;
+        if (!shape_of(n.in[0], &as, &adt) || !shape_of(n.in[1], &bs, &bdt)) {
+            set_error("Equal: an input tensor is missing");
+            return ICX_ERR_INVALID_ARG;
+        }
+        if (adt != bdt) {
+            set_error("Equal: operands of dtypes %s and %s", dtype_name(adt), dtype_name(bdt));
+            return ICX_ERR_DTYPE;
+        }
+        bool ok;
+        const std::vector<int64_t> oshape = broadcast_shape(as, bs, &ok);
+        if (!ok) {
+            set_error("Equal: shapes %s and %s do not broadcast", shape_str(as).c_str(), shape_str(bs).c_str());
+            return ICX_ERR_SHAPE;
+        }
+        const std::vector<int64_t> ast = bcast_strides(as, oshape), bst = bcast_strides(bs, oshape);
+        std::vector<const HostTensor*> hs;
+        if (all_host(n, 2, &hs) && numel(oshape) <= kHostFoldMax) {
+            HostTensor y = host_tensor(ICX_BOOL, oshape);
+            for_each_offset(oshape, {ast, bst}, {0, 0}, [&](int64_t e, const std::vector<int64_t>& o) {
+                y.data[(size_t)e] = int_at(*hs[0], o[0]) == int_at(*hs[1], o[1]);
+            });
+            return set_host(n.out[0], std::move(y));
+        }
+        const DevTensor *A, *B;
+        int rc = need(n.in[0], &A, "Equal");
+        if (!rc) rc = need(n.in[1], &B, "Equal");
+        if (rc) return rc;
+        const void *a = A->ptr, *b = B->ptr;
+        DevTensor* Y;
+        rc = alloc(n.out[0], ICX_BOOL, oshape, &Y);
+        if (rc) return rc;
+        return icx::compare_equal(s_, adt, a, ast.data(), b, bst.data(), (int)oshape.size(), oshape.data(),
+                                  static_cast<uint8_t*>(Y->ptr));
+    }
+
+    // Where (src/operators/where_op.rs; GPU layout.rs:62-134): three-way numpy broadcasting;
+    // a condition that is not Bool is cast to Bool first, as the reference does.
+    int run_where(const Node& n) {
+        if (n.in.size() != 3 || n.out.size() != 1) {
+            set_error("Where requires [condition, x, y] and one output");
+            return ICX_ERR_INVALID_ARG;
+        }
+        std::vector<int64_t> cs, xs, ys;
+        int cdt, xdt, ydt;
+        if (!shape_of(n.in[0], &cs, &cdt) || !shape_of(n.in[1], &xs, &xdt) || !shape_of(n.in[2], &ys, &ydt)) {
+            set_error("Where: an input tensor is missing");
+            return ICX_ERR_INVALID_ARG;
+        }
+        if (xdt != ydt) {
+            set_error("Where: x and y of dtypes %s and %s", dtype_name(xdt), dtype_name(ydt));
+            return ICX_ERR_DTYPE;
+        }
+        bool ok1, ok2;
+        const std::vector<int64_t> cx = broadcast_shape(cs, xs, &ok1);
+        const std::vector<int64_t> oshape = broadcast_shape(cx, ys, &ok2);
+        if (!ok1 || !ok2) {
+            set_error("Where: shapes %s, %s and %s are not broadcastable", shape_str(cs).c_str(), shape_str(xs).c_str(),
+                      shape_str(ys).c_str());
+            return ICX_ERR_SHAPE;
+        }
+        const std::vector<int64_t> cst = bcast_strides(cs, oshape), xst = bcast_strides(xs, oshape),
+                                   yst = bcast_strides(ys, oshape);
+        const size_t es = dtype_size(xdt);
+        std::vector<const HostTensor*> hs;
+        if (all_host(n, 3, &hs) && numel(oshape) <= kHostFoldMax) {
+            HostTensor y = host_tensor(xdt, oshape);
+            for_each_offset(oshape, {cst, xst, yst}, {0, 0, 0}, [&](int64_t e, const std::vector<int64_t>& o) {
+                const bool c = int_at(*hs[0], o[0]) != 0;
+                std::memcpy(&y.data[(size_t)e * es], &(c ? hs[1] : hs[2])->data[(size_t)(c ? o[1] : o[2]) * es], es);
+            });
+            return set_host(n.out[0], std::move(y));
+        }
+        const DevTensor *C, *X, *Yv;
+        int rc = need(n.in[0], &C, "Where");
+        if (!rc) rc = need(n.in[1], &X, "Where");
+        if (!rc) rc = need(n.in[2], &Yv, "Where");
+        if (rc) return rc;
+        const void* c = C->ptr;
+        const void *x = X->ptr, *yv = Yv->ptr;
+        if (cdt != ICX_BOOL && cdt != ICX_U8) {  // condition to Bool (x != 0)
+            DevTensor* T;
+            const size_t cnt = (size_t)numel(cs);
+            rc = alloc(n.out[0] + "::cond", ICX_BOOL, cs, &T);
+            if (!rc) rc = icx::cast_any(s_, cdt, c, ICX_BOOL, T->ptr, cnt);
+            if (rc) return rc;
+            c = T->ptr;
+        }
+        DevTensor* O;
+        rc = alloc(n.out[0], xdt, oshape, &O);
+        if (rc) return rc;
+        return icx::select_where(s_, es, static_cast<const uint8_t*>(c), cst.data(), x, xst.data(), yv, yst.data(),
+                                 (int)oshape.size(), oshape.data(), O->ptr);
+    }
+
+    // Gather of a host-known integer tensor (typically a Shape result) on the host, with the
+    // index rules of icx_gather.
+    int host_gather(const Node& n, const HostTensor& D, const HostTensor& I) const {
+        if (I.dtype != ICX_I64 && I.dtype != ICX_I32) {
+            set_error("Gather: indices must be Int64 or Int32, got %s", dtype_name(I.dtype));
+            return ICX_ERR_DTYPE;
+        }
+        const int64_t nd = (int64_t)D.shape.size();
+        const int64_t ax0 = n.attr_or("axis", 0);
+        const int64_t ax = ax0 < 0 ? ax0 + nd : ax0;
+        if (nd < 1 || ax < 0 || ax >= nd) {
+            set_error("Gather: axis %lld out of range for rank-%lld data", (long long)ax0, (long long)nd);
+            return ICX_ERR_SHAPE;
+        }
+        int64_t outer = 1, inner = 1;
+        for (int64_t d = 0; d < ax; ++d) outer *= D.shape[(size_t)d];
+        for (int64_t d = ax + 1; d < nd; ++d) inner *= D.shape[(size_t)d];
+        std::vector<int64_t> oshape(D.shape.begin(), D.shape.begin() + ax);
+        oshape.insert(oshape.end(), I.shape.begin(), I.shape.end());
+        oshape.insert(oshape.end(), D.shape.begin() + ax + 1, D.shape.end());
+        if (numel(oshape) > kHostFoldMax) return kHostTooLarge;
+        const int64_t alen = D.shape[(size_t)ax], ni = numel(I.shape);
+        if (alen == 0 && ni * outer * inner > 0) {
+            set_error("Gather: %lld indices into an empty axis", (long long)ni);
+            return ICX_ERR_SHAPE;
+        }
+        const size_t es = dtype_size(D.dtype);
+        HostTensor y = host_tensor(D.dtype, oshape);
+        for (int64_t o = 0; o < outer; ++o)
+            for (int64_t j = 0; j < ni; ++j) {
+                int64_t k = int_at(I, j);  // negative from the end, then clamped as icx_gather does
+                if (k < 0) k += alen;
+                k = std::min(std::max<int64_t>(k, 0), alen - 1);
+                std::memcpy(&y.data[(size_t)((o * ni + j) * inner) * es], &D.data[(size_t)((o * alen + k) * inner) * es],
+                            (size_t)inner * es);
+            }
+        return set_host(n.out[0], std::move(y));
+    }
+
+    // Add / Sub / Mul / Div of host-known integer tensors (shape arithmetic), numpy
+    // broadcasting, wrapping as Rust's release build; integer division truncates, and
+    // division by zero or of the minimum by -1 is an error (Rust panics).
+    int host_binary(const Node& n, const HostTensor& A, const HostTensor& B) const {
+        if (A.dtype != B.dtype || A.dtype == ICX_BOOL) {
+            set_error("%s: operands of dtypes %s and %s", n.op.c_str(), dtype_name(A.dtype), dtype_name(B.dtype));
+            return ICX_ERR_DTYPE;
+        }
+        bool ok;
+        const std::vector<int64_t> oshape = broadcast_shape(A.shape, B.shape, &ok);
+        if (!ok) {
+            set_error("%s: shapes %s and %s do not broadcast", n.op.c_str(), shape_str(A.shape).c_str(),
+                      shape_str(B.shape).c_str());
+            return ICX_ERR_SHAPE;
+        }
+        if (numel(oshape) > kHostFoldMax) return kHostTooLarge;
+        HostTensor y = host_tensor(A.dtype, oshape);
+        const int op = op_code(n.op);
+        const int64_t lo = A.dtype == ICX_I64 ? INT64_MIN : A.dtype == ICX_I32 ? INT32_MIN : A.dtype == ICX_I8 ? -128 : 0;
+        int bad = 0;
+        for_each_offset(oshape, {bcast_strides(A.shape, oshape), bcast_strides(B.shape, oshape)}, {0, 0},
+                        [&](int64_t e, const std::vector<int64_t>& o) {
+                            const int64_t a = int_at(A, o[0]), b = int_at(B, o[1]);
+                            uint64_t r = 0;
+                            switch (op) {
+                                case ICX_OP_ADD: r = (uint64_t)a + (uint64_t)b; break;
+                                case ICX_OP_SUB: r = (uint64_t)a - (uint64_t)b; break;
+                                case ICX_OP_MUL: r = (uint64_t)a * (uint64_t)b; break;
+                                default:
+                                    if (b == 0 || (b == -1 && a == lo)) bad = 1;
+                                    else r = (uint64_t)(a / b);
+                            }
+                            put_int(y, e, (int64_t)r);
+                        });
+        if (bad) {
+            set_error("%s: integer division by zero or overflow", n.op.c_str());
+            return ICX_ERR_INVALID_ARG;
+        }
+        return set_host(n.out[0], std::move(y));
+    }
+
+   public:
+    // Outputs the caller asked for that exist only on the host this run: upload them.
+    int finish_outputs() {
+        for (auto& o : g_.live_outputs) {
+            if (g_.values.count(o) || !g_.hv.count(o)) continue;
+            const DevTensor* d;
+            int rc = materialize(o, &d);
+            if (rc) return rc;
+        }
+        return ICX_OK;
+    }
 };
 
 std::vector<std::string> names_of(int n, const char* const* p) {
@@ -2279,7 +3021,9 @@ std::vector<std::string> names_of(int n, const char* const* p) {
     return v;
 }
 
-bool valid_dtype(int dt) { return dt == ICX_I8 || dt == ICX_U8 || dt == ICX_I32 || dt == ICX_F32; }
+bool valid_dtype(int dt) {
+    return dt == ICX_I8 || dt == ICX_U8 || dt == ICX_I32 || dt == ICX_F32 || dt == ICX_BOOL;
+}
 
 }  // namespace
 
@@ -2645,7 +3389,7 @@ static int icx_graph_run_impl(icx_graph* g, icx_stream_t stream, RunProfile* pro
         }
         r.release_dead(i);
     }
-    return ICX_OK;
+    return r.finish_outputs();
 }
 
 static int icx_graph_run_profiled_impl(icx_graph* g, icx_stream_t stream, icx_op_profile* ops, int capacity,

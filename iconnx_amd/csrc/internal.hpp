@@ -74,14 +74,15 @@ int qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int
                 size_t M, size_t K, size_t N, const void* a_zp, const icx_chain* chain, uint8_t* y,
                 float* y_scale, uint8_t* y_zp, unsigned* sync);
 
-// DynamicQuantizeLinear of a small flat x as one launch: the blocks keep x in registers and
-// trade their (min, max) through `sync` (the layout, contract and failure reporting of
-// qlinear_dql's).  Needs 16-byte aligned x, 4-byte aligned y and n <= 128 * 1024 + 3 (it is
-// slower than the two launches beyond that); otherwise ICX_ERR_UNSUPPORTED, having launched
-// nothing.  y, y_scale, y_zp equal icx_dynamic_quantize_linear's bit for bit.
 // Synchronise `s`, then read and clear the exchange buffer's sticky error word:
 // ICX_ERR_KERNEL (with a message) if any launch since the last check gave up waiting.
 int exchange_status(hipStream_t s, unsigned* sync);
+
+// DynamicQuantizeLinear of a flat x as one launch: the blocks keep x in registers (1, 2 or
+// 4 float4 per lane) and trade their (min, max) through `sync` (the layout, contract and
+// failure reporting of qlinear_dql's).  Needs 16-byte aligned x, 4-byte aligned y and a grid
+// of at most kQoutMaxBlocks resident blocks (n <= 4 Mi + 3); otherwise ICX_ERR_UNSUPPORTED,
+// having launched nothing.  y, y_scale, y_zp equal icx_dynamic_quantize_linear's bit for bit.
 int dql_exchange(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
                  unsigned* sync);
 
@@ -112,6 +113,41 @@ inline unsigned long long wall_ticks(unsigned us) {
 // non-temporal stores (the C entry point); the graph executor passes false.
 int dql_two_launch(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
                    int32_t* opt_rowsum, size_t row_len, void* ws, size_t ws_bytes, bool nt_y);
+
+// ---- layout.hip: the shape / mask plumbing of an exported encoder -----------------------
+constexpr int kLayoutMaxRank = 8;
+constexpr size_t kUploadMaxBytes = 64 * 1024;
+
+// y[y_off + sum_d i_d * y_strides[d]] = x[x_off + sum_d i_d * x_strides[d]] for every index
+// of `dims` (element strides, negative for a reversed walk, 0 for a broadcast dimension);
+// elements of es = 1, 2, 4 or 8 bytes.  Slice, Expand and each input of Concat.
+int strided_copy(hipStream_t s, const void* x, void* y, size_t es, int rank, const int64_t* dims,
+                 const int64_t* x_strides, int64_t x_off, const int64_t* y_strides, int64_t y_off);
+
+// y (dense Bool, one byte 0 / 1) = a == b over `dims`, the operands read through their own
+// (broadcast) element strides; dtype: ICX_I8 / U8 / BOOL / I32 / F32 / I64.
+int compare_equal(hipStream_t s, int dtype, const void* a, const int64_t* a_strides, const void* b,
+                  const int64_t* b_strides, int rank, const int64_t* dims, uint8_t* y);
+
+// out (dense) = c ? x : y over `dims`, each input read through its own (broadcast) strides;
+// c is Bool (one byte, nonzero = true), x / y / out elements of es bytes.
+int select_where(hipStream_t s, size_t es, const uint8_t* c, const int64_t* c_strides, const void* x,
+                 const int64_t* x_strides, const void* y, const int64_t* y_strides, int rank,
+                 const int64_t* dims, void* out);
+
+// y (dense) = a op b over `dims` (op: ICX_OP_ADD / SUB / MUL / DIV), each operand read
+// through its own (broadcast) strides, one IEEE f32 rounding per element.
+int binary_f32(hipStream_t s, int op, const float* a, const int64_t* a_strides, const float* b,
+               const int64_t* b_strides, int rank, const int64_t* dims, float* y);
+
+// Elementwise Cast of n elements from I8 / U8 / BOOL / I32 / I64 / F32 to F32 / I64 / I32 /
+// BOOL, as Rust's `as` (integers wrap or widen; to Float32 rounds to nearest even; Float32
+// to an integer is NaN -> 0, saturating, else toward zero); to Bool is x != 0.
+int cast_any(hipStream_t s, int src_dtype, const void* x, int dst_dtype, void* y, size_t n);
+
+// Copy `bytes` (<= kUploadMaxBytes) of host memory to `dev` through kernel arguments: the
+// host buffer may be reused as soon as this returns, and a captured graph replays the copy.
+int upload_bytes(hipStream_t s, const void* host, size_t bytes, void* dev);
 
 // DynamicQuantizeLinear of x from the n_part partials its producer left: one launch (the
 // quantize pass of icx_dynamic_quantize_linear, which folds them).

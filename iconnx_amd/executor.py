@@ -25,11 +25,11 @@ from collections import namedtuple
 
 import numpy as np
 
-from ._lib import ICX_F32, ICX_I8, ICX_I32, ICX_I64, ICX_U8, IconnxError, OpProfile, check, lib
+from ._lib import ICX_BOOL, ICX_F32, ICX_I8, ICX_I32, ICX_I64, ICX_U8, IconnxError, OpProfile, check, lib
 
 _NP_DT = {np.dtype(np.int8): ICX_I8, np.dtype(np.uint8): ICX_U8,
           np.dtype(np.int32): ICX_I32, np.dtype(np.float32): ICX_F32,
-          np.dtype(np.int64): ICX_I64}  # Int64: Gather indices
+          np.dtype(np.int64): ICX_I64, np.dtype(np.bool_): ICX_BOOL}
 _INIT_DT = {**_NP_DT, np.dtype(np.int64): ICX_I64}
 _DT_NP = {v: k for k, v in _NP_DT.items()}
 
@@ -46,7 +46,7 @@ def _torch():
 def _torch_dt(code):
     torch = _torch()
     return {ICX_I8: torch.int8, ICX_U8: torch.uint8, ICX_I32: torch.int32,
-            ICX_F32: torch.float32, ICX_I64: torch.int64}[code]
+            ICX_F32: torch.float32, ICX_I64: torch.int64, ICX_BOOL: torch.bool}[code]
 
 
 def _dims(shape):
@@ -174,9 +174,9 @@ class GpuGraphExecutor:
         check(self._L.icx_graph_add_input(self._g, name.encode(), len(dims), _dims(dims)))
 
     def add_initializer(self, name, tensor):
-        """Host array (numpy or CPU torch).  Int8 / UInt8 / Int32 / Float32 are kept, Int64
-        too (shape constants, read on the host); other dtypes are skipped, so a node reading
-        one fails at run (as the reference does)."""
+        """Host array (numpy or CPU torch).  Int8 / UInt8 / Int32 / Float32 / Int64 / Bool
+        are kept (small integer ones are also read on the host as shape constants); other
+        dtypes are skipped, so a node reading one fails at run (as the reference does)."""
         arr = tensor.numpy() if hasattr(tensor, "numpy") and not isinstance(tensor, np.ndarray) \
             else np.asarray(tensor)
         code = _INIT_DT.get(arr.dtype)

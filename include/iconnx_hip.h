@@ -35,8 +35,9 @@ typedef enum {
     ICX_ERR_KERNEL = 7,      /* a kernel reported a failure on the device (icx_graph_status) */
 } icx_status;
 
-/* ICX_I64: Reshape shapes (graph initializers, read on the host) and Gather indices / data. */
-typedef enum { ICX_I8 = 0, ICX_U8 = 1, ICX_I32 = 2, ICX_F32 = 3, ICX_I64 = 4 } icx_dtype;
+/* ICX_I64: Reshape shapes (graph initializers, read on the host) and Gather indices / data.
+ * ICX_BOOL: one byte per element, 0 or 1 (ONNX BOOL; Equal's output, Where's condition). */
+typedef enum { ICX_I8 = 0, ICX_U8 = 1, ICX_I32 = 2, ICX_F32 = 3, ICX_I64 = 4, ICX_BOOL = 5 } icx_dtype;
 
 const char* icx_status_str(int status);
 /* Message of the last failing call on this host thread ("" if none). */

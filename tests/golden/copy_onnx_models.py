@@ -28,6 +28,24 @@ TESTS = [
     "test_reduce_mean_negative_axes_keepdims_example", "test_reduce_mean_negative_axes_keepdims_random",
     "test_pow", "test_pow_bcast_array", "test_pow_bcast_scalar", "test_pow_example",
     "test_sqrt", "test_sqrt_example",
+    # the shape / mask plumbing of an exported encoder: reshape targets from Shape, position
+    # ids by Slice, the attention mask by Equal / Unsqueeze / Expand / Where
+    "test_shape", "test_shape_example", "test_shape_start_1", "test_shape_end_1",
+    "test_shape_start_negative_1", "test_shape_end_negative_1", "test_shape_start_1_end_2",
+    "test_shape_start_1_end_negative_1", "test_shape_clip_start", "test_shape_clip_end",
+    "test_unsqueeze_axis_0", "test_unsqueeze_axis_1", "test_unsqueeze_axis_2",
+    "test_unsqueeze_negative_axes", "test_unsqueeze_three_axes", "test_unsqueeze_two_axes",
+    "test_unsqueeze_unsorted_axes", "test_squeeze", "test_squeeze_negative_axes",
+    "test_concat_1d_axis_0", "test_concat_1d_axis_negative_1", "test_concat_2d_axis_0",
+    "test_concat_2d_axis_1", "test_concat_2d_axis_negative_1", "test_concat_2d_axis_negative_2",
+    "test_concat_3d_axis_0", "test_concat_3d_axis_1", "test_concat_3d_axis_2",
+    "test_concat_3d_axis_negative_1", "test_concat_3d_axis_negative_2",
+    "test_concat_3d_axis_negative_3",
+    "test_slice", "test_slice_default_axes", "test_slice_default_steps",
+    "test_slice_end_out_of_bounds", "test_slice_neg", "test_slice_neg_steps",
+    "test_slice_negative_axes", "test_slice_start_out_of_bounds",
+    "test_expand_dim_changed", "test_expand_dim_unchanged", "test_equal", "test_equal_bcast",
+    "test_where_example", "test_where_long_example",
 ]
 
 

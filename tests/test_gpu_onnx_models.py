@@ -12,6 +12,11 @@
   same graphs built directly.
 * ReduceMean / Pow / Sqrt (the node-by-node LayerNorm's ops): ReduceMean and Sqrt bit-exact
   against the oracle; Pow within two ulps of the oracle's C-library powf (device powf).
+* Shape / Unsqueeze / Squeeze / Concat / Slice / Expand / Equal / Where (an exported encoder's
+  shape and mask plumbing): exact against the oracle (oracle/layout.py) and the file, once
+  with the inputs bound from host memory (integer inputs are then shape arithmetic, computed
+  on the host) and once with every input a device tensor (the device kernels; Slice bounds
+  and axes read back to the host as the reference's get_or_fetch_i64 does).
 """
 import glob
 import os
@@ -25,6 +30,8 @@ from iconnx_amd import graphs
 from iconnx_amd.executor import GpuGraphExecutor
 from iconnx_amd.onnx import OnnxParser, decode_tensor
 from tests.golden_util import bits
+from tests.test_oracle_layout import OPS as LAYOUT_OPS
+from tests.test_oracle_layout import oracle_of as layout_oracle_of
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -117,6 +124,15 @@ def test_vendored_onnx_model_executes(d):
         assert int(got["y_zero_point"]) == int(want["y_zero_point"])
         return
     name, want = outs[0]
+    if op in LAYOUT_OPS:
+        ref = layout_oracle_of(node, list(ins.values()))
+        for where in ("host", "device"):
+            feed = ins if where == "host" else {k: torch.from_numpy(np.ascontiguousarray(v)).cuda()
+                                                   for k, v in ins.items()}
+            got = run_model(m, feed, [name])[name]
+            assert got.dtype == want.dtype and got.shape == want.shape, (where, got.dtype, got.shape)
+            assert np.array_equal(got, ref) and np.array_equal(got, want), where
+        return
     got = run_model(m, ins, [name])[name]
     assert got.shape == want.shape, (got.shape, want.shape)
     ref = oracle_of(op, ins, node.attributes)
