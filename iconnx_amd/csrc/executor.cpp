@@ -1959,15 +1959,8 @@ class Runner {
         if (rc) return rc;
         if (R && R->shape != X->shape) {
             // the Add broadcasts: materialise it, then normalise
-            Step st;
-            st.op = ICX_OP_ADD;
-            bool ok;
-            const std::vector<int64_t> bs = broadcast_shape(X->shape, R->shape, &ok);
-            const bool x_full = bs == X->shape;
-            st.opnd0 = x_full ? resn : xn;
-            st.lhs = !x_full;
             const std::string tmp = out + "::sum";
-            rc = run_chain(x_full ? xn : resn, {st}, tmp, who);
+            rc = binary_f32_into(ICX_OP_ADD, xn, resn, tmp, who);
             if (rc) return rc;
             return run_layer_norm(tmp, "", sn, bn, eps, out, who);
         }
@@ -2366,40 +2359,47 @@ class Runner {
             int rc = host_binary(n, *hs[0], *hs[1]);
             if (rc != kHostTooLarge) return rc;
         }
+        return binary_f32_into(op_code(n.op), n.in[0], n.in[1], n.out[0], n.op.c_str());
+    }
+
+    // out = a op b on Float32 device tensors: the chain kernel when the output has one
+    // operand's shape and the other broadcasts as a chain operand, else the general
+    // broadcast kernel (e.g. [1, S, D] over [B, S, D]).
+    int binary_f32_into(int op, const std::string& an, const std::string& bn, const std::string& outn,
+                        const char* who) {
         const DevTensor *A, *B;
-        int rc = need(n.in[0], &A, n.op.c_str());
-        if (!rc) rc = need(n.in[1], &B, n.op.c_str());
+        int rc = need(an, &A, who);
+        if (!rc) rc = need(bn, &B, who);
         if (rc) return rc;
         bool ok;
         const std::vector<int64_t> out = broadcast_shape(A->shape, B->shape, &ok);
         if (!ok) {
-            set_error("%s: shapes %s and %s do not broadcast", n.op.c_str(), shape_str(A->shape).c_str(),
+            set_error("%s: shapes %s and %s do not broadcast", who, shape_str(A->shape).c_str(),
                       shape_str(B->shape).c_str());
             return ICX_ERR_SHAPE;
         }
         if (A->dtype != ICX_F32 || B->dtype != ICX_F32) {
             set_error("%s: device operands of dtypes %s and %s (Float32 only; integer arithmetic runs on host-known "
-                      "shape tensors)", n.op.c_str(), dtype_name(A->dtype), dtype_name(B->dtype));
+                      "shape tensors)", who, dtype_name(A->dtype), dtype_name(B->dtype));
             return ICX_ERR_DTYPE;
         }
         Step st;
-        st.op = op_code(n.op);
+        st.op = op;
         if (A->shape == out && bcast_kind(B->shape, out) >= 0) {
-            st.opnd0 = n.in[1];
-            return run_chain(n.in[0], {st}, n.out[0], n.op.c_str());
+            st.opnd0 = bn;
+            return run_chain(an, {st}, outn, who);
         }
         if (B->shape == out && bcast_kind(A->shape, out) >= 0) {
             st.lhs = true;
-            st.opnd0 = n.in[0];
-            return run_chain(n.in[1], {st}, n.out[0], n.op.c_str());
+            st.opnd0 = an;
+            return run_chain(bn, {st}, outn, who);
         }
-        // any other numpy broadcast (e.g. [1, S, D] over [B, S, D])
         const std::vector<int64_t> ast = bcast_strides(A->shape, out), bst = bcast_strides(B->shape, out);
         const float *a = static_cast<const float*>(A->ptr), *b = static_cast<const float*>(B->ptr);
         DevTensor* Y;
-        rc = alloc(n.out[0], ICX_F32, out, &Y);
+        rc = alloc(outn, ICX_F32, out, &Y);
         if (rc) return rc;
-        return icx::binary_f32(s_, st.op, a, ast.data(), b, bst.data(), (int)out.size(), out.data(),
+        return icx::binary_f32(s_, op, a, ast.data(), b, bst.data(), (int)out.size(), out.data(),
                                static_cast<float*>(Y->ptr));
     }
 

@@ -168,8 +168,10 @@ class GpuGraphExecutor:
             exec_.add_node("n%d" % i, node.op_type, node.inputs, node.outputs, node.attributes)
         return exec_
 
-    def add_input(self, name, shape):
-        """``shape[i] is None`` marks a dynamic dimension."""
+    def add_input(self, name, shape, elem_type=None):
+        """``shape[i] is None`` marks a dynamic dimension.  ``elem_type`` (an ONNX element
+        type, as a model file declares it) is accepted for the builders' sake and not
+        needed: the dtype comes with the tensor bound at run."""
         dims = [-1 if d is None else int(d) for d in shape]
         check(self._L.icx_graph_add_input(self._g, name.encode(), len(dims), _dims(dims)))
 

@@ -270,6 +270,136 @@ def encoder_graph(ex, layers=6, heads=12, hidden=768, ffn=3072, eps=1e-12, x_nam
     return x, names, params
 
 
+# ---------------------------------------------------------------------------------------
+# The same encoder as an exported DistilBERT-INT8 writes it (torch.onnx of Hugging Face's
+# DistilBertModel, opset 13-16, then ONNX Runtime's dynamic quantization — the form whose op
+# list the reference's INT8 design names, docs/superpowers/specs/2026-04-25-ws4-int8-
+# quantization-design.md:171): Int64 input_ids / attention_mask; the UINT8 word table through
+# Gather + DequantizeLinear, position ids sliced from a [1, 512] constant up to the sequence
+# length; every reshape target assembled at run time from Shape / Gather / Unsqueeze / Concat;
+# the key transposed twice; the padding mask as Equal / Reshape / Expand / Where(finfo.min)
+# on the scores; LayerNorms node by node (ReduceMean / Sub / Pow / Sqrt / Div / Mul / Add).
+# ---------------------------------------------------------------------------------------
+F32_MIN = np.float32(np.finfo(np.float32).min)
+
+
+def add_self_attention_export(ex, x, q, k, v, mask, heads, head_dim, prefix):
+    """MultiHeadSelfAttention over [B, S, H*D] projections q, k, v of ``x`` with the Int64
+    padding mask ``mask`` [B, S] (0 = padding), as exported.  Returns the context name."""
+    p = prefix
+    cst = lambda n, a: ex.add_initializer("%s.%s" % (p, n), np.asarray(a))  # noqa: E731
+    cst("i0", np.array(0, np.int64))
+    cst("i1", np.array(1, np.int64))
+    cst("ax0", np.array([0], np.int64))
+    cst("m1", np.array([-1], np.int64))
+    cst("one", np.array([1], np.int64))
+    cst("nh", np.array([heads], np.int64))
+    cst("dh", np.array([head_dim], np.int64))
+    cst("hid", np.array([heads * head_dim], np.int64))
+    cst("zero", np.array(0, np.int64))
+    cst("sqrt_d", np.array(np.sqrt(head_dim), np.float32))
+    cst("fmin", F32_MIN)
+    ext = {x, q, k, v, mask}
+
+    def n(name, op, ins, outs, attrs=None):  # names local to this block get the prefix
+        ex.add_node("%s.%s" % (p, name), op, [i if i in ext else "%s.%s" % (p, i) for i in ins],
+                    ["%s.%s" % (p, o) for o in outs], attrs)
+    # bs = x.size(0), k_length = x.size(1)
+    n("shape_x", "Shape", [x], ["xs"])
+    n("bs", "Gather", ["xs", "i0"], ["bs"], {"axis": 0})
+    n("klen", "Gather", ["xs", "i1"], ["klen"], {"axis": 0})
+    n("bs_u", "Unsqueeze", ["bs", "ax0"], ["bs_u"])
+    n("klen_u", "Unsqueeze", ["klen", "ax0"], ["klen_u"])
+    n("split", "Concat", ["bs_u", "m1", "nh", "dh"], ["split"], {"axis": 0})
+    for t, tag in ((q, "q"), (k, "k"), (v, "v")):  # x.view(bs, -1, H, D).transpose(1, 2)
+        n("view_" + tag, "Reshape", [t, "split"], [tag + "4"])
+        n("tr_" + tag, "Transpose", [tag + "4"], [tag + "t"], {"perm": [0, 2, 1, 3]})
+    n("scale_q", "Div", ["qt", "sqrt_d"], ["qs"])
+    n("tr_k2", "Transpose", ["kt"], ["kT"], {"perm": [0, 1, 3, 2]})
+    n("scores", "MatMul", ["qs", "kT"], ["s"])
+    # mask = (mask == 0).view(bs, 1, 1, k_length).expand_as(scores)
+    n("mask_eq", "Equal", [mask, "zero"], ["meq"])
+    n("mask_shape", "Concat", ["bs_u", "one", "one", "klen_u"], ["mshape"], {"axis": 0})
+    n("mask_view", "Reshape", ["meq", "mshape"], ["m4"])
+    n("shape_s", "Shape", ["s"], ["ss"])
+    n("mask_expand", "Expand", ["m4", "ss"], ["mx"])
+    n("masked_fill", "Where", ["mx", "fmin", "s"], ["sm"])
+    n("softmax", "Softmax", ["sm"], ["pr"], {"axis": -1})
+    n("context", "MatMul", ["pr", "vt"], ["c"])
+    n("tr_c", "Transpose", ["c"], ["ct"], {"perm": [0, 2, 1, 3]})
+    n("merge", "Concat", ["bs_u", "m1", "hid"], ["merge"], {"axis": 0})
+    n("unshape", "Reshape", ["ct", "merge"], ["ctx"])
+    return p + ".ctx"
+
+
+def add_embeddings_export(ex, ids, word_table, scale, zp, pos_table, ln, eps, prefix):
+    """DistilBERT's Embeddings: Gather(UInt8 word table, input_ids) -> DequantizeLinear, plus
+    Gather(position table, position_ids[:, :seq_len]) (a Slice of a [1, max_pos] Int64
+    constant), then a LayerNorm node by node.  Returns the output name."""
+    p = prefix
+    we = add_quantized_embedding(ex, ids, word_table, scale, zp, p + ".word")
+    ex.add_initializer(p + ".position_ids", np.arange(pos_table.shape[0], dtype=np.int64).reshape(1, -1))
+    ex.add_initializer(p + ".pos_table", np.asarray(pos_table, np.float32))
+    ex.add_initializer(p + ".i1", np.array(1, np.int64))
+    ex.add_initializer(p + ".z", np.array([0], np.int64))
+    ex.add_initializer(p + ".ax1", np.array([1], np.int64))
+    ex.add_node(p + ".shape_ids", "Shape", [ids], [p + ".ids_shape"])
+    ex.add_node(p + ".seq_len", "Gather", [p + ".ids_shape", p + ".i1"], [p + ".slen"], {"axis": 0})
+    ex.add_node(p + ".seq_len_u", "Unsqueeze", [p + ".slen", p + ".z"], [p + ".slen_u"])
+    ex.add_node(p + ".pos_slice", "Slice", [p + ".position_ids", p + ".z", p + ".slen_u", p + ".ax1"], [p + ".pid"])
+    ex.add_node(p + ".pos_gather", "Gather", [p + ".pos_table", p + ".pid"], [p + ".pemb"], {"axis": 0})
+    ex.add_node(p + ".sum", "Add", [we, p + ".pemb"], [p + ".e"])
+    return add_layer_norm_decomposed(ex, p + ".e", None, ln["scale"], ln["bias"], eps, p + ".ln")
+
+
+def export_encoder_graph(ex, layers=6, heads=12, hidden=768, ffn=3072, eps=1e-12, vocab=30522,
+                         max_pos=512, seed=3000):
+    """DistilBERT-INT8 as exported (see above) on executor or writer ``ex``: inputs
+    ``input_ids`` and ``attention_mask`` (Int64 [B, S]).  The layers carry the weights of
+    encoder_graph's; the embedding tables are seeded too.  Returns (output name, names dict
+    with the embedding output and per-layer tensor names, per-layer params, embedding
+    params)."""
+    ex.add_input("input_ids", [None, None], 7)
+    ex.add_input("attention_mask", [None, None], 7)
+    emb = dict(word=seeded_uniform(vocab * hidden, seed - 7, 0.0, 255.0).astype(np.uint8).reshape(vocab, hidden),
+               scale=np.float32(0.004), zp=np.uint8(128),
+               pos=(0.02 * seeded_normal(max_pos * hidden, seed - 6).astype(np.float64)).astype(np.float32)
+               .reshape(max_pos, hidden),
+               ln=dict(scale=seeded_uniform(hidden, seed - 5, 0.9, 1.1),
+                       bias=(0.02 * seeded_normal(hidden, seed - 4).astype(np.float64)).astype(np.float32)))
+    x = add_embeddings_export(ex, "input_ids", emb["word"], emb["scale"], emb["zp"], emb["pos"], emb["ln"], eps,
+                              "emb")
+    names, params = dict(emb=x, layers=[]), []
+    for l in range(layers):
+        prm = encoder_layer_params(l, hidden, ffn, seed)
+        p = "L%d" % l
+        lin = lambda name, inp, **kw: add_quantized_linear(  # noqa: E731
+            ex, inp, prm[name]["w"], prm[name]["w_zp"], prm[name]["w_scale"], prm[name]["bias"],
+            prefix="%s.%s" % (p, name), **kw)
+        dql = add_dynamic_quantize(ex, x, p + ".qkv")
+        q, k, v = (lin(nm, x, dql=dql) for nm in ("q", "k", "v"))
+        ctx = add_self_attention_export(ex, x, q, k, v, "attention_mask", heads, hidden // heads, p + ".attn")
+        o = lin("o", ctx)
+        x1 = add_layer_norm_decomposed(ex, o, x, prm["ln1"]["scale"], prm["ln1"]["bias"], eps, p + ".ln1")
+        h = lin("ff1", x1, gelu=True)
+        f = lin("ff2", h)
+        x2 = add_layer_norm_decomposed(ex, f, x1, prm["ln2"]["scale"], prm["ln2"]["bias"], eps, p + ".ln2")
+        names["layers"].append(dict(x=x, xq=dql[0], q=q, k=k, v=v, ctx=ctx, o=o, x1=x1, h=h, f=f, out=x2))
+        params.append(prm)
+        x = x2
+    return x, names, params, emb
+
+
+def export_inputs(batch=32, seq=128, vocab=30522, seed=2998):
+    """Seeded input_ids (uniform over the vocabulary) and an attention mask whose rows keep a
+    seeded number of leading tokens (the rest is padding, 0)."""
+    ids = (seeded_uniform(batch * seq, seed, 0.0, float(vocab)).astype(np.int64) % vocab).reshape(batch, seq)
+    lens = 1 + (seeded_uniform(batch, seed + 1, 0.0, float(seq)).astype(np.int64) % seq)
+    lens[0] = seq  # one unpadded row
+    mask = (np.arange(seq)[None, :] < lens[:, None]).astype(np.int64)
+    return ids, mask
+
+
 def encoder_input(batch=32, seq=128, hidden=768, seed=2999):
     """Input embeddings ~ N(0, 1), [batch, seq, hidden] float32."""
     return seeded_normal(batch * seq * hidden, seed).reshape(batch, seq, hidden)

@@ -4,8 +4,8 @@ INFRASTRUCTURE ONLY (the checker for tests/ and the CPU baseline of bench.py).
 Each function follows the node pattern that iconnx_amd.graphs builds and that the reference
 executes node by node (src/graph_executor.rs:356-432): DynamicQuantizeLinear, MatMulInteger,
 Cast, Mul (x_scale * w_scale, then the dequant), Add (bias), the erf-GELU (Div, Erf, Add,
-Mul, Mul), the attention (Reshape, Transpose, Div, MatMul, Softmax, MatMul, Transpose,
-Reshape) and LayerNormalization(Add(.)).
+Mul, Mul), the attention (Reshape, Transpose, Div, MatMul, [the padding mask,] Softmax,
+MatMul, Transpose, Reshape) and LayerNormalization(Add(.)).
 """
 import numpy as np
 
@@ -29,8 +29,10 @@ def gelu_ref(t):
     return mul(mul(t, add(erf(d), np.float32(1.0))), np.float32(0.5))
 
 
-def attention_ref(q, k, v, heads, scale=8.0, scale_q=True):
-    """The exported self-attention subgraph over [B, S, H*D] tensors."""
+def attention_ref(q, k, v, heads, scale=8.0, scale_q=True, mask=None):
+    """The exported self-attention subgraph over [B, S, H*D] tensors; ``mask`` (Int64 [B, S],
+    0 = padding) adds the export's masked_fill: Where(Expand(Reshape(Equal(mask, 0),
+    [B, 1, 1, S]), scores' shape), finfo(f32).min, scores) before the Softmax."""
     B, S, HD = q.shape
     D = HD // heads
     split = lambda t: transpose(np.ascontiguousarray(t).reshape(B, S, heads, D), (0, 2, 1, 3))  # noqa: E731
@@ -41,6 +43,10 @@ def attention_ref(q, k, v, heads, scale=8.0, scale_q=True):
     s = matmul_f32(qh.reshape(B * heads, S, D), kt.reshape(B * heads, D, S)).reshape(B, heads, S, S)
     if not scale_q:
         s = div(s, np.float32(scale))
+    if mask is not None:
+        from . import layout
+        m4 = layout.equal(np.asarray(mask, np.int64), np.array(0, np.int64)).reshape(B, 1, 1, S)
+        s = layout.where(layout.expand(m4, s.shape), np.float32(np.finfo(np.float32).min), s)
     pr = softmax(s)
     ctx = matmul_f32(pr.reshape(B * heads, S, S), vh.reshape(B * heads, S, D)).reshape(B, heads, S, D)
     return transpose(ctx, (0, 2, 1, 3)).reshape(B, S, HD)

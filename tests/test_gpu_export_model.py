@@ -1,0 +1,150 @@
+"""GPU: DistilBERT-INT8 in the form an export writes it (graphs.export_encoder_graph: Hugging
+Face's DistilBertModel through torch.onnx and ONNX Runtime's dynamic quantization — Int64
+input_ids / attention_mask, the UINT8 word table through Gather + DequantizeLinear, position
+ids sliced to the sequence length, every reshape target assembled from Shape / Gather /
+Unsqueeze / Concat, the padding mask as Equal / Reshape / Expand / Where, LayerNorms node by
+node), run by GpuGraphExecutor — from an .onnx file through OnnxParser / from_model, and at
+the full BASELINE size (6 layers, batch 32, seq 128, vocabulary 30522) directly.
+
+Node by node, each node group's GPU output against the oracle applied to that group's GPU
+inputs: bit-exact for the embeddings (Gather, DequantizeLinear, the broadcast Add, the
+LayerNorm), every DynamicQuantizeLinear (x_q, scale, zero point), every quantized linear and
+every LayerNorm (the LayerNormalization arithmetic: the node-by-node form with Mul(c, c) for
+Pow(c, 2), which the reference's powf matches to the last ulp or within 1e-6); within 1e-6 for
+the GELU linears (device erf / exp) and 1e-5 for the masked attention (fp32 MFMA summation
+order, device exp) — the tolerances of the unmasked encoder's node-by-node test.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from iconnx_amd import graphs
+from iconnx_amd.executor import GpuGraphExecutor
+from iconnx_amd.onnx import OnnxParser
+from oracle import layout as L
+from tests import encoder_ref as ref
+from tests.golden_util import bits
+
+pytestmark = pytest.mark.gpu
+H = 12
+
+
+def rel_err(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(float(np.max(np.abs(want))), 1e-30))
+
+
+def assert_bits(got, want, what):
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    bad = int(np.count_nonzero(bits(got) != bits(want))) if got.dtype == np.float32 else \
+        int(np.count_nonzero(got != want))
+    assert bad == 0, "%s: %d of %d elements differ" % (what, bad, want.size)
+
+
+def wanted(names):
+    want = [names["emb"], "emb.word.out", "emb.pemb", "emb.e"]
+    for t in names["layers"]:
+        base = t["q"].rsplit(".", 2)[0]
+        for tag in ("qkv", "o", "ff1", "ff2"):
+            want += ["%s.%s.x_q" % (base, tag), "%s.%s.x_scale" % (base, tag), "%s.%s.x_zp" % (base, tag)]
+        want += [t[k] for k in ("q", "k", "v", "ctx", "o", "x1", "h", "f", "out")]
+    return list(dict.fromkeys(want))
+
+
+def check_node_by_node(got, names, params, emb, ids, mask, eps=1e-12, rows=None):
+    flat = lambda a: np.asarray(a).reshape(-1, np.asarray(a).shape[-1])  # noqa: E731
+    B, S = ids.shape
+    # embeddings
+    we = oracle.dequantize_linear(oracle.gather(emb["word"], ids), emb["scale"], emb["zp"])
+    assert_bits(got["emb.word.out"], we, "word embeddings")
+    pid = L.slice_(np.arange(emb["pos"].shape[0], dtype=np.int64).reshape(1, -1), [0], [S], [1])
+    assert_bits(got["emb.pemb"], oracle.gather(emb["pos"], pid), "position embeddings")
+    assert_bits(got["emb.e"], oracle.add(got["emb.word.out"], got["emb.pemb"]), "embedding sum")
+    e_ln = oracle.layer_norm_decomposed(got["emb.e"], emb["ln"]["scale"], emb["ln"]["bias"], eps, square=True)
+    assert_bits(got[names["emb"]], e_ln, "embedding LayerNorm")
+    all_rows = [(0, B * S)] if rows is None else rows
+    for l, t in enumerate(names["layers"]):
+        base, p = "L%d" % l, params[l]
+
+        def dql_check(src, tag):
+            yq, ys, yz = oracle.dynamic_quantize_linear(got[src])
+            assert_bits(got["%s.%s.x_q" % (base, tag)], yq, "%s %s x_q" % (base, tag))
+            assert_bits(got["%s.%s.x_scale" % (base, tag)], np.asarray(ys, np.float32), "%s %s scale" % (base, tag))
+            assert int(got["%s.%s.x_zp" % (base, tag)]) == int(yz)
+
+        def lin_check(tag, xq_name, out_name, gelu=False):
+            xq = got["%s.%s.x_q" % (base, xq_name)]
+            xs = got["%s.%s.x_scale" % (base, xq_name)]
+            xz = got["%s.%s.x_zp" % (base, xq_name)]
+            for r0, r1 in all_rows:
+                y = ref.dequant_linear(xq, xs, xz, p[tag], rows=(r0, r1), gelu=gelu)
+                g = flat(got[out_name])[r0:r1]
+                if gelu:
+                    assert rel_err(g, y) < 1e-6, "%s %s rows %d:%d" % (base, tag, r0, r1)
+                else:
+                    assert_bits(g, y, "%s %s rows %d:%d" % (base, tag, r0, r1))
+
+        def ln_check(a, b, prm, out_name):  # every row
+            y = oracle.layer_norm_decomposed(flat(got[a]), prm["scale"], prm["bias"], eps, residual=flat(got[b]),
+                                             square=True)
+            assert_bits(flat(got[out_name]), y, "%s %s" % (base, out_name))
+
+        dql_check(t["x"], "qkv")
+        for n in ("q", "k", "v"):
+            lin_check(n, "qkv", t[n])
+        a = ref.attention_ref(got[t["q"]], got[t["k"]], got[t["v"]], H, 8.0, mask=mask)
+        for b in range(B):
+            assert rel_err(got[t["ctx"]][b], a[b]) < 1e-5, "%s masked attention batch %d" % (base, b)
+        dql_check(t["ctx"], "o")
+        lin_check("o", "o", t["o"])
+        ln_check(t["o"], t["x"], p["ln1"], t["x1"])
+        dql_check(t["x1"], "ff1")
+        lin_check("ff1", "ff1", t["h"], gelu=True)
+        dql_check(t["h"], "ff2")
+        lin_check("ff2", "ff2", t["f"])
+        ln_check(t["f"], t["x1"], p["ln2"], t["out"])
+
+
+def test_export_model_from_file(tmp_path):
+    path = str(tmp_path / "distilbert_int8_export.onnx")
+    out, names, params, emb = graphs.write_model(path, graphs.export_encoder_graph, layers=2, vocab=1000)
+    model = OnnxParser.parse_file(path)
+    ops = set(model.list_unique_operators())
+    assert {"Shape", "Unsqueeze", "Concat", "Slice", "Equal", "Expand", "Where", "Pow", "ReduceMean",
+            "Sqrt", "DequantizeLinear", "Gather"} <= ops
+    ex = GpuGraphExecutor.from_model(model)
+    ids, mask = graphs.export_inputs(4, 32, 1000)
+    got = ex.run({"input_ids": ids, "attention_mask": mask}, wanted(names))
+    check_node_by_node(got, names, params, emb, ids, mask)
+    # the padding matters: the same ids unmasked give another context
+    got2 = ex.run({"input_ids": ids, "attention_mask": np.ones_like(mask)}, [names["layers"][0]["ctx"]])
+    assert not np.array_equal(got2[names["layers"][0]["ctx"]], got[names["layers"][0]["ctx"]])
+    # every reshape target and mask shape came from the host: no node of the shape arithmetic
+    # runs as a kernel, and the quantized linears / LayerNorms still fuse
+    pats = [e.pattern for e in ex.plan()[0] if e.kind == "FusedHead"]
+    assert pats.count("DecomposedLayerNorm") == 1 + 2 * 2 and pats.count("QuantizedLinear") == 6 * 2
+
+
+def test_export_model_full_size():
+    cfg = graphs.ENCODER
+    B, S, layers = cfg["batch"], cfg["seq"], cfg["layers"]
+    ex = GpuGraphExecutor()
+    out, names, params, emb = graphs.export_encoder_graph(ex, layers=layers)
+    ids, mask = graphs.export_inputs(B, S)
+    feeds = {"input_ids": torch.from_numpy(ids).cuda(), "attention_mask": torch.from_numpy(mask).cuda()}
+    got = ex.run(feeds, wanted(names))
+    rows = [(0, 8), (B * S // 2 + 3, B * S // 2 + 11), (B * S - 8, B * S)]
+    check_node_by_node(got, names, params, emb, ids, mask, rows=rows)
+    assert np.all(np.isfinite(got[out]))
+    # captured with only the final output requested (heads then quantize their own outputs
+    # for the next DQL where they can): every replay bit-identical to the eager run
+    ex2 = GpuGraphExecutor()
+    graphs.export_encoder_graph(ex2, layers=layers)
+    ex2.capture(feeds, [out])
+    for _ in range(2):
+        ex2.replay()
+        rep = ex2.outputs([out])[out].cpu().numpy()
+        ex2.check_status()
+        assert_bits(rep, got[out], "captured replay vs eager")
