@@ -399,6 +399,11 @@ struct AttnArgs {
     unsigned* q_sync;
     unsigned long long q_wait;  // exchange wait limit, wall-clock ticks
     unsigned q_poison;          // test hook: a tag no block publishes
+    // padding mask (an export's Where(mask, fill, scores) before the Softmax): key j of batch
+    // b is masked when mask[b * mask_bs + j] != 0, its score then replaced by `fill`; null: none
+    const uint8_t* mask;
+    int64_t mask_bs;
+    float fill;
 };
 
 __device__ __forceinline__ float apply_scale(float x, const AttnArgs& a) {
@@ -418,6 +423,7 @@ __device__ __forceinline__ float f4c(const float4& v, int e) {
 template <bool QOUT>
 __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float lds[ATT_LDS_FLOATS];
+    __shared__ uint8_t kmask[ATT_S];
     unsigned tag0 = 0;  // the exchange's tag, read early to hide its latency
     if (QOUT && threadIdx.x == 0) tag0 = icx::qx::read_tag(a.q_sync);
     // The two halves of a (batch, head) are blocks g and g + 8 of a group of 16, which the
@@ -460,6 +466,7 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; ++u)
         *reinterpret_cast<float4*>(lds + (u * 16 + (t >> 4)) * K_STRIDE + c4) = kr[u];
+    if (a.mask && t < S) kmask[t] = a.mask[(int64_t)b * a.mask_bs + t];  // read after the barrier below
     if (a.scale_q) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -488,6 +495,7 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
             const int key = 16 * kt + 4 * lg + r;
             float x = a.scale_q ? st[kt][r] : apply_scale(st[kt][r], a);
             if (key >= S) x = -INFINITY;
+            else if (a.mask && kmask[key]) x = a.fill;  // masked_fill after the scale, as exported
             st[kt][r] = x;
             m = fmaxf(m, x);
         }
@@ -784,7 +792,7 @@ namespace {
 // Shape checks and kernel arguments shared by the f32 and the quantized-output launches.
 int attention_args(const float* q, const float* k, const float* v, size_t B, size_t S, size_t H, size_t D,
                    size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale, int scale_div, int scale_q,
-                   AttnArgs* a, size_t* blocks) {
+                   const icx::AttnMask* mask, AttnArgs* a, size_t* blocks) {
     if (!q || !k || !v) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention: null pointer argument");
     if (D != (size_t)ATT_D || S == 0 || S > (size_t)ATT_S)
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention: head size %zu / sequence %zu unsupported (D = 64, S <= 128)", D, S);
@@ -809,6 +817,11 @@ int attention_args(const float* q, const float* k, const float* v, size_t B, siz
     a->scale_div = scale_div ? 1 : 0;
     a->scale_q = scale_q ? 1 : 0;
     a->qsplit = (int)per;
+    if (mask && mask->keys) {
+        a->mask = mask->keys;
+        a->mask_bs = mask->batch_stride;
+        a->fill = mask->fill;
+    }
     // a power-of-two scale whose reciprocal is a normal float: x / scale == x * (1 / scale)
     int e = 0;
     const float m = std::frexp(scale, &e);
@@ -823,12 +836,12 @@ int attention_args(const float* q, const float* k, const float* v, size_t B, siz
 
 int icx::attention_f32(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
                        size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
-                       int scale_div, int scale_q, float* out, float2* part, int* n_part) {
+                       int scale_div, int scale_q, const AttnMask* mask, float* out, float2* part, int* n_part) {
     if (n_part) *n_part = 0;
     if (!out) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention: null pointer argument");
     AttnArgs a;
     size_t blocks;
-    int rc = attention_args(q, k, v, B, S, H, D, ldq, ldk, ldv, ldo, scale, scale_div, scale_q, &a, &blocks);
+    int rc = attention_args(q, k, v, B, S, H, D, ldq, ldk, ldv, ldo, scale, scale_div, scale_q, mask, &a, &blocks);
     if (rc) return rc;
     if (blocks == 0) return ICX_OK;
     a.out = out;
@@ -842,13 +855,14 @@ int icx::attention_f32(hipStream_t s, const float* q, const float* k, const floa
 
 int icx::attention_dql(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
                        size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
-                       int scale_div, int scale_q, uint8_t* y, float* y_scale, uint8_t* y_zp, unsigned* sync) {
+                       int scale_div, int scale_q, const AttnMask* mask, uint8_t* y, float* y_scale,
+                       uint8_t* y_zp, unsigned* sync) {
     if (!y || !y_scale || !y_zp || !sync) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention+DQL: null pointer argument");
     if (ldo % 16 || !icx::aligned16(y))
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention+DQL: the u8 rows must keep 16-byte alignment");
     AttnArgs a;
     size_t blocks;
-    int rc = attention_args(q, k, v, B, S, H, D, ldq, ldk, ldv, ldo, scale, scale_div, scale_q, &a, &blocks);
+    int rc = attention_args(q, k, v, B, S, H, D, ldq, ldk, ldv, ldo, scale, scale_div, scale_q, mask, &a, &blocks);
     if (rc) return rc;
     if (blocks == 0 || blocks > (size_t)icx::kQoutMaxBlocks)
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention+DQL: %zu blocks outside the exchange's 1..%d", blocks,
@@ -886,5 +900,5 @@ extern "C" int icx_attention_f32(icx_stream_t stream, const float* q, const floa
                                  int scale_div, int scale_q, float* out) {
     icx::clear_error();
     return icx::attention_f32(reinterpret_cast<hipStream_t>(stream), q, k, v, B, S, H, D, ldq, ldk, ldv, ldo,
-                              scale, scale_div, scale_q, out, nullptr, nullptr);
+                              scale, scale_div, scale_q, nullptr, out, nullptr, nullptr);
 }

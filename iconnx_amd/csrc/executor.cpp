@@ -168,7 +168,10 @@ struct PlannedOp {
     int64_t heads = 0, head_dim = 0;
     float scale = 1.0f;
     bool scale_div = false, scale_q = false;
-    std::string q_shape, k_shape, v_shape, o_shape;  // Reshape shape initializers
+    std::string q_shape, k_shape, v_shape, o_shape;  // Reshape targets (initializers, or computed at run)
+    std::string mask;        // padding mask (Where before the Softmax) broadcasting as [B, 1, 1, S], or ""
+    std::string mask_shape;  // the absorbed Expand's target when not the scores' own Shape, or ""
+    float fill = 0.0f;       // the score a masked key takes
     // AddLayerNorm, DecomposedLayerNorm: LN(x + res); the decomposed form may lack scale / bias
     std::string ln_x, ln_res, ln_scale, ln_bias;
     float eps = 1e-5f;
@@ -1093,19 +1096,50 @@ class Planner {
     }
 
     // [B,S,H*D] --Reshape--> [B,S,H,D] --Transpose(perm)--> ; returns the Reshape input
+    // t = Transpose(perm)(Reshape(src, shape)), or the same permutation as two Transposes in a
+    // row (an export writes k.transpose(1, 2).transpose(2, 3)); the shape is a 4-element Int64
+    // initializer or a tensor computed at run time (checked then).
     bool split_heads(const std::string& t, std::initializer_list<int64_t> perm, std::string* src,
                      std::string* shape, std::vector<int>& mem) const {
+        const std::vector<int64_t> want(perm);
         const int ti = producer(t);
-        if (!is_op(ti, "Transpose") || !has_perm(ti, perm) || sole_consumer(t) < 0) return false;
-        const int ri = producer(nodes_[ti].in[0]);
-        if (!is_op(ri, "Reshape") || nodes_[ri].in.size() != 2 || sole_consumer(nodes_[ti].in[0]) != ti)
-            return false;
+        if (!is_op(ti, "Transpose") || sole_consumer(t) < 0) return false;
+        auto pa = nodes_[ti].iattrs.find("perm");
+        if (pa == nodes_[ti].iattrs.end() || pa->second.size() != 4) return false;
+        std::vector<int> m = {ti};
+        std::string r_out = nodes_[ti].in[0];
+        if (pa->second != want) {  // Transpose(p2)(Transpose(p1)(.)): out dim d = in dim p1[p2[d]]
+            const int t1 = producer(r_out);
+            if (!is_op(t1, "Transpose") || sole_consumer(r_out) != ti) return false;
+            auto p1 = nodes_[t1].iattrs.find("perm");
+            if (p1 == nodes_[t1].iattrs.end() || p1->second.size() != 4) return false;
+            std::vector<int64_t> c(4);
+            for (int d = 0; d < 4; ++d) {
+                const int64_t j = pa->second[d];
+                if (j < 0 || j > 3) return false;
+                c[d] = p1->second[(size_t)j];
+            }
+            if (c != want) return false;
+            m.push_back(t1);
+            r_out = nodes_[t1].in[0];
+        }
+        const int ri = producer(r_out);
+        if (!is_op(ri, "Reshape") || nodes_[ri].in.size() != 2 || sole_consumer(r_out) != m.back()) return false;
         auto sh = g_.inits.find(nodes_[ri].in[1]);
-        if (sh == g_.inits.end() || sh->second.dtype != ICX_I64 || numel(sh->second.shape) != 4) return false;
+        if (sh != g_.inits.end() && (sh->second.dtype != ICX_I64 || numel(sh->second.shape) != 4)) return false;
         *src = nodes_[ri].in[0];
         *shape = nodes_[ri].in[1];
-        mem.push_back(ti);
+        mem.insert(mem.end(), m.begin(), m.end());
         mem.push_back(ri);
+        return true;
+    }
+    // Every reader of t is one of `ok` (and t is not a live output).
+    bool only_read_by(const std::string& t, std::initializer_list<int> ok) const {
+        if (outs_.count(t)) return false;
+        auto it = gi_.consumers.find(t);
+        if (it == gi_.consumers.end()) return false;
+        for (int c : it->second)
+            if (std::find(ok.begin(), ok.end(), c) == ok.end()) return false;
         return true;
     }
 
@@ -1116,20 +1150,49 @@ class Planner {
         const int64_t axis = sm.attr_or("axis", -1);
         if (axis != -1 && axis != 3) return false;
         std::vector<int> m;
-        // scores scale: Div / Mul by a scalar, on the scores or on Q
         std::string s = sm.in[0];
+        int next = si;  // the member that reads s
+        // padding mask: Where(cond, fill, scores) read only by the Softmax, fill a static scalar;
+        // cond = Expand(mask, shape) — absorbed, with a Shape of the scores feeding it — or the
+        // mask itself (checked at run time to broadcast as [B, 1, 1, S])
+        int shape_reader = -1;
+        const int wi = producer(s);
+        if (is_op(wi, "Where") && nodes_[wi].in.size() == 3 && sole_consumer(s) == si &&
+            static_scalar(nodes_[wi].in[1], &head.fill)) {
+            std::string cond = nodes_[wi].in[0];
+            const int ei = producer(cond);
+            if (is_op(ei, "Expand") && nodes_[ei].in.size() == 2 && sole_consumer(cond) == wi) {
+                const int shi = producer(nodes_[ei].in[1]);
+                if (is_op(shi, "Shape") && nodes_[shi].in.size() == 1 && nodes_[shi].in[0] == nodes_[wi].in[2] &&
+                    !nodes_[shi].attr.count("start") && !nodes_[shi].attr.count("end") &&
+                    sole_consumer(nodes_[ei].in[1]) == ei) {
+                    m.push_back(shi);
+                    shape_reader = shi;
+                } else {
+                    head.mask_shape = nodes_[ei].in[1];  // must equal the scores' shape at run time
+                }
+                m.push_back(ei);
+                cond = nodes_[ei].in[0];
+            }
+            head.mask = cond;
+            m.push_back(wi);
+            s = nodes_[wi].in[2];
+            next = wi;
+        }
+        // scores scale: Div / Mul by a scalar, on the scores or on Q
         bool scaled = false;
         int pi = producer(s);
-        if ((is_op(pi, "Div") || is_op(pi, "Mul")) && nodes_[pi].in.size() == 2 && sole_consumer(s) == si &&
-            static_scalar(nodes_[pi].in[1], &head.scale)) {
+        if ((is_op(pi, "Div") || is_op(pi, "Mul")) && nodes_[pi].in.size() == 2 &&
+            only_read_by(s, {next, shape_reader}) && static_scalar(nodes_[pi].in[1], &head.scale)) {
             head.scale_div = nodes_[pi].op == "Div";
             head.scale_q = false;
             scaled = true;
             m.push_back(pi);
             s = nodes_[pi].in[0];
+            next = pi;
         }
         const int m1 = producer(s);
-        if (!is_op(m1, "MatMul") || nodes_[m1].in.size() != 2 || sole_consumer(s) < 0) return false;
+        if (!is_op(m1, "MatMul") || nodes_[m1].in.size() != 2 || !only_read_by(s, {next, shape_reader})) return false;
         m.push_back(m1);
         std::string qa = nodes_[m1].in[0];
         const int qs = producer(qa);
@@ -1157,12 +1220,15 @@ class Planner {
         const int orr = sole_consumer(nodes_[ot].out[0]);
         if (!is_op(orr, "Reshape") || nodes_[orr].in.size() != 2) return false;
         auto osh = g_.inits.find(nodes_[orr].in[1]);
-        if (osh == g_.inits.end() || osh->second.dtype != ICX_I64 || numel(osh->second.shape) != 3) return false;
+        if (osh != g_.inits.end() && (osh->second.dtype != ICX_I64 || numel(osh->second.shape) != 3)) return false;
         m.push_back(ot);
         m.push_back(orr);
-        const int64_t* qsh = reinterpret_cast<const int64_t*>(g_.inits[head.q_shape].data.data());
-        head.heads = qsh[2];
-        head.head_dim = qsh[3];
+        auto qsh = g_.inits.find(head.q_shape);  // else the split is known at run time only
+        if (qsh != g_.inits.end()) {
+            const int64_t* d = reinterpret_cast<const int64_t*>(qsh->second.data.data());
+            head.heads = d[2];
+            head.head_dim = d[3];
+        }
         head.o_shape = nodes_[orr].in[1];
         head.kind = Kind::FusedHead;
         head.pattern = Pattern::Attention;
@@ -1871,17 +1937,6 @@ class Runner {
         return rc;
     }
 
-    int shape_init(const std::string& name, std::vector<int64_t>* v) const {
-        auto it = g_.inits.find(name);
-        if (it == g_.inits.end() || it->second.dtype != ICX_I64) {
-            set_error("Reshape: shape '%s' must be an Int64 initializer", name.c_str());
-            return ICX_ERR_UNSUPPORTED;
-        }
-        const int64_t* p = reinterpret_cast<const int64_t*>(it->second.data.data());
-        v->assign(p, p + numel(it->second.shape));
-        return ICX_OK;
-    }
-
     // Fused attention, or its member nodes when the shapes are outside the kernel.
     int run_attention(const PlannedOp& op) {
         const DevTensor *Q, *K, *V;
@@ -1889,21 +1944,59 @@ class Runner {
         if (!rc) rc = need_f32(op.k, &K, "Attention");
         if (!rc) rc = need_f32(op.v, &V, "Attention");
         if (rc) return rc;
-        bool fused = Q->shape.size() == 3 && Q->shape == K->shape && Q->shape == V->shape && op.head_dim == 64 &&
-                     op.heads > 0 && Q->shape[2] == op.heads * op.head_dim && Q->shape[1] > 0 && Q->shape[1] <= 128;
+        int64_t heads = op.heads, head_dim = op.head_dim;
+        bool fused = Q->shape.size() == 3 && Q->shape == K->shape && Q->shape == V->shape;
+        if (fused && heads == 0) {  // reshape targets computed at run time: the split is Q's
+            std::vector<int64_t> spec, tgt;
+            fused = !host_ints(op.q_shape, &spec, "Attention") && !reshape_target(Q->shape, spec, false, &tgt) &&
+                    tgt.size() == 4;
+            if (fused) {
+                heads = tgt[2];
+                head_dim = tgt[3];
+            }
+        }
+        fused = fused && head_dim == 64 && heads > 0 && Q->shape[2] == heads * head_dim && Q->shape[1] > 0 &&
+                Q->shape[1] <= 128;
         std::vector<int64_t> split = {Q->shape.empty() ? 0 : Q->shape[0], Q->shape.size() > 1 ? Q->shape[1] : 0,
-                                      op.heads, op.head_dim};
+                                      heads, head_dim};
         for (const std::string* sh : {&op.q_shape, &op.k_shape, &op.v_shape}) {
             std::vector<int64_t> spec, tgt;
             if (!fused) break;
-            if (shape_init(*sh, &spec) || reshape_target(Q->shape, spec, false, &tgt) || tgt != split) fused = false;
+            if (host_ints(*sh, &spec, "Attention") || reshape_target(Q->shape, spec, false, &tgt) || tgt != split)
+                fused = false;
         }
         std::vector<int64_t> oshape;
         if (fused) {
             std::vector<int64_t> spec;
-            std::vector<int64_t> full = {Q->shape[0], Q->shape[1], op.heads, op.head_dim};
-            if (shape_init(op.o_shape, &spec) || reshape_target(full, spec, false, &oshape) || oshape != Q->shape)
+            std::vector<int64_t> full = {Q->shape[0], Q->shape[1], heads, head_dim};
+            if (host_ints(op.o_shape, &spec, "Attention") || reshape_target(full, spec, false, &oshape) ||
+                oshape != Q->shape)
                 fused = false;
+        }
+        // the padding mask: one byte per key, [B | 1, 1, 1, S] (right-aligned), every batch row
+        // or one for all; an absorbed Expand must target the scores' shape
+        icx::AttnMask mask;
+        if (fused && !op.mask.empty()) {
+            std::vector<int64_t> ms;
+            int mdt;
+            const int64_t B = Q->shape[0], S = Q->shape[1];
+            fused = shape_of(op.mask, &ms, &mdt) && (mdt == ICX_BOOL || mdt == ICX_U8) && ms.size() <= 4 &&
+                    !ms.empty() && ms.back() == S;
+            while (fused && ms.size() < 4) ms.insert(ms.begin(), 1);
+            fused = fused && ms[1] == 1 && ms[2] == 1 && (ms[0] == 1 || ms[0] == B);
+            if (fused && !op.mask_shape.empty()) {
+                std::vector<int64_t> tgt;
+                fused = !host_ints(op.mask_shape, &tgt, "Attention") &&
+                        tgt == std::vector<int64_t>{B, heads, S, S};
+            }
+            const DevTensor* M = nullptr;
+            if (fused) {
+                rc = need(op.mask, &M, "Attention");
+                if (rc) return rc;
+                mask.keys = static_cast<const uint8_t*>(M->ptr);
+                mask.batch_stride = ms[0] == B && B > 1 ? S : 0;
+                mask.fill = op.fill;
+            }
         }
         icx::clear_error();
         if (!fused) {  // run the decomposed subgraph as the reference does
@@ -1925,8 +2018,9 @@ class Runner {
             if (!rc) rc = alloc(d.out[1], ICX_F32, {}, &QS);
             if (!rc) rc = alloc(d.out[2], ICX_U8, {}, &QZ);
             if (rc) return rc;
-            rc = icx::attention_dql(s_, q, k, v, shape[0], shape[1], op.heads, op.head_dim, hd, hd, hd, hd, op.scale,
-                                    op.scale_div ? 1 : 0, op.scale_q ? 1 : 0, static_cast<uint8_t*>(QY->ptr),
+            rc = icx::attention_dql(s_, q, k, v, shape[0], shape[1], heads, head_dim, hd, hd, hd, hd, op.scale,
+                                    op.scale_div ? 1 : 0, op.scale_q ? 1 : 0, mask.keys ? &mask : nullptr,
+                                    static_cast<uint8_t*>(QY->ptr),
                                     static_cast<float*>(QS->ptr), static_cast<uint8_t*>(QZ->ptr), g_.qsync);
             if (rc == ICX_OK) {
                 g_.dql_done.insert(d.out[0]);
@@ -1943,8 +2037,9 @@ class Runner {
         rc = range_parts(op.out, &part);
         if (rc) return rc;
         int n_part = 0;
-        rc = icx::attention_f32(s_, q, k, v, shape[0], shape[1], op.heads, op.head_dim, hd, hd, hd, hd, op.scale,
-                                op.scale_div ? 1 : 0, op.scale_q ? 1 : 0, static_cast<float*>(O->ptr), part, &n_part);
+        rc = icx::attention_f32(s_, q, k, v, shape[0], shape[1], heads, head_dim, hd, hd, hd, hd, op.scale,
+                                op.scale_div ? 1 : 0, op.scale_q ? 1 : 0, mask.keys ? &mask : nullptr,
+                                static_cast<float*>(O->ptr), part, &n_part);
         if (!rc) record_range(op.out, n_part);
         return rc;
     }

@@ -26,10 +26,19 @@ inline int num_cus() {
 int layer_norm_f32(hipStream_t s, const float* x, const float* residual, size_t rows, size_t cols,
                    const float* scale, const float* bias, float eps, float* y, float2* part, int* n_part);
 
-// icx_attention_f32 with the same partial output.
+// An exported attention's padding mask, Where(mask, fill, scores) before the Softmax with a
+// mask that broadcasts as [B, 1, 1, S]: key j of batch b is masked when keys[b * batch_stride
+// + j] != 0 (batch_stride 0: one row for every batch); a masked score becomes `fill`.
+struct AttnMask {
+    const uint8_t* keys = nullptr;
+    int64_t batch_stride = 0;
+    float fill = 0.0f;
+};
+
+// icx_attention_f32 (mask: null, or an AttnMask) with the same partial output.
 int attention_f32(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
                   size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
-                  int scale_div, int scale_q, float* out, float2* part, int* n_part);
+                  int scale_div, int scale_q, const AttnMask* mask, float* out, float2* part, int* n_part);
 
 // The attention of icx_attention_f32 followed by a DynamicQuantizeLinear of its output, as
 // one launch: y [B * S, row stride ldo] u8, y_scale, y_zp are what the DQL of the f32
@@ -39,7 +48,8 @@ int attention_f32(hipStream_t s, const float* q, const float* k, const float* v,
 // resident at once.
 int attention_dql(hipStream_t s, const float* q, const float* k, const float* v, size_t B, size_t S,
                   size_t H, size_t D, size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale,
-                  int scale_div, int scale_q, uint8_t* y, float* y_scale, uint8_t* y_zp, unsigned* sync);
+                  int scale_div, int scale_q, const AttnMask* mask, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                  unsigned* sync);
 
 // icx_qlinear_f32 with the same partial output.
 int qlinear_f32(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype, int b_packed,

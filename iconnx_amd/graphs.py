@@ -283,9 +283,11 @@ def encoder_graph(ex, layers=6, heads=12, hidden=768, ffn=3072, eps=1e-12, x_nam
 F32_MIN = np.float32(np.finfo(np.float32).min)
 
 
-def add_self_attention_export(ex, x, q, k, v, mask, heads, head_dim, prefix):
+def add_self_attention_export(ex, x, q, k, v, mask, heads, head_dim, prefix, cond=None):
     """MultiHeadSelfAttention over [B, S, H*D] projections q, k, v of ``x`` with the Int64
-    padding mask ``mask`` [B, S] (0 = padding), as exported.  Returns the context name."""
+    padding mask ``mask`` [B, S] (0 = padding), as exported; ``cond`` (a Bool tensor name)
+    replaces the mask's Equal / Reshape / Expand as the Where's condition.  Returns the
+    context name."""
     p = prefix
     cst = lambda n, a: ex.add_initializer("%s.%s" % (p, n), np.asarray(a))  # noqa: E731
     cst("i0", np.array(0, np.int64))
@@ -299,7 +301,7 @@ def add_self_attention_export(ex, x, q, k, v, mask, heads, head_dim, prefix):
     cst("zero", np.array(0, np.int64))
     cst("sqrt_d", np.array(np.sqrt(head_dim), np.float32))
     cst("fmin", F32_MIN)
-    ext = {x, q, k, v, mask}
+    ext = {x, q, k, v, mask, cond}
 
     def n(name, op, ins, outs, attrs=None):  # names local to this block get the prefix
         ex.add_node("%s.%s" % (p, name), op, [i if i in ext else "%s.%s" % (p, i) for i in ins],
@@ -318,12 +320,13 @@ def add_self_attention_export(ex, x, q, k, v, mask, heads, head_dim, prefix):
     n("tr_k2", "Transpose", ["kt"], ["kT"], {"perm": [0, 1, 3, 2]})
     n("scores", "MatMul", ["qs", "kT"], ["s"])
     # mask = (mask == 0).view(bs, 1, 1, k_length).expand_as(scores)
-    n("mask_eq", "Equal", [mask, "zero"], ["meq"])
-    n("mask_shape", "Concat", ["bs_u", "one", "one", "klen_u"], ["mshape"], {"axis": 0})
-    n("mask_view", "Reshape", ["meq", "mshape"], ["m4"])
-    n("shape_s", "Shape", ["s"], ["ss"])
-    n("mask_expand", "Expand", ["m4", "ss"], ["mx"])
-    n("masked_fill", "Where", ["mx", "fmin", "s"], ["sm"])
+    if cond is None:
+        n("mask_eq", "Equal", [mask, "zero"], ["meq"])
+        n("mask_shape", "Concat", ["bs_u", "one", "one", "klen_u"], ["mshape"], {"axis": 0})
+        n("mask_view", "Reshape", ["meq", "mshape"], ["m4"])
+        n("shape_s", "Shape", ["s"], ["ss"])
+        n("mask_expand", "Expand", ["m4", "ss"], ["mx"])
+    n("masked_fill", "Where", [cond if cond is not None else "mx", "fmin", "s"], ["sm"])
     n("softmax", "Softmax", ["sm"], ["pr"], {"axis": -1})
     n("context", "MatMul", ["pr", "vt"], ["c"])
     n("tr_c", "Transpose", ["c"], ["ct"], {"perm": [0, 2, 1, 3]})

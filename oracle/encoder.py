@@ -29,10 +29,11 @@ def gelu_ref(t):
     return mul(mul(t, add(erf(d), np.float32(1.0))), np.float32(0.5))
 
 
-def attention_ref(q, k, v, heads, scale=8.0, scale_q=True, mask=None):
+def attention_ref(q, k, v, heads, scale=8.0, scale_q=True, mask=None, cond=None):
     """The exported self-attention subgraph over [B, S, H*D] tensors; ``mask`` (Int64 [B, S],
     0 = padding) adds the export's masked_fill: Where(Expand(Reshape(Equal(mask, 0),
-    [B, 1, 1, S]), scores' shape), finfo(f32).min, scores) before the Softmax."""
+    [B, 1, 1, S]), scores' shape), finfo(f32).min, scores) before the Softmax; ``cond`` (Bool,
+    broadcasting over [B, H, S, S]) is that Where's condition given directly."""
     B, S, HD = q.shape
     D = HD // heads
     split = lambda t: transpose(np.ascontiguousarray(t).reshape(B, S, heads, D), (0, 2, 1, 3))  # noqa: E731
@@ -43,10 +44,12 @@ def attention_ref(q, k, v, heads, scale=8.0, scale_q=True, mask=None):
     s = matmul_f32(qh.reshape(B * heads, S, D), kt.reshape(B * heads, D, S)).reshape(B, heads, S, S)
     if not scale_q:
         s = div(s, np.float32(scale))
-    if mask is not None:
+    if mask is not None or cond is not None:
         from . import layout
-        m4 = layout.equal(np.asarray(mask, np.int64), np.array(0, np.int64)).reshape(B, 1, 1, S)
-        s = layout.where(layout.expand(m4, s.shape), np.float32(np.finfo(np.float32).min), s)
+        if cond is None:
+            m4 = layout.equal(np.asarray(mask, np.int64), np.array(0, np.int64)).reshape(B, 1, 1, S)
+            cond = layout.expand(m4, s.shape)
+        s = layout.where(cond, np.float32(np.finfo(np.float32).min), s)
     pr = softmax(s)
     ctx = matmul_f32(pr.reshape(B * heads, S, S), vh.reshape(B * heads, S, D)).reshape(B, heads, S, D)
     return transpose(ctx, (0, 2, 1, 3)).reshape(B, S, HD)

@@ -12,7 +12,10 @@ LayerNorm), every DynamicQuantizeLinear (x_q, scale, zero point), every quantize
 every LayerNorm (the LayerNormalization arithmetic: the node-by-node form with Mul(c, c) for
 Pow(c, 2), which the reference's powf matches to the last ulp or within 1e-6); within 1e-6 for
 the GELU linears (device erf / exp) and 1e-5 for the masked attention (fp32 MFMA summation
-order, device exp) — the tolerances of the unmasked encoder's node-by-node test.
+order, device exp) — the tolerances of the unmasked encoder's node-by-node test.  The masked
+attention runs as one fused kernel (the Where / Expand / Shape of the mask and the key's two
+transposes folded into the attention head); the same graph with a sequence past the kernel's
+128, or with a mask that is not per key, runs node by node, also against the oracle.
 """
 import numpy as np
 import pytest
@@ -125,6 +128,7 @@ def test_export_model_from_file(tmp_path):
     # runs as a kernel, and the quantized linears / LayerNorms still fuse
     pats = [e.pattern for e in ex.plan()[0] if e.kind == "FusedHead"]
     assert pats.count("DecomposedLayerNorm") == 1 + 2 * 2 and pats.count("QuantizedLinear") == 6 * 2
+    assert pats.count("Attention") == 2  # the masked attention as one kernel
 
 
 def test_export_model_full_size():
@@ -148,3 +152,56 @@ def test_export_model_full_size():
         rep = ex2.outputs([out])[out].cpu().numpy()
         ex2.check_status()
         assert_bits(rep, got[out], "captured replay vs eager")
+
+
+def attention_graph(cond=False):
+    """q, k, v, x [B, S, H*D] and the Int64 mask through add_self_attention_export; with
+    ``cond`` a Bool [B, 1, S, S] input is the Where's condition instead (not per key)."""
+    ex = GpuGraphExecutor()
+    for n in ("x", "q", "k", "v"):
+        ex.add_input(n, [None, None, H * 64])
+    ex.add_input("mask", [None, None])
+    if cond:
+        ex.add_input("cond", [None, 1, None, None])
+    return ex, graphs.add_self_attention_export(ex, "x", "q", "k", "v", "mask", H, 64, "att",
+                                                cond="cond" if cond else None)
+
+
+def attention_feeds(S, B=6, seed=0):
+    rng = np.random.default_rng(seed + S)
+    q, k, v = (rng.standard_normal((B, S, H * 64)).astype(np.float32) for _ in range(3))
+    x = np.zeros((B, S, H * 64), np.float32)
+    lens = np.array([S, 1, S // 2, 0, S - 1, 3])[:B]
+    mask = (np.arange(S)[None, :] < lens[:, None]).astype(np.int64)
+    return q, k, v, x, mask
+
+
+@pytest.mark.parametrize("S", [128, 77, 130])
+def test_masked_attention_fused_and_fallback(S):
+    """S <= 128: the fused kernel with the per-key mask (a batch whose every key is padding
+    included: a uniform softmax, as the node-by-node Where gives); S = 130: the node-by-node
+    fallback.  Both within 1e-5 of the oracle."""
+    q, k, v, x, mask = attention_feeds(S)
+    ex, ctx = attention_graph()
+    feeds = {n: torch.from_numpy(a).cuda() for n, a in (("x", x), ("q", q), ("k", k), ("v", v), ("mask", mask))}
+    got = ex.run(feeds, [ctx])[ctx]
+    assert [e.pattern for e in ex.plan()[0] if e.kind == "FusedHead"] == ["Attention"]
+    want = ref.attention_ref(q, k, v, H, 8.0, mask=mask)
+    for b in range(len(mask)):
+        assert rel_err(got[b], want[b]) < 1e-5, (S, b)
+
+
+def test_attention_with_a_condition_that_is_not_per_key_runs_node_by_node():
+    """A causal [B, 1, S, S] condition: the head matches, the run-time check sends it node by
+    node (Where broadcast over the heads, Softmax, MatMuls), against the oracle."""
+    S = 96
+    q, k, v, x, mask = attention_feeds(S, B=3)
+    cond = np.broadcast_to(np.triu(np.ones((S, S), np.bool_), 1), (3, 1, S, S)).copy()
+    ex, ctx = attention_graph(cond=True)
+    feeds = {n: torch.from_numpy(a).cuda() for n, a in (("x", x), ("q", q), ("k", k), ("v", v), ("mask", mask),
+                                                        ("cond", cond))}
+    got = ex.run(feeds, [ctx])[ctx]
+    assert [e.pattern for e in ex.plan()[0] if e.kind == "FusedHead"] == ["Attention"]
+    want = ref.attention_ref(q, k, v, H, 8.0, cond=cond)
+    for b in range(3):
+        assert rel_err(got[b], want[b]) < 1e-5, b
