@@ -5,6 +5,7 @@
 #include <type_traits>
 
 #include "chain.hpp"
+#include "internal.hpp"
 
 namespace icx {
 
@@ -139,6 +140,38 @@ gather_rows_kernel(const uint8_t* __restrict__ data, const void* __restrict__ in
     }
 }
 
+// Gather of rows of an 8-bit table [axis_len, cols] followed by its per-tensor
+// DequantizeLinear, in one pass (an INT8 model's embedding lookup): y[r, c] =
+// (float(table[k_r, c]) - float(zp)) * scale with dequantize_kernel's roundings, k_r under
+// gather_rows_kernel's index rules; one wave per output row, four table bytes per lane step.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+gather_dequant_kernel(const T* __restrict__ table, const void* __restrict__ indices, int idx64, size_t n_idx,
+                      size_t axis_len, size_t cols, const float* __restrict__ scale, const T* __restrict__ zp,
+                      float* __restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const size_t waves = (size_t)gridDim.x * (kThreads / 64);
+    const float sc = scale[0], zf = zp ? (float)zp[0] : 0.0f;
+    for (size_t r = (size_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6); r < n_idx; r += waves) {
+        long long k = idx64 ? reinterpret_cast<const long long*>(indices)[r]
+                            : (long long)reinterpret_cast<const int*>(indices)[r];
+        if (k < 0) k += (long long)axis_len;
+        if (k < 0) k = 0;
+        if (k >= (long long)axis_len) k = (long long)axis_len - 1;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(table + (size_t)k * cols);
+        float4* dst = reinterpret_cast<float4*>(y + r * cols);
+        for (size_t c = lane; c < cols / 4; c += 64) {
+            const uint32_t v = src[c];
+            float4 o;
+            o.x = __fmul_rn(__fsub_rn((float)(T)(v & 0xff), zf), sc);
+            o.y = __fmul_rn(__fsub_rn((float)(T)((v >> 8) & 0xff), zf), sc);
+            o.z = __fmul_rn(__fsub_rn((float)(T)((v >> 16) & 0xff), zf), sc);
+            o.w = __fmul_rn(__fsub_rn((float)(T)(v >> 24), zf), sc);
+            dst[c] = o;
+        }
+    }
+}
+
 unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
     size_t b = icx::cdiv(work, per_block);
     if (b < 1) b = 1;
@@ -241,6 +274,30 @@ extern "C" int icx_dequantize_linear_f32(icx_stream_t stream, const void* x, int
             ICX_FAIL(ICX_ERR_DTYPE, "DequantizeLinear: input dtype %d unsupported (must be Int8, UInt8, or Int32)", x_dtype);
     }
     ICX_LAUNCH_CHECK("dequantize_kernel");
+    return ICX_OK;
+}
+
+int icx::gather_dequant_f32(hipStream_t s, const void* table, int dtype, size_t axis_len, size_t cols,
+                            const void* indices, int idx_dtype, size_t n_idx, const float* scale, const void* zp,
+                            float* y) {
+    if (dtype != ICX_U8 && dtype != ICX_I8)
+        ICX_FAIL(ICX_ERR_DTYPE, "Gather+DequantizeLinear: table dtype %d (must be UInt8 or Int8)", dtype);
+    if (idx_dtype != ICX_I64 && idx_dtype != ICX_I32)
+        ICX_FAIL(ICX_ERR_DTYPE, "Gather+DequantizeLinear: indices dtype %d (must be Int64 or Int32)", idx_dtype);
+    if (n_idx == 0 || cols == 0) return ICX_OK;
+    if (axis_len == 0) ICX_FAIL(ICX_ERR_SHAPE, "Gather+DequantizeLinear: %zu indices into an empty table", n_idx);
+    if (!table || !indices || !scale || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "Gather+DequantizeLinear: null pointer");
+    if (cols % 4 || (reinterpret_cast<uintptr_t>(table) & 3) || !icx::aligned16(y))
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "Gather+DequantizeLinear: rows of %zu bytes or unaligned operands", cols);
+    const dim3 grid(grid_for(n_idx, kThreads / 64, 8192)), block(kThreads);
+    const int i64 = idx_dtype == ICX_I64;
+    if (dtype == ICX_U8)
+        hipLaunchKernelGGL(gather_dequant_kernel<uint8_t>, grid, block, 0, s, static_cast<const uint8_t*>(table),
+                           indices, i64, n_idx, axis_len, cols, scale, static_cast<const uint8_t*>(zp), y);
+    else
+        hipLaunchKernelGGL(gather_dequant_kernel<int8_t>, grid, block, 0, s, static_cast<const int8_t*>(table),
+                           indices, i64, n_idx, axis_len, cols, scale, static_cast<const int8_t*>(zp), y);
+    ICX_LAUNCH_CHECK("gather_dequant_kernel");
     return ICX_OK;
 }
 

@@ -44,16 +44,18 @@ __device__ __forceinline__ float ln_in(const float* x, const float* res, size_t 
     return res ? __fadd_rn(x[i], res[i]) : x[i];
 }
 
-// 32 rows per block: 8 rows per wave, 8 lanes per row.
+// 32 rows per block: 8 rows per wave, 8 lanes per row.  res_rows != 0: the residual has that
+// many rows, row r of x adding residual row r % res_rows (a [S, cols] table broadcast over a
+// [B, S, cols] x, e.g. position embeddings).
 __global__ void __launch_bounds__(kThreads)
-layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t rows,
+layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t res_rows, size_t rows,
                   size_t cols, const float* __restrict__ scale, const float* __restrict__ bias,
                   float eps, float* __restrict__ y) {
     const int lane = threadIdx.x & 63, j = lane & 7;
     const size_t row = (size_t)blockIdx.x * 32 + (threadIdx.x >> 3);
     if (row >= rows) return;  // a whole 8-lane group leaves together
     const float* xr = x + row * cols;
-    const float* rr = res ? res + row * cols : nullptr;
+    const float* rr = res ? res + (res_rows ? row % res_rows : row) * cols : nullptr;
     const size_t n8 = cols / 8 * 8;
     const float fcols = (float)cols;
     // mean
@@ -94,7 +96,7 @@ layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ res, si
 // per block where the range partials allow it.
 template <int PER, int ROWS>
 __global__ void __launch_bounds__(256)
-layer_norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t rows,
+layer_norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ res, size_t res_rows, size_t rows,
                         const float* __restrict__ scale, const float* __restrict__ bias, float eps,
                         float* __restrict__ y, float2* __restrict__ part) {
     constexpr int cols = 8 * PER, C4 = cols / 4, STRIDE = cols + 8;
@@ -106,7 +108,7 @@ layer_norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ re
     const size_t row0 = (size_t)blockIdx.x * ROWS;
     const int nr = (int)(rows - row0 < ROWS ? rows - row0 : ROWS);
     const float4* x4 = reinterpret_cast<const float4*>(x + row0 * cols);
-    const float4* r4 = res ? reinterpret_cast<const float4*>(res + row0 * cols) : nullptr;
+    const float4* r4 = res ? reinterpret_cast<const float4*>(res) : nullptr;
     {
         float4 v[PL], w[PL];
 #pragma unroll
@@ -118,7 +120,8 @@ layer_norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ re
 #pragma unroll
             for (int u = 0; u < PL; ++u) {
                 const int q = t + u * 256;
-                if (q < nr * C4) w[u] = r4[q];
+                if (q < nr * C4)
+                    w[u] = r4[res_rows ? ((row0 + q / C4) % res_rows) * C4 + q % C4 : row0 * C4 + q];
             }
         }
 #pragma unroll
@@ -445,6 +448,8 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
     const int lq = lane & 15, lg = lane >> 4;
     const int qi = half * ATT_QB + 16 * w + lq;  // this lane's query row
 
+    // the padding mask's byte for key t first: its load is then not the last one to land
+    const uint8_t mk = a.mask && t < S ? a.mask[(int64_t)b * a.mask_bs + t] : (uint8_t)0;
     // every load in flight at once: K and V of (b, h) (rows past S are zero), and this lane's
     // Q row segment, dims [16 lg, 16 lg + 16)
     float4 kr[8], vr[8], qr[4];
@@ -466,7 +471,7 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; ++u)
         *reinterpret_cast<float4*>(lds + (u * 16 + (t >> 4)) * K_STRIDE + c4) = kr[u];
-    if (a.mask && t < S) kmask[t] = a.mask[(int64_t)b * a.mask_bs + t];  // read after the barrier below
+    if (a.mask && t < S) kmask[t] = mk;  // read after the barrier below
     if (a.scale_q) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -621,12 +626,14 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
 
 
 template <int PER>
-void launch_ln_rows(bool rows4, dim3 grid, hipStream_t s, const float* x, const float* res, size_t rows,
-                    const float* scale, const float* bias, float eps, float* y, float2* part) {
+void launch_ln_rows(bool rows4, dim3 grid, hipStream_t s, const float* x, const float* res, size_t res_rows,
+                    size_t rows, const float* scale, const float* bias, float eps, float* y, float2* part) {
     if (rows4)
-        hipLaunchKernelGGL((layer_norm_rows_kernel<PER, 4>), grid, dim3(256), 0, s, x, res, rows, scale, bias, eps, y, part);
+        hipLaunchKernelGGL((layer_norm_rows_kernel<PER, 4>), grid, dim3(256), 0, s, x, res, res_rows, rows, scale,
+                           bias, eps, y, part);
     else
-        hipLaunchKernelGGL((layer_norm_rows_kernel<PER, 8>), grid, dim3(256), 0, s, x, res, rows, scale, bias, eps, y, part);
+        hipLaunchKernelGGL((layer_norm_rows_kernel<PER, 8>), grid, dim3(256), 0, s, x, res, res_rows, rows, scale,
+                           bias, eps, y, part);
 }
 
 unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
@@ -637,13 +644,15 @@ unsigned grid_for(size_t work, size_t per_block, unsigned cap) {
 
 }  // namespace
 
-int icx::layer_norm_f32(hipStream_t s, const float* x, const float* residual, size_t rows, size_t cols,
-                        const float* scale, const float* bias, float eps, float* y, float2* part,
+int icx::layer_norm_f32(hipStream_t s, const float* x, const float* residual, size_t res_rows, size_t rows,
+                        size_t cols, const float* scale, const float* bias, float eps, float* y, float2* part,
                         int* n_part) {
     if (n_part) *n_part = 0;
     if (!x || !y) ICX_FAIL(ICX_ERR_INVALID_ARG, "LayerNormalization: null pointer argument");
     if (cols == 0 && rows) ICX_FAIL(ICX_ERR_SHAPE, "LayerNormalization: empty normalized axis");
     if (rows == 0) return ICX_OK;
+    if (res_rows && (!residual || rows % res_rows))
+        ICX_FAIL(ICX_ERR_SHAPE, "LayerNormalization: %zu rows over a residual of %zu rows", rows, res_rows);
     // partials only from the LDS-staged kernel, one per block: blocks of 4 rows while their
     // partials fit, else of 8
     const bool rows4 = icx::cdiv(rows, 4) <= (size_t)icx::kMaxRangeParts;
@@ -653,13 +662,13 @@ int icx::layer_norm_f32(hipStream_t s, const float* x, const float* residual, si
     const bool a16 = icx::aligned16(x) && icx::aligned16(y) && icx::aligned16(scale) &&
                      icx::aligned16(bias) && (!residual || icx::aligned16(residual));
     switch (a16 ? cols : 0) {
-        case 512: launch_ln_rows<64>(rows4, g8, s, x, residual, rows, scale, bias, eps, y, pp); break;
-        case 768: launch_ln_rows<96>(rows4, g8, s, x, residual, rows, scale, bias, eps, y, pp); break;
-        case 1024: launch_ln_rows<128>(rows4, g8, s, x, residual, rows, scale, bias, eps, y, pp); break;
+        case 512: launch_ln_rows<64>(rows4, g8, s, x, residual, res_rows, rows, scale, bias, eps, y, pp); break;
+        case 768: launch_ln_rows<96>(rows4, g8, s, x, residual, res_rows, rows, scale, bias, eps, y, pp); break;
+        case 1024: launch_ln_rows<128>(rows4, g8, s, x, residual, res_rows, rows, scale, bias, eps, y, pp); break;
         default:
             pp = nullptr;
             hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)icx::cdiv(rows, 32)), dim3(kThreads), 0, s, x,
-                               residual, rows, cols, scale, bias, eps, y);
+                               residual, res_rows, rows, cols, scale, bias, eps, y);
     }
     ICX_LAUNCH_CHECK("layer_norm_kernel");
     if (pp && n_part) *n_part = (int)g8.x;
@@ -670,7 +679,7 @@ extern "C" int icx_layer_norm_f32(icx_stream_t stream, const float* x, const flo
                                   size_t rows, size_t cols, const float* scale,
                                   const float* bias, float eps, float* y) {
     icx::clear_error();
-    return icx::layer_norm_f32(reinterpret_cast<hipStream_t>(stream), x, residual, rows, cols, scale, bias,
+    return icx::layer_norm_f32(reinterpret_cast<hipStream_t>(stream), x, residual, 0, rows, cols, scale, bias,
                                eps, y, nullptr, nullptr);
 }
 

@@ -129,7 +129,8 @@ enum class Pattern {
     Gelu,
     Attention,
     AddLayerNorm,
-    DecomposedLayerNorm
+    DecomposedLayerNorm,
+    GatherDequantize
 };
 
 const char* kind_name(Kind k) {
@@ -148,6 +149,7 @@ const char* pattern_name(Pattern p) {
         case Pattern::Attention: return "Attention";
         case Pattern::AddLayerNorm: return "AddLayerNorm";
         case Pattern::DecomposedLayerNorm: return "DecomposedLayerNorm";
+        case Pattern::GatherDequantize: return "GatherDequantize";
         default: return "-";
     }
 }
@@ -157,7 +159,9 @@ struct PlannedOp {
     Node node;
     Kind kind = Kind::Regular;
     Pattern pattern = Pattern::None;
-    std::string a, w, a_zp, w_zp;  // QuantizedLinear: the MatMulInteger operands
+    std::string a, w, a_zp, w_zp;  // QuantizedLinear: the MatMulInteger operands (GatherDequantize:
+                                   // indices, table, -, zero point)
+    std::string w_scale;           // GatherDequantize: the per-tensor scale
     bool w_zp_folded = false;      // all-zero weight zero point dropped
     std::string chain_in, out;     // chain input (elementwise heads) and fused output
     std::vector<Step> steps;
@@ -383,6 +387,7 @@ class Planner {
         nodes_ = live_nodes();
         int rc = topo_sort();
         if (rc) return rc;
+        merge_duplicates();
         gi_ = GraphIndex(nodes_);
         outs_.clear();
         outs_.insert(g_.live_outputs.begin(), g_.live_outputs.end());
@@ -402,7 +407,7 @@ class Planner {
                     case 0: hit = match_attention(i, head, mem); break;
                     case 1: hit = match_qlinear(i, head, mem); break;
                     case 2: hit = match_add_layer_norm(i, head, mem) || match_layer_norm_chain(i, head, mem); break;
-                    default: hit = match_chain(i, head, mem); break;
+                    default: hit = match_gather_dequant(i, head, mem) || match_chain(i, head, mem); break;
                 }
                 if (!hit) continue;
                 // The head runs at its last member's position: every operand of every member
@@ -417,7 +422,7 @@ class Planner {
                     ops[m].kind = Kind::Skip;
                 }
                 ops[i].kind = Kind::Skip;
-                if (head.pattern == Pattern::Attention) {
+                if (head.pattern == Pattern::Attention || head.pattern == Pattern::GatherDequantize) {
                     std::vector<int> all = mem;
                     all.push_back(i);
                     std::sort(all.begin(), all.end());
@@ -513,6 +518,65 @@ class Planner {
     }
 
    private:
+    // Shape / mask plumbing nodes with the same op, inputs and attributes compute the same
+    // outputs: keep the first, point the readers of the others at its outputs (an export
+    // recomputes the padding mask's Equal(mask, 0) in every layer).  Only those ops: a shared
+    // node of a fusion pattern (the x_scale * w_scale Mul of Q, K and V, say) would stop the
+    // pattern from owning it.  A node whose output the caller asked for stays.  Runs on the
+    // topologically sorted list, so the kept node precedes every reader of the ones it replaces.
+    static bool mergeable(const std::string& op) {
+        return op == "Shape" || op == "Equal" || op == "Cast" || op == "Slice" || op == "Concat" ||
+               op == "Unsqueeze" || op == "Squeeze" || op == "Gather" || op == "Expand" || op == "Where";
+    }
+    void merge_duplicates() {
+        std::map<std::string, std::string> rename;
+        std::map<std::string, size_t> seen;
+        std::set<std::string> live(g_.live_outputs.begin(), g_.live_outputs.end());
+        std::vector<Node> kept;
+        for (Node n : nodes_) {
+            for (auto& i : n.in) {
+                auto r = rename.find(i);
+                if (r != rename.end()) i = r->second;
+            }
+            std::ostringstream key;
+            key << n.op << '\x1f' << n.in.size() << '\x1f' << n.out.size();
+            for (auto& i : n.in) {  // a small initializer by its value (exports repeat constants)
+                auto it = g_.inits.find(i);
+                if (it != g_.inits.end() && it->second.data.size() <= 64) {
+                    key << "\x1f#" << it->second.dtype << shape_str(it->second.shape);
+                    for (uint8_t b : it->second.data) key << '.' << (int)b;
+                } else {
+                    key << '\x1f' << i;
+                }
+            }
+            for (auto& a : n.attr) key << '\x1e' << a.first << '=' << a.second;
+            for (auto& a : n.fattr) {
+                uint64_t b;
+                std::memcpy(&b, &a.second, 8);
+                key << '\x1d' << a.first << '=' << b;
+            }
+            for (auto& a : n.iattrs) {
+                key << '\x1c' << a.first << '=';
+                for (int64_t v : a.second) key << v << ',';
+            }
+            bool is_live = !mergeable(n.op);
+            for (auto& o : n.out) is_live = is_live || live.count(o);
+            auto it = seen.find(key.str());
+            bool same_outs = it != seen.end();
+            for (size_t j = 0; same_outs && j < n.out.size(); ++j)
+                same_outs = n.out[j].empty() || !kept[it->second].out[j].empty();
+            if (same_outs && !is_live) {
+                const Node& k = kept[it->second];
+                for (size_t j = 0; j < n.out.size(); ++j)
+                    if (!n.out[j].empty()) rename[n.out[j]] = k.out[j];
+                continue;
+            }
+            if (it == seen.end()) seen[key.str()] = kept.size();
+            kept.push_back(std::move(n));
+        }
+        nodes_ = std::move(kept);
+    }
+
     icx_graph& g_;
     GraphIndex gi_;
     std::vector<Node> nodes_;
@@ -1143,6 +1207,39 @@ class Planner {
         return true;
     }
 
+    // DequantizeLinear(Gather(table, indices, axis 0), scale, [zp]) of an 8-bit table
+    // initializer [V, D] with a per-tensor scale and zero point, the Gather read only by the
+    // DequantizeLinear: an INT8 model's embedding lookup, one launch (the members run one by
+    // one when the run-time shapes fall outside the kernel).
+    bool match_gather_dequant(int di, PlannedOp& head, std::vector<int>& mem) {
+        const Node& dq = nodes_[di];
+        if (dq.op != "DequantizeLinear" || dq.in.size() < 2 || dq.in.size() > 3 || dq.out.size() != 1) return false;
+        const int gi = producer(dq.in[0]);
+        if (!is_op(gi, "Gather") || nodes_[gi].in.size() != 2 || sole_consumer(dq.in[0]) != di ||
+            nodes_[gi].attr_or("axis", 0) != 0)
+            return false;
+        auto tb = g_.inits.find(nodes_[gi].in[0]);
+        if (tb == g_.inits.end() || (tb->second.dtype != ICX_U8 && tb->second.dtype != ICX_I8) ||
+            tb->second.shape.size() != 2)
+            return false;
+        auto sc = g_.inits.find(dq.in[1]);
+        if (sc == g_.inits.end() || sc->second.dtype != ICX_F32 || numel(sc->second.shape) != 1) return false;
+        if (dq.in.size() == 3 && !dq.in[2].empty()) {
+            auto zp = g_.inits.find(dq.in[2]);
+            if (zp == g_.inits.end() || zp->second.dtype != tb->second.dtype || numel(zp->second.shape) != 1)
+                return false;
+            head.w_zp = dq.in[2];
+        }
+        head.w = nodes_[gi].in[0];
+        head.a = nodes_[gi].in[1];
+        head.w_scale = dq.in[1];
+        head.kind = Kind::FusedHead;
+        head.pattern = Pattern::GatherDequantize;
+        head.out = dq.out[0];
+        mem = {gi};
+        return true;
+    }
+
     // Anchored at the Softmax of a BERT self-attention.
     bool match_attention(int si, PlannedOp& head, std::vector<int>& mem) {
         const Node& sm = nodes_[si];
@@ -1493,6 +1590,7 @@ class Runner {
                 case Pattern::DecomposedLayerNorm:
                     return run_layer_norm(op.ln_x, op.ln_res, op.ln_scale, op.ln_bias, op.eps, op.out,
                                           pattern_name(op.pattern));
+                case Pattern::GatherDequantize: return run_gather_dequant(op);
                 default: return run_chain(op.chain_in, op.steps, op.out, pattern_name(op.pattern));
             }
         }
@@ -1937,6 +2035,35 @@ class Runner {
         return rc;
     }
 
+    // Gather + DequantizeLinear of an 8-bit table in one launch, or the two nodes.
+    int run_gather_dequant(const PlannedOp& op) {
+        const DevTensor *T, *I, *S, *Z = nullptr;
+        int rc = need(op.w, &T, "GatherDequantize");
+        if (!rc) rc = need(op.a, &I, "GatherDequantize");
+        if (!rc) rc = need(op.w_scale, &S, "GatherDequantize");
+        if (!rc && !op.w_zp.empty()) rc = need(op.w_zp, &Z, "GatherDequantize");
+        if (rc) return rc;
+        if ((I->dtype == ICX_I64 || I->dtype == ICX_I32) && T->shape.size() == 2 && T->shape[1] % 4 == 0) {
+            std::vector<int64_t> oshape = I->shape;
+            oshape.push_back(T->shape[1]);
+            const void *tb = T->ptr, *ix = I->ptr, *zp = Z ? Z->ptr : nullptr;
+            const float* sc = static_cast<const float*>(S->ptr);
+            const int tdt = T->dtype, idt = I->dtype;
+            const size_t V = (size_t)T->shape[0], D = (size_t)T->shape[1], n = (size_t)numel(I->shape);
+            DevTensor* Y;
+            rc = alloc(op.out, ICX_F32, oshape, &Y);
+            if (rc) return rc;
+            rc = icx::gather_dequant_f32(s_, tb, tdt, V, D, ix, idt, n, sc, zp, static_cast<float*>(Y->ptr));
+            if (rc != ICX_ERR_UNSUPPORTED) return rc;
+            icx::clear_error();
+        }
+        for (const Node& m : op.sub) {
+            rc = run_node(m);
+            if (rc) return rc;
+        }
+        return ICX_OK;
+    }
+
     // Fused attention, or its member nodes when the shapes are outside the kernel.
     int run_attention(const PlannedOp& op) {
         const DevTensor *Q, *K, *V;
@@ -2052,12 +2179,24 @@ class Runner {
         if (!rc && !sn.empty()) rc = need_f32(sn, &S, who);
         if (!rc && !bn.empty()) rc = need_f32(bn, &B, who);
         if (rc) return rc;
+        size_t res_rows = 0;
         if (R && R->shape != X->shape) {
-            // the Add broadcasts: materialise it, then normalise
-            const std::string tmp = out + "::sum";
-            rc = binary_f32_into(ICX_OP_ADD, xn, resn, tmp, who);
-            if (rc) return rc;
-            return run_layer_norm(tmp, "", sn, bn, eps, out, who);
+            // a residual of X's trailing shape (leading unit dims aside: position embeddings
+            // [1, S, D] over [B, S, D]) is read row-periodically by the kernel; any other
+            // broadcast is materialised first
+            std::vector<int64_t> rs = R->shape;
+            while (!rs.empty() && rs.front() == 1 && rs.size() > 1) rs.erase(rs.begin());
+            bool periodic = !X->shape.empty() && rs.size() <= X->shape.size() && !rs.empty() &&
+                            std::equal(rs.begin(), rs.end(), X->shape.end() - (ptrdiff_t)rs.size()) &&
+                            numel(rs) > 0;
+            if (periodic) {
+                res_rows = (size_t)(numel(rs) / X->shape.back());
+            } else {
+                const std::string tmp = out + "::sum";
+                rc = binary_f32_into(ICX_OP_ADD, xn, resn, tmp, who);
+                if (rc) return rc;
+                return run_layer_norm(tmp, "", sn, bn, eps, out, who);
+            }
         }
         if (X->shape.empty()) {
             set_error("%s: input must have at least one axis", who);
@@ -2080,7 +2219,7 @@ class Runner {
         rc = range_parts(out, &part);
         if (rc) return rc;
         int n_part = 0;
-        rc = icx::layer_norm_f32(s_, x, r, cols ? numel(shape) / cols : 0, cols, sc, bi, eps,
+        rc = icx::layer_norm_f32(s_, x, r, res_rows, cols ? numel(shape) / cols : 0, cols, sc, bi, eps,
                                  static_cast<float*>(Y->ptr), part, &n_part);
         if (!rc) record_range(out, n_part);
         return rc;

@@ -23,7 +23,9 @@ inline int num_cus() {
 
 // icx_layer_norm_f32 leaving up to kMaxRangeParts (min, max) partials of y in `part`
 // (may be null); *n_part = partials written, 0 when this shape's kernel leaves none.
-int layer_norm_f32(hipStream_t s, const float* x, const float* residual, size_t rows, size_t cols,
+// res_rows != 0: the residual has res_rows rows (dividing rows), row r of x adding residual
+// row r % res_rows — a [S, cols] table broadcast over [B, S, cols].
+int layer_norm_f32(hipStream_t s, const float* x, const float* residual, size_t res_rows, size_t rows, size_t cols,
                    const float* scale, const float* bias, float eps, float* y, float2* part, int* n_part);
 
 // An exported attention's padding mask, Where(mask, fill, scores) before the Softmax with a
@@ -123,6 +125,13 @@ inline unsigned long long wall_ticks(unsigned us) {
 // non-temporal stores (the C entry point); the graph executor passes false.
 int dql_two_launch(hipStream_t s, const float* x, size_t n, uint8_t* y, float* y_scale, uint8_t* y_zp,
                    int32_t* opt_rowsum, size_t row_len, void* ws, size_t ws_bytes, bool nt_y);
+
+// Gather(table [axis_len, cols] UInt8 / Int8, indices) -> DequantizeLinear(., scale, zp) with a
+// per-tensor scale (and zero point, may be null) in one launch: y [n_idx, cols] f32, bit for
+// bit the two ops' result.  cols % 4 == 0, 4-byte aligned table, 16-byte aligned y; otherwise
+// ICX_ERR_UNSUPPORTED, having launched nothing.
+int gather_dequant_f32(hipStream_t s, const void* table, int dtype, size_t axis_len, size_t cols, const void* indices,
+                       int idx_dtype, size_t n_idx, const float* scale, const void* zp, float* y);
 
 // ---- layout.hip: the shape / mask plumbing of an exported encoder -----------------------
 constexpr int kLayoutMaxRank = 8;

@@ -120,14 +120,13 @@ cast_kernel(const S* __restrict__ x, D* __restrict__ y, size_t n, int to_bool) {
     }
 }
 
-constexpr int kUploadChunk = 256;
+constexpr int kUploadChunk = 2048;  // bytes per launch, passed as the kernel's argument
 struct Chunk {
     unsigned char b[kUploadChunk];
 };
 
 __global__ void __launch_bounds__(kThreads) upload_kernel(Chunk c, unsigned char* __restrict__ dst, int n) {
-    const int i = threadIdx.x;
-    if (i < n) dst[i] = c.b[i];
+    for (int i = threadIdx.x; i < n; i += kThreads) dst[i] = c.b[i];
 }
 
 constexpr int kMaxBlocks = 16384;

@@ -539,3 +539,53 @@ def test_encoder_with_decomposed_layer_norms_plans_like_the_fused_one():
     a, b = ([(norm.get(p, p), s) for p, s in pl] for pl in plans)
     assert a == b
     assert sum(p == "DecomposedLayerNorm" for p, _ in plans[1]) == 4
+
+
+def test_exported_encoder_plans_like_the_plain_one():
+    """DistilBERT-INT8 as exported (runtime reshape targets, the padding mask as Equal /
+    Reshape / Expand / Where, node-by-node LayerNorms, the UINT8 embedding Gather +
+    DequantizeLinear) plans to the plain encoder's fused heads plus the embedding lookup: no
+    MatMul / Softmax / Where / Expand left to run node by node, the mask's Equal(mask, 0)
+    computed once for all layers, the shape arithmetic as host-side regular entries."""
+    from collections import Counter
+    L = 3
+    ex = GpuGraphExecutor()
+    out, names, params, emb = graphs.export_encoder_graph(ex, layers=L, vocab=1000)
+    ex.add_output(out)
+    entries, _ = ex.plan()
+    live = [e for e in entries if e.kind != "Skip"]
+    heads = Counter(e.pattern for e in live if e.kind == "FusedHead")
+    assert heads == {"QuantizedLinear": 6 * L, "DecomposedLayerNorm": 1 + 2 * L, "Attention": L,
+                     "GatherDequantize": 1}
+    regular = Counter(e.op_type for e in live if e.kind == "Regular")
+    assert regular["Equal"] == 1 and regular["DynamicQuantizeLinear"] == 4 * L
+    for op in ("MatMul", "Softmax", "Where", "Expand", "Transpose", "Add", "Mul", "Div"):
+        assert regular[op] == 0, op
+    assert sorted({e.group for e in live if e.group}) == ["L%d.q.mmi" % l for l in range(L)]
+
+
+def test_duplicate_nodes_merge_only_in_the_shape_and_mask_plumbing():
+    """Identical Equal nodes (inputs, attributes, constant values) become one; the Q / K / V
+    projections' identical x_scale * w_scale Muls stay, owned by their quantized-linear heads
+    (and the three heads still run as one grouped GEMM); a duplicate whose output is requested
+    stays."""
+    ex = GpuGraphExecutor()
+    ex.add_input("m", [None, None])
+    for i in range(3):
+        ex.add_initializer("z%d" % i, np.array(0, np.int64))
+        ex.add_node("eq%d" % i, "Equal", ["m", "z%d" % i], ["e%d" % i])
+        ex.add_node("c%d" % i, "Cast", ["e%d" % i], ["f%d" % i], {"to": 1})
+    ex.add_node("sum", "Add", ["f0", "f1"], ["s01"])
+    ex.add_node("sum2", "Add", ["s01", "f2"], ["s"])
+    ex.add_output("s")
+    ops = [e.op_type for e in ex.plan()[0] if e.kind != "Skip"]
+    assert ops.count("Equal") == 1 and ops.count("Cast") == 1  # the Casts then coincide too
+    ex.add_output("e2")
+    ops = [e.op_type for e in ex.plan()[0] if e.kind != "Skip"]
+    assert ops.count("Equal") == 2
+    ex2 = GpuGraphExecutor()
+    out, _, _ = graphs.encoder_graph(ex2, layers=2)
+    ex2.add_output(out)
+    live = [e for e in ex2.plan()[0] if e.kind != "Skip"]
+    assert [e.op_type for e in live if e.kind == "Regular"] == ["DynamicQuantizeLinear"] * 8
+    assert sorted({e.group for e in live if e.group}) == ["L0.q.mmi", "L1.q.mmi"]

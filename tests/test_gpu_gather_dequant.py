@@ -76,6 +76,36 @@ def test_uint8_embedding_gather_then_dequantize():
     assert np.array_equal(bits(got[out]), bits(want))
 
 
+@pytest.mark.parametrize("dtype,idx_dt,zp", [(np.uint8, np.int64, 131), (np.int8, np.int32, -7),
+                                           (np.uint8, np.int64, None)])
+def test_embedding_gather_dequantize_fused(dtype, idx_dt, zp):
+    """Only the dequantized embeddings requested: Gather + DequantizeLinear plan as one
+    GatherDequantize head, one launch; bit-exact against the oracle's two ops (negative and
+    out-of-range indices under the Gather's rules)."""
+    rng = np.random.default_rng(768)
+    lo, hi = (0, 256) if dtype == np.uint8 else (-128, 128)
+    table = rng.integers(lo, hi, (30522, 768)).astype(dtype)
+    ids = rng.integers(0, 30522, (32, 128)).astype(idx_dt)
+    ids[0, :5] = [-1, -30522, 0, 30521, 30521]
+    scale = np.float32(0.0173)
+    ex = GpuGraphExecutor()
+    ex.add_input("ids", [None, None])
+    ex.add_initializer("table", table)
+    ex.add_initializer("scale", scale)
+    ins = ["q", "scale"]
+    if zp is not None:
+        ex.add_initializer("zp", np.array(zp, dtype))
+        ins.append("zp")
+    ex.add_node("g", "Gather", ["table", "ids"], ["q"], {"axis": 0})
+    ex.add_node("d", "DequantizeLinear", ins, ["y"])
+    got = ex.run({"ids": dev(ids)}, ["y"])["y"]
+    live = [e for e in ex.plan()[0] if e.kind != "Skip"]
+    assert [e.pattern for e in live] == ["GatherDequantize"]
+    want = oracle.dequantize_linear(oracle.gather(table, ids, axis=0), np.asarray(scale),
+                                    None if zp is None else np.asarray(zp, dtype))
+    assert got.shape == (32, 128, 768) and np.array_equal(bits(got), bits(want))
+
+
 @pytest.mark.parametrize("shape,per_col,zp_kind,axis", [
     ((512, 768), True, "col", 1),
     ((512, 768), False, "scalar", 1),
