@@ -11,8 +11,10 @@ launch whose blocks trade their (min, max) through an exchange buffer kept from 
 row sums (cfg4's weight zero points) or the input is past that launch's limit, the DQL is
 the two launches of icx_dynamic_quantize_linear (min/max, quantize).  The same run also reports the metric's second part,
 encoder seq/s (cfg3: the 6-layer DistilBERT-int8-shaped encoder at batch 32, seq 128, one
-captured forward replayed per step).  --config cfg3 makes that the primary line; the other
-configs (cfg1|cfg4|cfg5a|cfg5b) are for the per-kernel roofline figures.
+captured forward replayed per step), and next to it the same encoder in the form a
+DistilBERT-INT8 export writes it (Int64 ids and mask, embeddings, runtime shapes, padding mask).
+--config cfg3 makes the encoder the primary line; the other configs (cfg1|cfg4|cfg5a|cfg5b)
+are for the per-kernel roofline figures.
 
 Timing: W untimed warmup steps, then exactly K steps, each a replay of a HIP graph that
 holds one step (so host launch overhead is not measured), bracketed by synchronize.  The
@@ -232,6 +234,40 @@ class EncoderRunner:
 
     def step(self):
         self.ex.replay()
+
+
+class ExportEncoderRunner:
+    """The same encoder in the form a DistilBERT-INT8 export writes it (graphs.
+    export_encoder_graph): Int64 input_ids / attention_mask [32, 128] (seeded lengths, one row
+    unpadded), the UINT8 word-embedding lookup, position embeddings, runtime reshape targets,
+    the padding mask and node-by-node LayerNorms; one forward captured, a step is one replay."""
+
+    def __init__(self):
+        import torch
+
+        from iconnx_amd import graphs
+        from iconnx_amd.executor import GpuGraphExecutor
+
+        cfg = graphs.ENCODER
+        self.B, self.S = cfg["batch"], cfg["seq"]
+        self.ex = GpuGraphExecutor()
+        self.out, _, _, _ = graphs.export_encoder_graph(self.ex, layers=cfg["layers"], heads=cfg["heads"])
+        ids, mask = graphs.export_inputs(self.B, self.S)
+        self.feeds = {"input_ids": torch.from_numpy(ids).cuda(), "attention_mask": torch.from_numpy(mask).cuda()}
+        self.ex.capture(self.feeds, [self.out])
+        torch.cuda.synchronize()
+
+    def step(self):
+        self.ex.replay()
+
+
+def export_form_line(torch):
+    """seq/s of the exported form (a reported extra next to the encoder line)."""
+    exp = ExportEncoderRunner()
+    ms, _ = time_replays(exp.step, 50, 5, torch)
+    exp.ex.check_status()
+    return {"metric": "encoder seq/s, exported form", "value": round(exp.B / (ms * 1e-3), 1), "unit": "seq/s",
+            "ms_per_forward": round(ms, 4), "workload": EXPORT_WORKLOAD, "graph_replay": True}
 
 
 class FfnUpGeluRunner:
@@ -572,6 +608,7 @@ def main():
                           "unit": "seq/s", "ms_per_forward": round(ms_e, 4),
                           "int8_TOPS": round(e_tops, 2), "int8_frac_of_mfma_peak": round(e_tops / PEAK_INT8_TOPS, 4),
                           "workload": ENCODER_WORKLOAD, "graph_replay": True}
+        out["encoder"]["export_form"] = export_form_line(torch)
         if not args.no_cpu_baseline:
             out["encoder"]["cpu_baseline"] = encoder_cpu_baseline()
     if not args.no_cpu_baseline and args.config != "copy":
@@ -585,6 +622,10 @@ def main():
 ENCODER_WORKLOAD = ("cfg3: 6-layer DistilBERT-int8-shaped encoder, hidden 768, 12 heads, FFN 3072, "
                     "batch 32, seq 128; every linear DQL + MatMulInteger + dequant Mul + bias Add, "
                     "LayerNorm / Softmax / erf-GELU in fp32")
+EXPORT_WORKLOAD = ("cfg3 as a DistilBERT-INT8 export writes it: Int64 input_ids / attention_mask [32, 128], "
+                   "UINT8 word-embedding Gather + DequantizeLinear, position embeddings, reshape targets from "
+                   "Shape / Gather / Unsqueeze / Concat, padding mask Equal / Reshape / Expand / Where, "
+                   "node-by-node LayerNorms (embeddings and mask included in the forward)")
 
 
 def main_encoder(args, torch):
@@ -620,6 +661,7 @@ def main_encoder(args, torch):
                      "kernel_int8_TOPS": round(2.0 * ffn.M * ffn.N * ffn.K / (k_us * 1e-6) / 1e12, 2)},
         "timing": {"graph_replay": True, "wall_s": round(wall, 4),
                    "encoder_int8_TOPS": round(enc.int8_ops / (ms_step * 1e-3) / 1e12, 2)},
+        "export_form": export_form_line(torch),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = encoder_cpu_baseline()
