@@ -304,19 +304,27 @@ int icx_attention_f32(icx_stream_t stream, const float* q, const float* k, const
  * src/ir/lowering.rs:31-238: topological sort, fusion decision, initializer upload) and run
  * (:428) with the input-shape guard (:441-460).  Ops dispatched: DynamicQuantizeLinear,
  * MatMulInteger (2-D and 3-D x 2-D, layout.rs:1034-1095), DequantizeLinear, Cast (to
- * FLOAT), Mul / Add / Sub / Div, and the encoder's LayerNormalization, Softmax, Erf,
- * Transpose, Reshape (Int64 shape initializer; the output aliases the input) and f32
- * MatMul; anything else is an ICX_ERR_UNSUPPORTED error naming the node.
+ * FLOAT / INT32 / INT64 / BOOL), Mul / Add / Sub / Div, the encoder's LayerNormalization,
+ * ReduceMean, Pow, Sqrt, Softmax, Erf, Transpose, Reshape (the output aliases the input) and
+ * f32 MatMul, Gather, and an export's shape / mask plumbing: Shape, Unsqueeze, Squeeze,
+ * Identity, Concat, Slice, Expand, Equal, Where (integer tensors known on the host — Shape
+ * results, small initializers, inputs bound from host memory — are computed on the host, as
+ * the reference's get_or_fetch_i64 cache and shape-extraction folding do; the rest runs on
+ * the device); anything else is an ICX_ERR_UNSUPPORTED error naming the node.
  * Fused patterns (src/cuda/inference/fusion/patterns.rs:15-109 plus one new head):
  *   QuantizedLinear  MatMulInteger -> Cast -> Mul(scale or Mul(x_scale, w_scale)) [-> Add]
  *                    [-> Mul/Add/Sub/Div with static operands]*
  *                    [-> erf-GELU: Div, Erf, Add, Mul(x, .), Mul]      => icx_qlinear_f32
  *   MulAdd / AddMul / SubMul / DivMul / ElementwiseChain / Gelu — chains of elementwise ops
  *                    with static operands (scalar, [last dim], same shape) => icx_fused_chain_f32
- *   Attention        Reshape -> Transpose -> MatMul -> Div|Mul -> Softmax -> MatMul ->
- *                    Transpose -> Reshape of a self-attention => icx_attention_f32, or the
- *                    nodes one by one when the shapes fall outside that kernel
+ *   Attention        Reshape -> Transpose -> MatMul -> Div|Mul -> [Where(padding mask,
+ *                    fill, .)] -> Softmax -> MatMul -> Transpose -> Reshape of a
+ *                    self-attention (reshape targets may be computed at run time, the key
+ *                    transposed twice) => the attention kernel, or the nodes one by one when
+ *                    the shapes or the mask fall outside it
  *   AddLayerNorm     LayerNormalization(Add(a, b)) => icx_layer_norm_f32 with a residual
+ *   DecomposedLayerNorm  the same written node by node (ReduceMean / Sub / Pow / Sqrt / Div)
+ *   GatherDequantize DequantizeLinear(Gather(UInt8 / Int8 table, indices)), per-tensor scale
  * Attribute values are int64 (axis, to); names of absent optional inputs are "". */
 typedef struct icx_graph icx_graph;
 
@@ -324,14 +332,15 @@ icx_graph* icx_graph_create(void);
 void icx_graph_destroy(icx_graph* g);
 /* dims: rank entries; -1 marks a dynamic dimension (shape[i] == None in the reference). */
 int icx_graph_add_input(icx_graph* g, const char* name, int rank, const int64_t* dims);
-/* Host data is copied (uploaded at compile).  dtype: ICX_I8 / ICX_U8 / ICX_I32 / ICX_F32. */
+/* Host data is copied (uploaded at compile).  dtype: ICX_I8 / ICX_U8 / ICX_I32 / ICX_F32 /
+ * ICX_I64 / ICX_BOOL. */
 int icx_graph_add_initializer(icx_graph* g, const char* name, int dtype, int rank,
                               const int64_t* dims, const void* host_data);
 int icx_graph_add_node(icx_graph* g, const char* name, const char* op_type, int n_in,
                        const char* const* inputs, int n_out, const char* const* outputs,
                        int n_attr, const char* const* attr_names, const int64_t* attr_values);
 /* Non-integer attributes of an added node: a float (LayerNormalization epsilon) or a list
- * of ints (Transpose perm). */
+ * of ints (Transpose perm, Unsqueeze / Squeeze / ReduceMean axes). */
 int icx_graph_set_node_attr_float(icx_graph* g, const char* node, const char* attr, double value);
 int icx_graph_set_node_attr_ints(icx_graph* g, const char* node, const char* attr, int count,
                                  const int64_t* values);
