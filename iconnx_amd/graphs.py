@@ -356,12 +356,15 @@ def add_embeddings_export(ex, ids, word_table, scale, zp, pos_table, ln, eps, pr
 
 
 def export_encoder_graph(ex, layers=6, heads=12, hidden=768, ffn=3072, eps=1e-12, vocab=30522,
-                         max_pos=512, seed=3000):
+                         max_pos=512, seed=3000, per_channel=False, opset17_norm=False):
     """DistilBERT-INT8 as exported (see above) on executor or writer ``ex``: inputs
     ``input_ids`` and ``attention_mask`` (Int64 [B, S]).  The layers carry the weights of
-    encoder_graph's; the embedding tables are seeded too.  Returns (output name, names dict
-    with the embedding output and per-layer tensor names, per-layer params, embedding
-    params)."""
+    encoder_graph's; the embedding tables are seeded too.  ``per_channel``: every weight
+    with a seeded per-column scale [N] and an Int8 zero point [N] of zeros (ONNX Runtime's
+    per_channel quantization of symmetric int8 weights); ``opset17_norm``: the layers'
+    LayerNorms as LayerNormalization nodes (an export at opset 17 or later).  Returns (output
+    name, names dict with the embedding output and per-layer tensor names, per-layer params,
+    embedding params)."""
     ex.add_input("input_ids", [None, None], 7)
     ex.add_input("attention_mask", [None, None], 7)
     emb = dict(word=seeded_uniform(vocab * hidden, seed - 7, 0.0, 255.0).astype(np.uint8).reshape(vocab, hidden),
@@ -375,18 +378,26 @@ def export_encoder_graph(ex, layers=6, heads=12, hidden=768, ffn=3072, eps=1e-12
     names, params = dict(emb=x, layers=[]), []
     for l in range(layers):
         prm = encoder_layer_params(l, hidden, ffn, seed)
+        if per_channel:
+            for i, nm in enumerate(("q", "k", "v", "o", "ff1", "ff2")):
+                N = prm[nm]["w"].shape[1]
+                prm[nm]["w_scale"] = seeded_uniform(N, seed + 100 * l + 50 + i, 3e-4, 7e-4)
+                prm[nm]["w_zp"] = np.zeros(N, np.int8)
         p = "L%d" % l
         lin = lambda name, inp, **kw: add_quantized_linear(  # noqa: E731
             ex, inp, prm[name]["w"], prm[name]["w_zp"], prm[name]["w_scale"], prm[name]["bias"],
             prefix="%s.%s" % (p, name), **kw)
+        norm = (lambda a, r, prm_ln, tag: add_layer_norm(ex, a, r, prm_ln["scale"], prm_ln["bias"], eps, tag)) \
+            if opset17_norm else \
+            (lambda a, r, prm_ln, tag: add_layer_norm_decomposed(ex, a, r, prm_ln["scale"], prm_ln["bias"], eps, tag))
         dql = add_dynamic_quantize(ex, x, p + ".qkv")
         q, k, v = (lin(nm, x, dql=dql) for nm in ("q", "k", "v"))
         ctx = add_self_attention_export(ex, x, q, k, v, "attention_mask", heads, hidden // heads, p + ".attn")
         o = lin("o", ctx)
-        x1 = add_layer_norm_decomposed(ex, o, x, prm["ln1"]["scale"], prm["ln1"]["bias"], eps, p + ".ln1")
+        x1 = norm(o, x, prm["ln1"], p + ".ln1")
         h = lin("ff1", x1, gelu=True)
         f = lin("ff2", h)
-        x2 = add_layer_norm_decomposed(ex, f, x1, prm["ln2"]["scale"], prm["ln2"]["bias"], eps, p + ".ln2")
+        x2 = norm(f, x1, prm["ln2"], p + ".ln2")
         names["layers"].append(dict(x=x, xq=dql[0], q=q, k=k, v=v, ctx=ctx, o=o, x1=x1, h=h, f=f, out=x2))
         params.append(prm)
         x = x2

@@ -17,7 +17,8 @@ def dequant_linear(xq, xs, xzp, p, rows=None, gelu=False):
     """Linear from an already quantized input: MatMulInteger -> Cast -> Mul(x_scale *
     w_scale) -> Add(bias) [-> GELU], rows [r0, r1) of the flattened input (all if None)."""
     x2 = xq.reshape(-1, xq.shape[-1])
-    acc = matmul_integer(x2, p["w"], xzp, p["w_zp"], rows=rows)
+    per_col = np.size(p["w_zp"]) > 1  # a per-column weight zero point (the extension's form)
+    acc = matmul_integer(x2, p["w"], xzp, p["w_zp"], per_column_b_zp=per_col, rows=rows)
     if rows is not None:
         acc = acc[rows[0]:rows[1]]
     y = add(mul(cast_i32_f32(acc), mul(xs, p["w_scale"])), p["bias"])

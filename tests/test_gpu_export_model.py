@@ -110,13 +110,18 @@ def check_node_by_node(got, names, params, emb, ids, mask, eps=1e-12, rows=None)
         ln_check(t["f"], t["x1"], p["ln2"], t["out"])
 
 
-def test_export_model_from_file(tmp_path):
+@pytest.mark.parametrize("variant", ["opset13", "per_channel", "opset17_norm"])
+def test_export_model_from_file(tmp_path, variant):
+    """The export at opset 13-16 (LayerNorms node by node), with ONNX Runtime's per-channel
+    weight scales (zero points [N] of zeros), and at opset 17 (LayerNormalization nodes)."""
     path = str(tmp_path / "distilbert_int8_export.onnx")
-    out, names, params, emb = graphs.write_model(path, graphs.export_encoder_graph, layers=2, vocab=1000)
+    kw = {} if variant == "opset13" else {variant: True}
+    out, names, params, emb = graphs.write_model(path, graphs.export_encoder_graph, layers=2, vocab=1000, **kw)
     model = OnnxParser.parse_file(path)
     ops = set(model.list_unique_operators())
     assert {"Shape", "Unsqueeze", "Concat", "Slice", "Equal", "Expand", "Where", "Pow", "ReduceMean",
             "Sqrt", "DequantizeLinear", "Gather"} <= ops
+    assert ("LayerNormalization" in ops) == (variant == "opset17_norm")
     ex = GpuGraphExecutor.from_model(model)
     ids, mask = graphs.export_inputs(4, 32, 1000)
     got = ex.run({"input_ids": ids, "attention_mask": mask}, wanted(names))
@@ -127,7 +132,8 @@ def test_export_model_from_file(tmp_path):
     # every reshape target and mask shape came from the host: no node of the shape arithmetic
     # runs as a kernel, and the quantized linears / LayerNorms still fuse
     pats = [e.pattern for e in ex.plan()[0] if e.kind == "FusedHead"]
-    assert pats.count("DecomposedLayerNorm") == 1 + 2 * 2 and pats.count("QuantizedLinear") == 6 * 2
+    norms = pats.count("DecomposedLayerNorm") + pats.count("AddLayerNorm")
+    assert norms == 1 + 2 * 2 and pats.count("QuantizedLinear") == 6 * 2
     assert pats.count("Attention") == 2  # the masked attention as one kernel
 
 
