@@ -370,6 +370,7 @@ matmul_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, int 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int ATT_S = 128, ATT_D = 64, ATT_QB = 64;  // keys, head size, queries per block
+constexpr int ATT_MAX_S = icx::kAttentionMaxSeq;  // longest sequence (attention_long_kernel)
 constexpr int K_STRIDE = ATT_D + 4;   // floats per LDS row of K: 16-byte reads conflict-free
 constexpr int VT_STRIDE = ATT_S + 4;  // V^T rows [dim][key]
 // Key k of V^T row d is stored at column k ^ vt_swz(d).  With the 132-float rows alone, the
@@ -624,6 +625,167 @@ __global__ void __launch_bounds__(kThreads) attention_kernel(AttnArgs a) {
     if (a.part) icx::block_range_store<kThreads>(mn, mx, a.part);
 }
 
+// Sequences longer than the 128 keys attention_kernel keeps in one LDS tile (BERT at 384 or
+// 512, say): a block takes 64 queries of one (batch, head) and walks the keys in chunks of
+// 128 with the running (online) softmax — per chunk the S^T tile, scale and mask exactly as
+// attention_kernel forms them, the new row max m' = max(m, chunk max), the earlier partial
+// sums and context rescaled by exp(m - m'), then P V of the chunk — and divides by the row sum
+// once at the end.  The same MFMA layouts as attention_kernel (P stays in registers).  A row
+// whose every score is -inf gives 0 / 0 = NaN, as the Softmax node does.  f32 context only.
+// The blocks of one (batch, head) run on the same XCD (block i runs on XCD i % 8), so their
+// K / V chunk loads hit that XCD's L2.
+__global__ void __launch_bounds__(kThreads) attention_long_kernel(AttnArgs a, int nqt) {
+    __shared__ __attribute__((aligned(16))) float lds[ATT_LDS_FLOATS];
+    __shared__ uint8_t kmask[ATT_S];
+    const int P = (int)(gridDim.x / (unsigned)nqt);  // (batch, head) pairs
+    const int full = P / 8;
+    int pair, qt;
+    if ((int)blockIdx.x < full * 8 * nqt) {
+        const int g = blockIdx.x / (8 * nqt), rem = blockIdx.x % (8 * nqt);
+        qt = rem / 8;
+        pair = g * 8 + rem % 8;
+    } else {
+        const int x = blockIdx.x - full * 8 * nqt;
+        pair = full * 8 + x / nqt;
+        qt = x % nqt;
+    }
+    const int b = pair / a.H, h = pair % a.H;
+    const int S = a.S;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int lq = lane & 15, lg = lane >> 4;
+    const int qi = qt * ATT_QB + 16 * w + lq;  // this lane's query row
+    const int c4 = (t & 15) * 4;
+
+    float4 qr[4];
+    const float* qp = a.q + ((size_t)b * S + qi) * a.ldq + h * ATT_D + 16 * lg;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        qr[u] = qi < S ? *reinterpret_cast<const float4*>(qp + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (a.scale_q) {
+            qr[u].x = apply_scale(qr[u].x, a);
+            qr[u].y = apply_scale(qr[u].y, a);
+            qr[u].z = apply_scale(qr[u].z, a);
+            qr[u].w = apply_scale(qr[u].w, a);
+        }
+    }
+    float m = -INFINITY, sum = 0.0f;
+    v4f o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4f st[8];
+
+    for (int key0 = 0; key0 < S; key0 += ATT_S) {
+        // the chunk's mask bytes, K and V rows (rows past S are zero)
+        const uint8_t mk = a.mask && t < ATT_S && key0 + t < S ? a.mask[(int64_t)b * a.mask_bs + key0 + t] : (uint8_t)0;
+        float4 kr[8], vr[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int r = key0 + u * 16 + (t >> 4);
+            kr[u] = vr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < S) {
+                const size_t row = (size_t)b * S + r;
+                kr[u] = *reinterpret_cast<const float4*>(a.k + row * a.ldk + h * ATT_D + c4);
+                vr[u] = *reinterpret_cast<const float4*>(a.v + row * a.ldv + h * ATT_D + c4);
+            }
+        }
+        __syncthreads();  // the previous chunk's P V reads of LDS are done
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            *reinterpret_cast<float4*>(lds + (u * 16 + (t >> 4)) * K_STRIDE + c4) = kr[u];
+        if (t < ATT_S) kmask[t] = mk;
+        __syncthreads();
+        float mc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+            float4 kf[4];
+            const float* kp = lds + (16 * kt + lq) * K_STRIDE + 16 * lg;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) kf[u] = *reinterpret_cast<const float4*>(kp + 4 * u);
+            st[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4c(kf[u], e), f4c(qr[u], e), st[kt], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kc = 16 * kt + 4 * lg + r;
+                float x = a.scale_q ? st[kt][r] : apply_scale(st[kt][r], a);
+                if (key0 + kc >= S) x = -INFINITY;
+                else if (a.mask && kmask[kc]) x = a.fill;
+                st[kt][r] = x;
+                mc = fmaxf(mc, x);
+            }
+        }
+        mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
+        mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
+        const float mn = fmaxf(m, mc);
+        const float mu = mn == -INFINITY ? 0.0f : mn;  // every score so far -inf: weights 0
+        const float alpha = __expf(__fsub_rn(m, mu));
+        m = mn;
+        sum = __fmul_rn(sum, alpha);
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = __expf(__fsub_rn(st[kt][r], mu));
+                st[kt][r] = e;
+                sum = __fadd_rn(sum, e);
+            }
+        // context rows are queries 4 lg + r: their factors sit in lanes 4 lg + r
+        float alpha_r[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) alpha_r[r] = __shfl(alpha, 4 * lg + r, 64);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[dt][r] = __fmul_rn(o[dt][r], alpha_r[r]);
+        __syncthreads();  // every wave is done with K: the region takes V^T
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int r = (u * 16 + (t >> 4)) ^ vt_swz(c4);
+            lds[(c4 + 0) * VT_STRIDE + r] = vr[u].x;
+            lds[(c4 + 1) * VT_STRIDE + r] = vr[u].y;
+            lds[(c4 + 2) * VT_STRIDE + r] = vr[u].z;
+            lds[(c4 + 3) * VT_STRIDE + r] = vr[u].w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+            float4 vq[4];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+                vq[dt] = *reinterpret_cast<const float4*>(lds + (16 * dt + lq) * VT_STRIDE +
+                                                          ((16 * kt + 4 * lg) ^ vt_swz(16 * dt + lq)));
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[kt][r], f4c(vq[dt], r), o[dt], 0, 0, 0);
+        }
+    }
+    sum = __fadd_rn(sum, __shfl_xor(sum, 16, 64));
+    sum = __fadd_rn(sum, __shfl_xor(sum, 32, 64));
+    const float inv = __fdiv_rn(1.0f, sum);
+    float inv_r[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inv_r[r] = __shfl(inv, 4 * lg + r, 64);
+    float mn = 0.0f, mx = 0.0f;  // DQL range of out (when a.part is given)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = qt * ATT_QB + 16 * w + 4 * lg + r;
+        if (row >= S) continue;
+        float* dst = a.out + ((size_t)b * S + row) * a.ldo + h * ATT_D + lq;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const float y = __fmul_rn(o[dt][r], inv_r[r]);
+            dst[16 * dt] = y;
+            if (a.part) icx::range_acc(y, mn, mx);
+        }
+    }
+    if (a.part) icx::block_range_store<kThreads>(mn, mx, a.part);
+}
+
 
 template <int PER>
 void launch_ln_rows(bool rows4, dim3 grid, hipStream_t s, const float* x, const float* res, size_t res_rows,
@@ -803,14 +965,16 @@ int attention_args(const float* q, const float* k, const float* v, size_t B, siz
                    size_t ldq, size_t ldk, size_t ldv, size_t ldo, float scale, int scale_div, int scale_q,
                    const icx::AttnMask* mask, AttnArgs* a, size_t* blocks) {
     if (!q || !k || !v) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention: null pointer argument");
-    if (D != (size_t)ATT_D || S == 0 || S > (size_t)ATT_S)
-        ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention: head size %zu / sequence %zu unsupported (D = 64, S <= 128)", D, S);
+    if (D != (size_t)ATT_D || S == 0 || S > (size_t)ATT_MAX_S)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention: head size %zu / sequence %zu unsupported (D = 64, S <= %d)", D, S,
+                 ATT_MAX_S);
     if (ldq < H * D || ldk < H * D || ldv < H * D || ldo < H * D || (ldq | ldk | ldv) % 4 ||
         !icx::aligned16(q) || !icx::aligned16(k) || !icx::aligned16(v))
         ICX_FAIL(ICX_ERR_SHAPE, "Attention: row strides must cover H*D and keep 16-byte alignment");
-    if (B * H > 0x3fffffff) ICX_FAIL(ICX_ERR_SHAPE, "Attention: too many (batch, head) pairs");
-    // two blocks per (batch, head) when S > 64 (each takes 64 queries), one otherwise
-    const size_t per = S > (size_t)ATT_QB ? 2 : 1;
+    // blocks per (batch, head): one per 64 queries (attention_kernel takes S <= 128 keys in
+    // one tile: one or two blocks; attention_long_kernel walks longer ones in chunks)
+    const size_t per = S > (size_t)ATT_S ? icx::cdiv(S, (size_t)ATT_QB) : (S > (size_t)ATT_QB ? 2 : 1);
+    if (B * H * per > 0x3fffffff) ICX_FAIL(ICX_ERR_SHAPE, "Attention: too many (batch, head) pairs");
     *blocks = B * H * per;
     *a = AttnArgs{};
     a->q = q;
@@ -856,8 +1020,13 @@ int icx::attention_f32(hipStream_t s, const float* q, const float* k, const floa
     a.out = out;
     float2* pp = (part && blocks <= (size_t)icx::kMaxRangeParts) ? part : nullptr;
     a.part = pp;
-    hipLaunchKernelGGL(attention_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
-    ICX_LAUNCH_CHECK("attention_kernel");
+    if (S > (size_t)ATT_S) {
+        hipLaunchKernelGGL(attention_long_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, a, a.qsplit);
+        ICX_LAUNCH_CHECK("attention_long_kernel");
+    } else {
+        hipLaunchKernelGGL(attention_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
+        ICX_LAUNCH_CHECK("attention_kernel");
+    }
     if (pp && n_part) *n_part = (int)blocks;
     return ICX_OK;
 }
@@ -867,6 +1036,7 @@ int icx::attention_dql(hipStream_t s, const float* q, const float* k, const floa
                        int scale_div, int scale_q, const AttnMask* mask, uint8_t* y, float* y_scale,
                        uint8_t* y_zp, unsigned* sync) {
     if (!y || !y_scale || !y_zp || !sync) ICX_FAIL(ICX_ERR_INVALID_ARG, "Attention+DQL: null pointer argument");
+    if (S > (size_t)ATT_S) ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention+DQL: sequence %zu > %d", S, ATT_S);
     if (ldo % 16 || !icx::aligned16(y))
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "Attention+DQL: the u8 rows must keep 16-byte alignment");
     AttnArgs a;

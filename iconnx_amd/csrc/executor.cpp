@@ -2083,7 +2083,7 @@ class Runner {
             }
         }
         fused = fused && head_dim == 64 && heads > 0 && Q->shape[2] == heads * head_dim && Q->shape[1] > 0 &&
-                Q->shape[1] <= 128;
+                Q->shape[1] <= icx::kAttentionMaxSeq;
         std::vector<int64_t> split = {Q->shape.empty() ? 0 : Q->shape[0], Q->shape.size() > 1 ? Q->shape[1] : 0,
                                       heads, head_dim};
         for (const std::string* sh : {&op.q_shape, &op.k_shape, &op.v_shape}) {

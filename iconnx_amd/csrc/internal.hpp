@@ -28,6 +28,10 @@ inline int num_cus() {
 int layer_norm_f32(hipStream_t s, const float* x, const float* residual, size_t res_rows, size_t rows, size_t cols,
                    const float* scale, const float* bias, float eps, float* y, float2* part, int* n_part);
 
+// Longest sequence of the fused attention (up to 128 keys in one tile, longer ones in chunks
+// of 128 with a running softmax); head size 64.
+constexpr int kAttentionMaxSeq = 8192;
+
 // An exported attention's padding mask, Where(mask, fill, scores) before the Softmax with a
 // mask that broadcasts as [B, 1, 1, S]: key j of batch b is masked when keys[b * batch_stride
 // + j] != 0 (batch_stride 0: one row for every batch); a masked score becomes `fill`.

@@ -292,7 +292,9 @@ int icx_matmul_f32(icx_stream_t stream, const float* a, const float* b, size_t b
  * scale_div, else multiplication), applied to q before the product when scale_q, else to the
  * scores.  This is the BERT subgraph Reshape -> Transpose -> MatMul -> Div|Mul -> Softmax ->
  * MatMul -> Transpose -> Reshape the reference runs node by node
- * (src/operators/{reshape,transpose,matmul,div,softmax}.rs).  D == 64, S <= 128. */
+ * (src/operators/{reshape,transpose,matmul,div,softmax}.rs).  D == 64, S <= 8192 (up to 128
+ * keys in one tile with the exact row max; longer sequences in 128-key chunks with a running
+ * softmax, the same result within f32 rounding). */
 int icx_attention_f32(icx_stream_t stream, const float* q, const float* k, const float* v,
                       size_t B, size_t S, size_t H, size_t D, size_t ldq, size_t ldk,
                       size_t ldv, size_t ldo, float scale, int scale_div, int scale_q,

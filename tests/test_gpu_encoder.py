@@ -58,21 +58,28 @@ def test_small_encoder_end_to_end(seed):
 
 
 def test_attention_outside_the_fused_kernel_runs_node_by_node():
-    """S = 130 > 128: the Attention head falls back to its Reshape/Transpose/MatMul/Softmax
-    nodes (generic kernels); the result still matches the oracle composition."""
+    """Head size 32 (the kernels take 64): the Attention head falls back to its Reshape /
+    Transpose / MatMul / Softmax nodes (generic kernels), against the oracle composition; the
+    same graph shape with heads of 64 runs the one-tile kernel at S = 128 and the chunked one
+    at S = 130."""
     rng = np.random.default_rng(7)
+    q, k, v = (rng.standard_normal((2, 130, 4 * 32)).astype(np.float32) for _ in range(3))
+    ex = GpuGraphExecutor()
+    for n in "qkv":
+        ex.add_input(n, [None, None, 128])
+    ctx = graphs.add_self_attention(ex, "q", "k", "v", 4, 32, "att")
+    got = ex.run({"q": q, "k": k, "v": v}, [ctx])[ctx]
+    assert [e.pattern for e in ex.plan()[0] if e.kind == "FusedHead"] == ["Attention"]
+    assert rel_err(got, ref.attention_ref(q, k, v, 4, np.sqrt(32))) < 1e-5
     q, k, v = (rng.standard_normal((2, 130, 4 * 64)).astype(np.float32) for _ in range(3))
     ex = GpuGraphExecutor()
     for n in "qkv":
         ex.add_input(n, [None, None, 256])
     ctx = graphs.add_self_attention(ex, "q", "k", "v", 4, 64, "att")
-    got = ex.run({"q": q, "k": k, "v": v}, [ctx])[ctx]
-    assert [e.pattern for e in ex.plan()[0] if e.kind == "FusedHead"] == ["Attention"]
-    assert rel_err(got, ref.attention_ref(q, k, v, 4)) < 1e-5
-    # and the fused kernel at S = 128 on the same graph
-    q2, k2, v2 = (t[:, :128].copy() for t in (q, k, v))
-    got2 = ex.run({"q": q2, "k": k2, "v": v2}, [ctx])[ctx]
-    assert rel_err(got2, ref.attention_ref(q2, k2, v2, 4)) < 1e-5
+    for S in (130, 128):
+        q2, k2, v2 = (t[:, :S].copy() for t in (q, k, v))
+        got2 = ex.run({"q": q2, "k": k2, "v": v2}, [ctx])[ctx]
+        assert rel_err(got2, ref.attention_ref(q2, k2, v2, 4)) < 1e-5, S
 
 
 def test_full_size_encoder_node_by_node():

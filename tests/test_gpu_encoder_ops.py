@@ -209,7 +209,22 @@ def test_fused_attention_other_scales_and_grids(B, S, H, scale, scale_q):
     assert rel_err(out, attention_oracle(q, k, v, H, scale, scale_q)) < 1e-5
 
 
+@pytest.mark.parametrize("B,S,H,scale_q", [(2, 129, 3, False), (2, 384, 12, True), (1, 512, 16, False),
+                                           (3, 1000, 2, True)])
+def test_fused_attention_long_sequences(B, S, H, scale_q):
+    """Past 128 keys: 128-key chunks with a running softmax (attention_long_kernel), 64
+    queries per block; (batch, head) counts that fill whole groups of 8 (the XCD-local block
+    order) and that do not."""
+    rng = np.random.default_rng(S * 7 + H)
+    q, k, v = (rng.standard_normal((B, S, H * 64)).astype(np.float32) for _ in range(3))
+    out = host(ops.gpu_attention(dev(q), dev(k), dev(v), H, 8.0, scale_div=True, scale_q=scale_q))
+    assert rel_err(out, attention_oracle(q, k, v, H, 8.0, scale_q)) < 1e-5
+
+
 def test_attention_rejects_unsupported_shapes():
-    q = torch.zeros((1, 129, 64), device="cuda")
+    q = torch.zeros((1, 10, 32), device="cuda")  # head size 32
+    with pytest.raises(IconnxError, match="unsupported"):
+        ops.gpu_attention(q, q, q, 1, 8.0)
+    q = torch.zeros((1, 8193, 64), device="cuda")  # past the longest sequence
     with pytest.raises(IconnxError, match="unsupported"):
         ops.gpu_attention(q, q, q, 1, 8.0)

@@ -15,7 +15,8 @@ the GELU linears (device erf / exp) and 1e-5 for the masked attention (fp32 MFMA
 order, device exp) — the tolerances of the unmasked encoder's node-by-node test.  The masked
 attention runs as one fused kernel (the Where / Expand / Shape of the mask and the key's two
 transposes folded into the attention head); the same graph with a sequence past the kernel's
-128, or with a mask that is not per key, runs node by node, also against the oracle.
+128 runs the chunked kernel; with heads of 32 or a mask that is not per key, the nodes run one by
+one; all against the oracle.
 """
 import numpy as np
 import pytest
@@ -160,39 +161,40 @@ def test_export_model_full_size():
         assert_bits(rep, got[out], "captured replay vs eager")
 
 
-def attention_graph(cond=False):
+def attention_graph(cond=False, D=64):
     """q, k, v, x [B, S, H*D] and the Int64 mask through add_self_attention_export; with
     ``cond`` a Bool [B, 1, S, S] input is the Where's condition instead (not per key)."""
     ex = GpuGraphExecutor()
     for n in ("x", "q", "k", "v"):
-        ex.add_input(n, [None, None, H * 64])
+        ex.add_input(n, [None, None, H * D])
     ex.add_input("mask", [None, None])
     if cond:
         ex.add_input("cond", [None, 1, None, None])
-    return ex, graphs.add_self_attention_export(ex, "x", "q", "k", "v", "mask", H, 64, "att",
+    return ex, graphs.add_self_attention_export(ex, "x", "q", "k", "v", "mask", H, D, "att",
                                                 cond="cond" if cond else None)
 
 
-def attention_feeds(S, B=6, seed=0):
+def attention_feeds(S, B=6, seed=0, D=64):
     rng = np.random.default_rng(seed + S)
-    q, k, v = (rng.standard_normal((B, S, H * 64)).astype(np.float32) for _ in range(3))
-    x = np.zeros((B, S, H * 64), np.float32)
+    q, k, v = (rng.standard_normal((B, S, H * D)).astype(np.float32) for _ in range(3))
+    x = np.zeros((B, S, H * D), np.float32)
     lens = np.array([S, 1, S // 2, 0, S - 1, 3])[:B]
     mask = (np.arange(S)[None, :] < lens[:, None]).astype(np.int64)
     return q, k, v, x, mask
 
 
-@pytest.mark.parametrize("S", [128, 77, 130])
-def test_masked_attention_fused_and_fallback(S):
-    """S <= 128: the fused kernel with the per-key mask (a batch whose every key is padding
-    included: a uniform softmax, as the node-by-node Where gives); S = 130: the node-by-node
-    fallback.  Both within 1e-5 of the oracle."""
-    q, k, v, x, mask = attention_feeds(S)
-    ex, ctx = attention_graph()
+@pytest.mark.parametrize("S,D", [(128, 64), (77, 64), (130, 64), (384, 64), (512, 64), (100, 32)])
+def test_masked_attention_fused_and_fallback(S, D):
+    """S <= 128: the one-tile kernel with the per-key mask (a batch whose every key is padding
+    included: a uniform softmax, as the node-by-node Where gives); S > 128: the chunked
+    kernel with the mask; head size 32: the node-by-node fallback.  All within 1e-5 of the
+    oracle."""
+    q, k, v, x, mask = attention_feeds(S, D=D)
+    ex, ctx = attention_graph(D=D)
     feeds = {n: torch.from_numpy(a).cuda() for n, a in (("x", x), ("q", q), ("k", k), ("v", v), ("mask", mask))}
     got = ex.run(feeds, [ctx])[ctx]
     assert [e.pattern for e in ex.plan()[0] if e.kind == "FusedHead"] == ["Attention"]
-    want = ref.attention_ref(q, k, v, H, 8.0, mask=mask)
+    want = ref.attention_ref(q, k, v, H, np.sqrt(D), mask=mask)
     for b in range(len(mask)):
         assert rel_err(got[b], want[b]) < 1e-5, (S, b)
 
