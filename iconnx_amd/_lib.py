@@ -75,6 +75,7 @@ SIGNATURES = {
     "icx_matmul_integer_noalloc": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, P], I),
     "icx_fused_chain_f32": ([P, P, S, S, ctypes.POINTER(Chain), P], I),
     "icx_qlinear_f32": ([P, P, I, P, I, I, P, S, S, S, P, P, S, P, ctypes.POINTER(Chain), P, P, S], I),
+    "icx_dql_qlinear_f32": ([P, P, S, S, P, P, P, P, I, P, S, ctypes.POINTER(Chain), P, P], I),
     "icx_cast_i32_f32": ([P, P, S, P], I),
     "icx_dequantize_linear_f32": ([P, P, I, P, P, S, S, S, P], I),
     "icx_gather": ([P, P, S, S, S, S, P, I, S, P], I),

@@ -79,6 +79,11 @@ struct GemmArgs {
     unsigned* q_sync;
     unsigned long long q_wait;  // exchange wait limit, wall-clock ticks
     unsigned q_poison;  // 0; the fault test hook makes block 0's wait expect tag ^ q_poison
+    // Quantized input (the GEMM runs the DynamicQuantizeLinear of its A operand itself): x
+    // f32 [M, K]; A (= qy) receives the DQL's y, q_scale / q_zp its scale and zero point,
+    // through the same exchange; each block quantizes q_rows rows of its row panel.
+    const float* xin;
+    int q_rows;
 };
 
 // Output of the tile whose first column is n0: base pointer, row stride and the global
@@ -216,6 +221,24 @@ struct EpiOperands {
             bzp = load_global(g.b_zp ? reinterpret_cast<const uint8_t*>(g.b_zp) + (g.b_zp_len == 1 ? 0 : c) : &kZeroByte);
         }
         if (g.rowsum_raw && wid < RG) rsum = load_global(g.rowsum_raw + min(m0 + wid * 64 + lane, g.M - 1));
+    }
+
+    // The fused DQL + GEMM launch loaded its activation scale and zero point before its
+    // blocks had computed them: put the values in (every chain factor read from the scale's
+    // address is a scalar operand; the host checks that).
+    __device__ __forceinline__ void patch_dql(const GemmArgs& g, int wid, float xs, uint8_t zp) {
+        azp = zp;
+        if constexpr (OPS) {
+            const int og = wid / CG;
+#pragma unroll
+            for (int i = 0; i < OPW; ++i) {
+                const int k = og * OPW + i;
+                const icx_chain_op& op = g.chain.ops[min(k, ICX_MAX_CHAIN - 1)];
+                const bool live = k < g.chain.n_ops && icx::op_takes_operand(op.op);
+                if (live && op.p0 == g.q_scale) f0[i] = xs;
+                if (live && op.p1 == g.q_scale) f1[i] = xs;
+            }
+        }
     }
 
     // Column terms (the zero-point correction's per-column part and factor), chain operands
@@ -498,6 +521,15 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
                  : "memory", "m0");
 }
 
+// The same copy with the sc1 (agent-scope coherence) cache bit: it reads what agent-scope
+// stores of other CUs wrote, not an older copy of the line in this CU's or XCD's caches.
+__device__ __forceinline__ void dma16s_coherent(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_addr)
+                 : "memory", "m0");
+}
+
 __device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -773,8 +805,22 @@ __device__ __forceinline__ void qout_epilogue(const GemmArgs& g, v16i (&acc)[BM 
 // into LDS than three 128x128 tiles per CU; 128x96 with 12 waves of 32x32 for shapes that
 // give every CU one or more of those; and 64x96 with 6 waves of 32x32, two blocks per CU,
 // where 128x96 would give about one (the FFN-down and output projection: 512 tiles).
-template <int BM, int BN, int WGM, int WGN, int OUT, int CH, int QOUT = 0>
+// QIN: the launch also runs the DynamicQuantizeLinear of A from x (GemmArgs::xin).  Before
+// its main loop, block (tm, tn) reads its q_rows rows of row panel tm into registers (QV
+// float4 per lane), trades (min, max) with every block through the range exchange, quantizes
+// its rows into A and publishes them (its tagged panel word); it streams its weight stages
+// into LDS meanwhile, waits for the panel words of the other blocks of panel tm, and only
+// then copies A.  The panel's rows cross XCDs (each XCD has its own L2): they are written
+// with agent-scope stores (the sc1 bit: through to memory), every wave waits for its stores
+// to complete before the barrier after which the panel word is written, and A is copied with
+// sc1 loads, which do not take a stale line from this CU's or XCD's caches — the ordering an
+// agent-scope release / acquire gives atomics, without the fences' passes over the whole L2
+// (measured: 3.6 us of a 39 us launch).
+constexpr int QV = 4;
+
+template <int BM, int BN, int WGM, int WGN, int OUT, int CH, int QOUT = 0, int QIN = 0>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs g) {
+    static_assert(!(QOUT && QIN), "one exchange per launch");
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TI = WM / 32, TJ = WN / 32;
     constexpr int ROWB = 128;
@@ -821,14 +867,24 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
     __shared__ unsigned s_qtag;
     unsigned q_tag0 = 0;
     if (QOUT != 0 && t == 0) q_tag0 = icx::qx::read_tag(g.q_sync);
-    auto issue = [&](int buf, int kt) {
+    auto issue_a = [&](int buf, int kt) {
         if (!copier) return;
         const int8_t* a = g.A + kt * ROWB;
+#pragma unroll
+        for (int i = 0; i < PA; ++i) {
+            if constexpr (QIN != 0) dma16s_coherent(a, offA[i], lds_a + buf * STAGE + i * 8 * ROWB);
+            else dma16s(a, offA[i], lds_a + buf * STAGE + i * 8 * ROWB);
+        }
+    };
+    auto issue_b = [&](int buf, int kt) {
+        if (!copier) return;
         const int8_t* b = g.Bp + kt * ROWB;
 #pragma unroll
-        for (int i = 0; i < PA; ++i) dma16s(a, offA[i], lds_a + buf * STAGE + i * 8 * ROWB);
-#pragma unroll
         for (int i = 0; i < PB; ++i) dma16s(b, offB[i], lds_b + buf * STAGE + i * 8 * ROWB);
+    };
+    auto issue = [&](int buf, int kt) {
+        issue_a(buf, kt);
+        issue_b(buf, kt);
     };
 
     v16i acc[TI][TJ];
@@ -871,10 +927,75 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
     // complete in issue order, so the stage-0 wait below also covers them, and the main
     // loop's waits count the same copies as without them
     EpiOperandsFor<BM, BN, WGM, WGN, OUT, CH> eo;
-    issue(0, 0);
-    eo.load(g, m0, n0, __builtin_amdgcn_readfirstlane(wid), lane);
-    issue(1, min(1, KT - 1));
-    wait_vmcnt<PA + PB>();  // stage 0 has landed
+    if constexpr (QIN != 0) {
+        constexpr int NT = 64 * WGM * WGN;
+        __shared__ unsigned s_itag;
+        __shared__ int s_late;
+        if (t == 0) {
+            s_itag = icx::qx::read_tag(g.q_sync);
+            s_late = 0;
+        }
+        const int rows_m = min(BM, g.M - m0);
+        const int r0 = min(tn * g.q_rows, rows_m), r1 = min(r0 + g.q_rows, rows_m);
+        const int n4 = (r1 - r0) * (g.K / 4);
+        const float4* xs4 = reinterpret_cast<const float4*>(g.xin + (size_t)(m0 + r0) * g.K);
+        float4 xv[QV];
+#pragma unroll
+        for (int u = 0; u < QV; ++u) {
+            const int q = t + u * NT;
+            xv[u] = q < n4 ? xs4[q] : make_float4(0.f, 0.f, 0.f, 0.f);  // 0.0 never moves the range
+        }
+        float qmn = 0.0f, qmx = 0.0f;
+#pragma unroll
+        for (int u = 0; u < QV; ++u) icx::dql::acc4(xv[u], qmn, qmx);
+        icx::dql::block_minmax<NT>(qmn, qmx);  // its barrier also publishes s_itag
+        const unsigned tag = s_itag;
+        if (t == 0) icx::qx::publish(g.q_sync, tag, qmn, qmx);
+        // the weight's first two stages and the epilogue operands stream in during the exchange
+        issue_b(0, 0);
+        eo.load(g, m0, n0, __builtin_amdgcn_readfirstlane(wid), lane);
+        issue_b(1, min(1, KT - 1));
+        bool ok;
+        const icx::dql::DqlParams p = icx::qx::gather<NT>(g.q_sync, tag, tag ^ g.q_poison, g.q_wait, ok);
+        uint32_t* ya = reinterpret_cast<uint32_t*>(g.qy + (size_t)(m0 + r0) * g.K);
+#pragma unroll
+        for (int u = 0; u < QV; ++u) {
+            const int q = t + u * NT;
+            if (q < n4)
+                __hip_atomic_store(ya + q, ok ? icx::dql::quant4(xv[u], p) : 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (t == 0) icx::qx::finish(g.q_sync, ok, p, g.q_scale, g.q_zp);
+        // every wave's rows in memory before the block's panel word says they are there
+        wait_vmcnt<0>();
+        __syncthreads();
+        unsigned* pw = icx::qx::panel(g.q_sync) + tm * g.tiles_n;
+        if (t == 0) __hip_atomic_store(pw + tn, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t < g.tiles_n) {
+            const unsigned long long t0 = wall_clock64();
+            while (__hip_atomic_load(pw + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag) {
+                if (wall_clock64() - t0 > g.q_wait) {
+                    s_late = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        __syncthreads();  // the copies of A (coherent loads) start after every panel word was seen
+        const bool good = ok && s_late == 0;
+        if (t == 0 && ok && !good)
+            __hip_atomic_fetch_add(g.q_sync + icx::kQoutErrWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        eo.patch_dql(g, __builtin_amdgcn_readfirstlane(wid), good ? (float)p.s : __builtin_nanf(""),
+                     (uint8_t)p.zp);
+        issue_a(0, 0);
+        issue_a(1, min(1, KT - 1));
+        wait_vmcnt<PA>();  // stage 0 has landed (the wait before the panel word covered the weight's)
+    } else {
+        issue(0, 0);
+        eo.load(g, m0, n0, __builtin_amdgcn_readfirstlane(wid), lane);
+        issue(1, min(1, KT - 1));
+        wait_vmcnt<PA + PB>();  // stage 0 has landed
+    }
     __syncthreads();
     read_q(0, 0, fa0, fb0);
     // Per stage: the reads of K step q+1 are issued before the MFMAs of step q; between
@@ -1463,6 +1584,26 @@ int launch_qout(unsigned blocks, hipStream_t s, const GemmArgs& g) {
     return ICX_OK;
 }
 
+template <int CH>
+int launch_qin(unsigned blocks, hipStream_t s, const GemmArgs& g) {
+    auto kern = gemm_i8_dma128_kernel<256, 192, 4, 3, OUT_F32, CH, 0, 1>;
+    static int per_cu[64] = {0};
+    int d = 0;
+    ICX_HIP_CHECK(hipGetDevice(&d));
+    if (d < 0 || d >= 64) ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: device index %d", d);
+    if (!per_cu[d]) {
+        int n = 0;
+        ICX_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 768, 0));
+        per_cu[d] = n > 0 ? n : -1;
+    }
+    if (per_cu[d] < 0 || blocks > (unsigned)(per_cu[d] * icx::num_cus()))
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: %u blocks exceed the %d resident ones", blocks,
+                 per_cu[d] * icx::num_cus());
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(768), 0, s, g);
+    ICX_LAUNCH_CHECK("gemm_i8_dma128_kernel (quantized input)");
+    return ICX_OK;
+}
+
 int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,
                 int b_packed, const int32_t* b_colsum, size_t M, size_t K, size_t N,
                 const void* a_zp, const void* b_zp, size_t b_zp_len, const int32_t* a_rowsum,
@@ -1786,6 +1927,86 @@ int icx::qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp
         return launch_qout<CH_COL_EXT>(blocks, s, g);
     }
     return launch_qout<CH_COL>(blocks, s, g);
+}
+
+int icx::dql_qlinear(hipStream_t s, const float* x, size_t M, size_t K, uint8_t* y, float* y_scale,
+                     uint8_t* y_zp, const int8_t* Bp, int b_dtype, const int32_t* b_colsum, size_t N,
+                     const icx_chain* chain, float* Y, unsigned* sync) {
+    if (!x || !y || !y_scale || !y_zp || !Bp || !b_colsum || !Y || !sync)
+        ICX_FAIL(ICX_ERR_INVALID_ARG, "DQL+QLinear: null pointer");
+    if (b_dtype != ICX_I8) ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: needs an Int8 weight (dtype %d)", b_dtype);
+    if (M == 0 || M > 0x7fffffff || K > 0x7fffffff || N > 0x7fffffff || K < 128 || K % 128 != 0 ||
+        N % 192 != 0 || (uint64_t)M * K > 0xffffffffull || (uint64_t)N * K > 0xffffffffull ||
+        !icx::aligned16(x) || !icx::aligned16(y) || !icx::aligned16(Bp))
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: shape %zux%zux%zu or alignment outside the 256x192 kernel",
+                 M, K, N);
+    const size_t tiles_m = icx::cdiv(M, 256), tiles_n = N / 192;
+    const size_t blocks = tiles_m * tiles_n;
+    if (blocks > (size_t)icx::kQoutMaxBlocks)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: %zu tiles exceed %d", blocks, icx::kQoutMaxBlocks);
+    // every block quantizes q_rows rows of its row panel, QV float4 per lane of 768
+    const size_t q_rows = icx::cdiv(256, tiles_n);
+    if (q_rows * K > (size_t)QV * 4 * 768)
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: %zu rows of %zu per block exceed the registers", q_rows, K);
+    GemmArgs g{};
+    if (chain) {
+        int rc = icx::validate_chain(chain, "DQL+QLinear");
+        if (rc) return rc;
+        g.chain = *chain;
+    } else {
+        g.chain.n_ops = 0;
+    }
+    if (!icx::chain_is_col_only(g.chain))
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: the epilogue has row or full-tensor operands");
+    for (int k = 0; k < g.chain.n_ops; ++k) {  // the activation scale is computed in the launch
+        const icx_chain_op& op = g.chain.ops[k];
+        if ((op.p0 == y_scale && op.kind0 != ICX_BCAST_SCALAR) || (op.p1 == y_scale && op.kind1 != ICX_BCAST_SCALAR))
+            ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: the DQL scale is read as a non-scalar operand");
+    }
+    g.A = reinterpret_cast<const int8_t*>(y);
+    g.Bp = Bp;
+    g.colsum = b_colsum;
+    g.a_zp = y_zp;
+    g.C = Y;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.tiles_m = (int)tiles_m;
+    g.tiles_n = (int)tiles_n;
+    g.a_xor = 0x80808080u;
+    g.alpha = 128;
+    g.beta = 0;
+    g.a_zp_u8 = 1;
+    g.b_zp_len = 1;
+    g.codes = icx::chain_codes(g.chain);
+    g.xin = x;
+    g.q_rows = (int)q_rows;
+    g.qy = y;
+    g.q_scale = y_scale;
+    g.q_zp = y_zp;
+    g.q_sync = sync;
+    g.q_wait = icx::wall_ticks(icx::kExchangeWaitUs);
+    g.q_poison = 0;
+    if (const int f = icx::qout_fault_spin()) {  // test hook
+        g.q_wait = icx::wall_ticks((unsigned)f);
+        g.q_poison = 0x80000000u;
+    }
+    if (icx::chain_mode(g.chain) == 2) {
+        if (!icx::is_gelu8(g.codes, g.chain.n_ops))
+            ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: an operand-free chain other than the erf-GELU");
+        return launch_qin<CH_COL_EXT>((unsigned)blocks, s, g);
+    }
+    return launch_qin<CH_COL>((unsigned)blocks, s, g);
+}
+
+extern "C" int icx_dql_qlinear_f32(icx_stream_t stream, const float* x, size_t M, size_t K, uint8_t* y,
+                                   float* y_scale, uint8_t* y_zp, const void* B, int b_dtype,
+                                   const int32_t* b_colsum, size_t N, const icx_chain* chain, float* Y,
+                                   void* sync) {
+    icx::clear_error();
+    return icx::dql_qlinear(reinterpret_cast<hipStream_t>(stream), x, M, K, y, y_scale, y_zp,
+                            reinterpret_cast<const int8_t*>(B), b_dtype, b_colsum, N, chain, Y,
+                            static_cast<unsigned*>(sync));
 }
 
 int icx::qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, int b_dtype,

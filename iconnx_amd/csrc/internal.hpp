@@ -81,14 +81,27 @@ int qlinear_f32_seg(hipStream_t s, const void* A, int a_dtype, const void* B, in
 // ICX_ERR_UNSUPPORTED, having launched nothing, for a shape outside the kernel or a grid
 // that would not be resident at once.
 constexpr int kQoutMaxBlocks = 1024;  // blocks of one quantized-output launch
-// qexchange.hpp's layout: words and the launch's result, a tagged pair per block, 9 counters
-constexpr size_t kQoutSyncBytes = 256 + 16 * (size_t)kQoutMaxBlocks + 9 * 128;
+// qexchange.hpp's layout: words and the launch's result, a tagged pair per block, 9 counters,
+// a tagged word per block
+constexpr size_t kQoutSyncBytes = 256 + 16 * (size_t)kQoutMaxBlocks + 9 * 128 + 4 * (size_t)kQoutMaxBlocks;
 constexpr int kQoutErrWord = 2;  // word of that buffer counting launches whose exchange failed
 // icx_matmul_integer_noalloc's file-scope device scratch (one per GPU, for the process's life)
 constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 int qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int b_dtype, const int32_t* b_colsum,
                 size_t M, size_t K, size_t N, const void* a_zp, const icx_chain* chain, uint8_t* y,
                 float* y_scale, uint8_t* y_zp, unsigned* sync);
+
+// icx_dynamic_quantize_linear of x [M, K] (y, y_scale, y_zp) and the quantized linear that
+// reads it (icx_qlinear_f32 with A = y, its zero point y_zp, packed Int8 weight without zero
+// point) as one launch, the blocks trading ranges and row-panel slices through `sync`
+// (qlinear_dql's buffer and contract).  Y and the DQL outputs equal those of the two calls
+// bit for bit.  K % 128 == 0, N % 192 == 0, column-only chain whose reads of y_scale are
+// scalar, every block's share of its 256-row panel within its registers (N / 192 tiles per
+// panel), 16-byte aligned x, y and weight, a grid of at most kQoutMaxBlocks resident
+// blocks; otherwise ICX_ERR_UNSUPPORTED, having launched nothing.
+int dql_qlinear(hipStream_t s, const float* x, size_t M, size_t K, uint8_t* y, float* y_scale, uint8_t* y_zp,
+                const int8_t* Bp, int b_dtype, const int32_t* b_colsum, size_t N, const icx_chain* chain, float* Y,
+                unsigned* sync);
 
 // Synchronise `s`, then read and clear the exchange buffer's sticky error word:
 // ICX_ERR_KERNEL (with a message) if any launch since the last check gave up waiting.

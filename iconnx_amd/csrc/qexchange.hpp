@@ -12,6 +12,9 @@
 //               halves, written by block 0
 //   bytes 256+  two such tagged words per block: its own (min, max)
 //   then        kGroups + 1 counters of published blocks, one per 128-byte line
+//   then        one word per block, tagged E + 1 when the block's slice of a GEMM's
+//               quantized input is in memory (the fused DQL + GEMM launch: the blocks of a
+//               row panel wait for each other's slices before their main loop)
 // A tag tells a reader that a word is this launch's as soon as it sees it (zeroed memory
 // never matches), so nothing is cleared between launches.  Each block publishes its pair;
 // block 0 alone polls all pairs (one round trip per round for the whole grid; polls by
@@ -52,6 +55,8 @@ namespace qx {
 
 constexpr int kGroups = 8;
 constexpr size_t kCountOff = 256 + 16 * (size_t)kQoutMaxBlocks;
+constexpr size_t kPanelOff = kCountOff + 128 * (kGroups + 1);
+static_assert(kPanelOff + 4 * (size_t)kQoutMaxBlocks == kQoutSyncBytes, "exchange buffer layout");
 
 __device__ __forceinline__ unsigned long long* slots(unsigned* sync) {
     return reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(sync) + 256);
@@ -61,6 +66,9 @@ __device__ __forceinline__ unsigned long long* result(unsigned* sync) {
 }
 __device__ __forceinline__ unsigned* counter(unsigned* sync, int k) {  // k < kGroups: group, kGroups: top
     return reinterpret_cast<unsigned*>(reinterpret_cast<char*>(sync) + kCountOff + 128 * k);
+}
+__device__ __forceinline__ unsigned* panel(unsigned* sync) {
+    return reinterpret_cast<unsigned*>(reinterpret_cast<char*>(sync) + kPanelOff);
 }
 
 // E + 1 for this launch; read it early (before the main work) to hide the latency, in one

@@ -326,6 +326,39 @@ def gpu_qlinear(a, b, a_zp=None, b_zp=None, epilogue=(), a_rowsum=None, out=None
     return y
 
 
+def exchange_buffer():
+    """A zeroed exchange buffer (icx_exchange_buffer_size() bytes) for the single-launch
+    entry points; keep it and pass it to every later call on the same stream."""
+    return torch.zeros(lib().icx_exchange_buffer_size(), dtype=torch.uint8, device="cuda")
+
+
+def gpu_dql_qlinear(x, b, epilogue, sync, out=None):
+    """DynamicQuantizeLinear(x) and the quantized linear that reads it, as one launch:
+    returns (y u8, y_scale, y_zp, Y f32), equal bit for bit to gpu_dynamic_quantize_linear(x)
+    followed by gpu_qlinear(y, b, y_zp, epilogue=...).  ``b``: a PackedWeight of an Int8
+    weight (no zero point); ``epilogue(y_scale)`` returns the chain (its reads of the scale,
+    e.g. ("Mul", (y_scale, w_scale), False), see the DQL's output tensor); ``sync`` from
+    exchange_buffer().  Raises IconnxError(ICX_ERR_UNSUPPORTED) for shapes outside the fused
+    kernel."""
+    if x.dtype != torch.float32 or x.dim() != 2:
+        raise IconnxError(ERR_DTYPE, "DQL+QLinear: x must be a 2-D Float32 tensor")
+    if not isinstance(b, PackedWeight):
+        raise IconnxError(ERR_INVALID, "DQL+QLinear: the weight must be a PackedWeight")
+    _require_cuda(x, sync)
+    x = x.contiguous()
+    M, K = x.shape
+    N = b.shape[1]
+    y = torch.empty((M, K), dtype=torch.uint8, device=x.device)
+    ys = torch.empty((), dtype=torch.float32, device=x.device)
+    yz = torch.empty((), dtype=torch.uint8, device=x.device)
+    ch, keep = build_chain(list(epilogue(ys)), M, N)
+    Y = out if out is not None else torch.empty((M, N), dtype=torch.float32, device=x.device)
+    check(lib().icx_dql_qlinear_f32(_stream(), _p(x), M, K, _p(y), _p(ys), _p(yz), _p(b.packed),
+                                    _DT[b.dtype], _p(b.colsum), N, ctypes.byref(ch), _p(Y), _p(sync)))
+    del keep
+    return y, ys, yz, Y
+
+
 # ---------------------------------------------------------------------------------------
 # DequantizeLinear
 # ---------------------------------------------------------------------------------------

@@ -209,6 +209,26 @@ int icx_qlinear_f32(icx_stream_t stream, const void* A, int a_dtype, const void*
                     const int32_t* a_rowsum, const icx_chain* chain, float* Y, void* ws,
                     size_t ws_bytes);
 
+/* DynamicQuantizeLinear of x [M, K] and the quantized linear that reads its output, as ONE
+ * launch (no counterpart in the reference, which runs the DQL's host loop and then the
+ * linear's nodes): y, y_scale, y_zp are icx_dynamic_quantize_linear(x)'s outputs and Y is
+ * icx_qlinear_f32(A = y, a_zp = y_zp, packed Int8 B, colsum, no b zero point, chain)'s, bit
+ * for bit; the chain reads the activation scale as the scalar y_scale (e.g. its first op
+ * Mul(y_scale * w_scale)).  The GEMM's blocks compute the range of their slices of x, trade
+ * it through `sync` (an icx_exchange_buffer_size() buffer, as for
+ * icx_dynamic_quantize_linear_exchange: zeroed once, kept, calls sharing it must not overlap),
+ * quantize their slices into y and wait only for the slices of their own row panel.
+ * K % 128 == 0, N % 192 == 0 with at least about 16 column tiles per 256-row panel
+ * (256 / (N / 192) rows of K per block must fit its registers: 4 * 4 * 768 floats), column-
+ * only chain, x / y / B 16-byte aligned, at most 1024 resident blocks: otherwise
+ * ICX_ERR_UNSUPPORTED with nothing launched (call the two entry points instead).  A wait
+ * that runs out (blocks kept from running by other work) is reported by icx_exchange_status
+ * as ICX_ERR_KERNEL, with y_scale NaN. */
+int icx_dql_qlinear_f32(icx_stream_t stream, const float* x, size_t M, size_t K, uint8_t* y,
+                        float* y_scale, uint8_t* y_zp, const void* B, int b_dtype,
+                        const int32_t* b_colsum, size_t N, const icx_chain* chain, float* Y,
+                        void* sync);
+
 /* Cast INT32 -> FLOAT (src/operators/cast.rs:46-49; GPU src/cuda/ops/cast.rs:134-148). */
 int icx_cast_i32_f32(icx_stream_t stream, const int32_t* x, size_t n, float* y);
 
