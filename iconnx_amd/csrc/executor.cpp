@@ -274,6 +274,11 @@ struct icx_graph {
     // head's kernel writes itself when the shape allows (the f32 output is never formed): a
     // quantized linear's GEMM (icx::qlinear_dql) or an attention (icx::attention_dql)
     std::map<std::string, Node> quant_out;
+    // quantized-linear head output -> the DynamicQuantizeLinear whose outputs only that head
+    // reads: the head's launch runs the DQL too (icx::dql_qlinear); the DQL's own plan entry
+    // does nothing (names in qin_dql)
+    std::map<std::string, Node> qin;
+    std::set<std::string> qin_dql;
 
     // device state
     std::map<std::string, DevTensor> weights;      // uploaded initializers
@@ -285,6 +290,7 @@ struct icx_graph {
     std::map<std::string, std::pair<std::string, int>> range_of;  // DQL x -> (partials tensor, count)
     std::set<std::string> dql_done;  // DQL outputs already written by their producer's GEMM
     int64_t quant_fused = 0;         // head launches that quantized their own output
+    int64_t qin_fused = 0;           // head launches that ran their input's DQL too
     int64_t dql_single = 0;          // DynamicQuantizeLinear runs done as one launch
     unsigned* qsync = nullptr;       // range-exchange buffer of every launch that uses one (zeroed once)
     hipStream_t last_stream = nullptr;
@@ -512,6 +518,40 @@ class Planner {
             if (d.op != "DynamicQuantizeLinear" || d.in.size() != 1 || d.out.size() != 3) continue;
             if (g_.rowsum_wanted.count(d.out[0])) continue;
             g_.quant_out[op.out] = d;
+        }
+        // a DynamicQuantizeLinear whose outputs only one quantized-linear head reads (Int8
+        // weight without zero point, no sibling group, f32 output) and whose input no head
+        // leaves the range of: the head's GEMM launch runs the DQL too
+        g_.qin.clear();
+        g_.qin_dql.clear();
+        for (size_t i = 0; i < g_.plan.size() && g_.quant_out_on; ++i) {
+            const PlannedOp& op = g_.plan[i];
+            if (op.kind != Kind::FusedHead || op.pattern != Pattern::QuantizedLinear || !op.group.empty()) continue;
+            if (g_.inits[op.w].dtype != ICX_I8 || !(op.w_zp.empty() || op.w_zp_folded)) continue;
+            if (g_.quant_out.count(op.out)) continue;
+            auto pr = gi_.producer.find(op.a);
+            if (pr == gi_.producer.end()) continue;
+            const Node& d = nodes_[pr->second];
+            if (d.op != "DynamicQuantizeLinear" || d.in.size() != 1 || d.out.size() != 3 || op.a_zp != d.out[2])
+                continue;
+            if (g_.range_wanted.count(d.in[0]) || g_.rowsum_wanted.count(d.out[0])) continue;
+            std::set<std::string> mine = {op.node.name};
+            for (auto& m : op.members) mine.insert(m.name);
+            bool only = true;
+            for (auto& o : d.out) {
+                auto cs = gi_.consumers.find(o);
+                if (cs == gi_.consumers.end()) continue;
+                for (int c : cs->second) only = only && mine.count(nodes_[c].name) > 0;
+            }
+            bool regular = false;  // the DQL runs as a plan entry of its own (before the head)
+            for (size_t j = 0; j < i; ++j)
+                regular = regular || (g_.plan[j].kind == Kind::Regular && g_.plan[j].node.name == d.name);
+            if (!only || !regular) continue;
+            g_.qin[op.out] = d;
+            g_.qin_dql.insert(d.name);
+            // the DQL's input is read at the head now: keep its buffer until then
+            for (auto& x : {d.in[0], root_of(d.in[0])})
+                if (g_.last_use[x] < i) g_.last_use[x] = i;
         }
         g_.planned = true;
         return ICX_OK;
@@ -1965,9 +2005,54 @@ class Runner {
                                     rowsum, &ch, ys, n_seg, g_.ws, g_.ws_bytes);
     }
 
+    // The head whose input's DQL it runs in the same launch: ICX_OK when that launch ran
+    // (*done), else the DQL has run on its own and the head continues as usual.
+    int run_qin(const PlannedOp& op, const Node& d, bool* done) {
+        *done = false;
+        const DevTensor* X;
+        int rc = need_f32(d.in[0], &X, "DynamicQuantizeLinear");
+        if (rc) return rc;
+        auto pk = g_.packed.find(op.w);
+        const int64_t K = X->shape.empty() ? 0 : X->shape.back();
+        if (g_.qsync && pk != g_.packed.end() && K == pk->second.K && K > 0 && !X->shape.empty()) {
+            const PackedW& pw = pk->second;
+            const std::vector<int64_t> xshape = X->shape;
+            const int64_t M = numel(xshape) / K;
+            std::vector<int64_t> oshape(xshape.begin(), xshape.end() - 1);
+            oshape.push_back(pw.N);
+            DevTensor *QY, *QS, *QZ, *Y;
+            rc = alloc(d.out[0], ICX_U8, xshape, &QY);
+            if (!rc) rc = alloc(d.out[1], ICX_F32, {}, &QS);
+            if (!rc) rc = alloc(d.out[2], ICX_U8, {}, &QZ);
+            if (rc) return rc;
+            icx_chain ch;
+            rc = make_chain(op.steps, oshape, ch, "QuantizedLinear");
+            if (!rc) rc = alloc(op.out, ICX_F32, oshape, &Y);
+            if (rc) return rc;
+            const float* x = static_cast<const float*>(find(d.in[0])->ptr);
+            rc = icx::dql_qlinear(s_, x, (size_t)M, (size_t)K, static_cast<uint8_t*>(QY->ptr),
+                                  static_cast<float*>(QS->ptr), static_cast<uint8_t*>(QZ->ptr), pw.packed, pw.dtype,
+                                  pw.colsum, pw.N, &ch, static_cast<float*>(Y->ptr), g_.qsync);
+            if (rc == ICX_OK) {
+                ++g_.qin_fused;
+                *done = true;
+                return ICX_OK;
+            }
+            if (rc != ICX_ERR_UNSUPPORTED) return rc;
+            icx::clear_error();  // shape outside the fused kernel: the DQL on its own, then the GEMM
+        }
+        return run_dql(d, true);
+    }
+
     int run_qlinear(const PlannedOp& op) {
         if (!op.group.empty())  // members other than the lead were written by its launch
             return op.group_members.empty() ? ICX_OK : run_qlinear_group(op);
+        auto qi = g_.qin.find(op.out);
+        if (qi != g_.qin.end()) {
+            bool done;
+            int rc = run_qin(op, qi->second, &done);
+            if (rc || done) return rc;
+        }
         const DevTensor* A;
         int rc = need(op.a, &A, "QuantizedLinear");
         if (rc) return rc;
@@ -2412,13 +2497,14 @@ class Runner {
                                   nullptr, static_cast<int32_t*>(C->ptr), g_.ws, g_.ws_bytes);
     }
 
-    int run_dql(const Node& n) {
+    int run_dql(const Node& n, bool from_head = false) {
         if (n.in.size() != 1 || n.out.size() != 3) {
             set_error("DynamicQuantizeLinear: expected 1 input and 3 outputs, got %zu and %zu", n.in.size(),
                       n.out.size());
             return ICX_ERR_INVALID_ARG;
         }
         if (g_.dql_done.count(n.out[0])) return ICX_OK;  // its producer's GEMM wrote y, scale, zp
+        if (!from_head && g_.qin_dql.count(n.name)) return ICX_OK;  // its reader's launch runs it
         const DevTensor* X;
         int rc = need(n.in[0], &X, "DynamicQuantizeLinear");
         if (rc) return rc;
@@ -3388,6 +3474,8 @@ static int icx_graph_plan_impl(icx_graph* g, char* buf, size_t buf_len) {
         for (auto& r : g->range_wanted) o << "range " << r << "\n";
         for (auto& q : g->quant_out) o << "quantout " << q.first << " " << q.second.name << "\n";
         if (g->quant_fused) o << "quantout-launches " << g->quant_fused << "\n";
+        for (auto& q : g->qin) o << "quantin " << q.first << " " << q.second.name << "\n";
+        if (g->qin_fused) o << "quantin-launches " << g->qin_fused << "\n";
         if (g->dql_single) o << "dql-single-launches " << g->dql_single << "\n";
         const std::string s = o.str();
         if (s.size() + 1 > buf_len)

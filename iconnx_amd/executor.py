@@ -219,7 +219,8 @@ class GpuGraphExecutor:
     def set_option(self, name, value):
         """Planner option; ``"quantized_outputs"``: True (default) lets a head whose output
         only a DynamicQuantizeLinear reads write that DQL's outputs in the same launch, False
-        runs every DQL as its own launch (bit-identical results).  Replans at the next run."""
+        runs every DQL as its own launch (bit-identical results), also the DQL that a quantized
+        linear's launch would run for its own input.  Replans at the next run."""
         check(self._L.icx_graph_set_option(self._g, name.encode(), int(value)))
 
     # ---- lowering -------------------------------------------------------------------------
@@ -236,8 +237,8 @@ class GpuGraphExecutor:
             if "buffer has" not in msg or size > (1 << 26):
                 check(rc)
             size *= 4
-        entries, rowsums, ranges, quant_out = [], [], [], {}
-        self._quant_launches = self._dql_single = 0
+        entries, rowsums, ranges, quant_out, quant_in = [], [], [], {}, {}
+        self._quant_launches = self._dql_single = self._qin_launches = 0
         for line in buf.value.decode().splitlines():
             parts = line.split()
             if parts[0] == "rowsum":
@@ -252,6 +253,12 @@ class GpuGraphExecutor:
             if parts[0] == "quantout-launches":
                 self._quant_launches = int(parts[1])
                 continue
+            if parts[0] == "quantin":
+                quant_in[parts[1]] = parts[2]
+                continue
+            if parts[0] == "quantin-launches":
+                self._qin_launches = int(parts[1])
+                continue
             if parts[0] == "dql-single-launches":
                 self._dql_single = int(parts[1])
                 continue
@@ -261,6 +268,7 @@ class GpuGraphExecutor:
                                      extra.get("wzp") == "folded", extra.get("group")))
         self._range_inputs = ranges
         self._quant_out = quant_out
+        self._quant_in = quant_in
         return entries, rowsums
 
     def quantized_outputs(self):
@@ -270,6 +278,13 @@ class GpuGraphExecutor:
         far did that."""
         self.plan()
         return dict(self._quant_out), self._quant_launches
+
+    def quantized_inputs(self):
+        """Quantized-linear head outputs whose input's DynamicQuantizeLinear (read by that head
+        alone) the head's GEMM launch runs too, mapped to that DQL node; second value: how many
+        head launches so far did that (the others ran the DQL on its own first)."""
+        self.plan()
+        return dict(self._quant_in), self._qin_launches
 
     def single_launch_dqls(self):
         """How many DynamicQuantizeLinear runs so far were one launch (the blocks trading

@@ -181,3 +181,42 @@ def test_repeated_calls_smaller_input_capture_and_failure():
     assert L.icx_exchange_status(ops._stream(), ops._p(sync)) == 0  # cleared
     xd = dev(x)
     assert_same(ops.gpu_dql_qlinear(xd, w, epi, sync), separate(xd, w, epi), "after the failure")
+
+
+# ---- through the graph executor -----------------------------------------------------------
+def qlinear_graph(ex, K, N, gelu, seed):
+    from tests.test_gpu_quant_out import build
+    h = build(ex, K, N, gelu, seed)
+    ex.add_node("after", "Add", [h, h], ["out"])  # a reader other than a DQL: h is formed
+    return h
+
+
+@pytest.mark.parametrize("M,K,N,gelu,fused", [
+    (4096, 768, 3072, False, True),   # cfg2's shape
+    (1000, 768, 3072, True, True),    # erf-GELU chain, ragged last panel
+    (4096, 768, 768, False, False),   # 64 rows per block: the DQL runs on its own first
+])
+def test_executor_runs_the_input_dql_in_the_gemm_launch(M, K, N, gelu, fused):
+    """GpuGraphExecutor plans the DQL whose outputs only one quantized-linear head reads into
+    that head's launch; the results equal the same graph with the fusions off (every DQL its
+    own launch), including the DQL's outputs requested as graph outputs."""
+    from iconnx_amd.executor import GpuGraphExecutor
+
+    x = (np.random.default_rng(M + N).standard_normal((M, K)) * 2.0).astype(np.float32)
+    ex, ref_ex = GpuGraphExecutor(), GpuGraphExecutor()
+    h = qlinear_graph(ex, K, N, gelu, seed=3)
+    qlinear_graph(ref_ex, K, N, gelu, seed=3)
+    ref_ex.set_option("quantized_outputs", False)
+    names = ["out", h, "xq", "xs", "xzp"]
+    want = ref_ex.run({"x": x}, names)
+    assert ref_ex.quantized_inputs() == ({}, 0)
+    for rep in range(2):
+        got = ex.run({"x": x * (1.0 + rep)}, names)
+        want = ref_ex.run({"x": x * (1.0 + rep)}, names)
+        for n in names:
+            bad = int(np.count_nonzero(bits(got[n]) != bits(want[n])))
+            assert bad == 0, "run %d %s: %d of %d differ" % (rep, n, bad, want[n].size)
+    planned, launches = ex.quantized_inputs()
+    assert planned == {h: "dql_x"}
+    assert launches == (2 if fused else 0)
+    ex.check_status()
