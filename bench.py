@@ -5,9 +5,11 @@
 A step is one pass of the hot path over one batch of synthetic, HBM-resident input.  The
 default workload is BASELINE configs[1] (cfg2): x [32,128,768] f32 ->
 DynamicQuantizeLinear -> MatMulInteger with W int8 [768,3072] -> Cast -> Mul(x_scale *
-w_scale) -> Add(bias) -> Mul/Add/Div/Mul chain, i.e. two kernel launches: the DQL as one
-launch whose blocks trade their (min, max) through an exchange buffer kept from step to step
-(icx_dynamic_quantize_linear_exchange), then the fused GEMM.  Where a GEMM needs the DQL's
+w_scale) -> Add(bias) -> Mul/Add/Div/Mul chain, as ONE kernel launch (icx_dql_qlinear_f32):
+the GEMM's blocks compute the range of their slices of x, trade it through an exchange buffer
+kept from step to step, quantize their rows and multiply once their row panel is complete.
+Where that kernel does not take the shape, the DQL is its own launch
+(icx_dynamic_quantize_linear_exchange) before the fused GEMM; where a GEMM needs the DQL's
 row sums (cfg4's weight zero points) or the input is past that launch's limit, the DQL is
 the two launches of icx_dynamic_quantize_linear (min/max, quantize).  The same run also reports the metric's second part,
 encoder seq/s (cfg3: the 6-layer DistilBERT-int8-shaped encoder at batch 32, seq 128, one
