@@ -264,6 +264,7 @@ struct icx_graph {
     // plan
     bool planned = false, compiled = false;
     bool quant_out_on = true;  // option "quantized_outputs"
+    bool qin_on = true;        // option "quantized_inputs" (with quantized_outputs)
     std::vector<PlannedOp> plan;
     std::vector<std::string> live_outputs;     // requested outputs, or the sinks
     std::set<std::string> keep;                // tensors that stay until the next run
@@ -524,7 +525,7 @@ class Planner {
         // leaves the range of: the head's GEMM launch runs the DQL too
         g_.qin.clear();
         g_.qin_dql.clear();
-        for (size_t i = 0; i < g_.plan.size() && g_.quant_out_on; ++i) {
+        for (size_t i = 0; i < g_.plan.size() && g_.quant_out_on && g_.qin_on; ++i) {
             const PlannedOp& op = g_.plan[i];
             if (op.kind != Kind::FusedHead || op.pattern != Pattern::QuantizedLinear || !op.group.empty()) continue;
             if (g_.inits[op.w].dtype != ICX_I8 || !(op.w_zp.empty() || op.w_zp_folded)) continue;
@@ -535,6 +536,7 @@ class Planner {
             if (d.op != "DynamicQuantizeLinear" || d.in.size() != 1 || d.out.size() != 3 || op.a_zp != d.out[2])
                 continue;
             if (g_.range_wanted.count(d.in[0]) || g_.rowsum_wanted.count(d.out[0])) continue;
+            if (g_.quant_out.count(d.in[0])) continue;  // its producer writes this DQL's outputs itself
             std::set<std::string> mine = {op.node.name};
             for (auto& m : op.members) mine.insert(m.name);
             bool only = true;
@@ -3426,10 +3428,13 @@ extern "C" int icx_graph_set_node_attr_ints(icx_graph* g, const char* node, cons
 extern "C" int icx_graph_set_option(icx_graph* g, const char* name, int64_t value) {
     icx::clear_error();
     if (!g || !name) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_option: bad arguments");
-    if (std::strcmp(name, "quantized_outputs") == 0) {
-        if (value != 0 && value != 1) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_option: quantized_outputs is 0 or 1");
-        if (g->quant_out_on != (value != 0)) {
-            g->quant_out_on = value != 0;
+    bool* flag = nullptr;
+    if (std::strcmp(name, "quantized_outputs") == 0) flag = &g->quant_out_on;
+    if (std::strcmp(name, "quantized_inputs") == 0) flag = &g->qin_on;
+    if (flag) {
+        if (value != 0 && value != 1) ICX_FAIL(ICX_ERR_INVALID_ARG, "set_option: %s is 0 or 1", name);
+        if (*flag != (value != 0)) {
+            *flag = value != 0;
             g->invalidate();
         }
         return ICX_OK;

@@ -220,7 +220,8 @@ class GpuGraphExecutor:
         """Planner option; ``"quantized_outputs"``: True (default) lets a head whose output
         only a DynamicQuantizeLinear reads write that DQL's outputs in the same launch, False
         runs every DQL as its own launch (bit-identical results), also the DQL that a quantized
-        linear's launch would run for its own input.  Replans at the next run."""
+        linear's launch would run for its own input; ``"quantized_inputs"`` turns off that
+        second fusion alone.  Replans at the next run."""
         check(self._L.icx_graph_set_option(self._g, name.encode(), int(value)))
 
     # ---- lowering -------------------------------------------------------------------------

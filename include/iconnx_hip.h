@@ -370,8 +370,10 @@ int icx_graph_add_output(icx_graph* g, const char* name);
 /* A planner option (no counterpart in the reference, whose nodes always run one by one):
  *   "quantized_outputs" 1 (default) / 0 — whether a head whose output only a
  *   DynamicQuantizeLinear reads (quantized linear, attention) may write that DQL's outputs
- *   itself in the same launch; 0 runs every DQL as its own launch (the results are
+ *   itself in the same launch, and a quantized linear may run the DQL of its own input
+ *   (icx_dql_qlinear_f32's kernel); 0 runs every DQL as its own launch (the results are
  *   bit-identical either way; the option isolates the fused kernels when checking that).
+ *   "quantized_inputs" 1 (default) / 0 — the second part alone.
  * ICX_ERR_INVALID_ARG for an unknown name or value.  Takes effect at the next plan. */
 int icx_graph_set_option(icx_graph* g, const char* name, int64_t value);
 /* Host passes only (topological sort, fusion decision, zero-point folding); no GPU work.
