@@ -18,10 +18,13 @@ DistilBERT-INT8 export writes it (Int64 ids and mask, embeddings, runtime shapes
 --config cfg3 makes the encoder the primary line; the other configs (cfg1|cfg4|cfg5a|cfg5b)
 are for the per-kernel roofline figures.
 
-Timing: W untimed warmup steps, then exactly K steps, each a replay of a HIP graph that
-holds one step (so host launch overhead is not measured), bracketed by synchronize.  The
-dominant kernel's average duration is measured live with HIP events around a graph of R
-back-to-back launches of that kernel on the same stream.  Prints ONE JSON line.
+Timing: W untimed warmup steps, then exactly K steps launched back to back on one stream
+(each step's host-side launch overlaps the previous step's kernels), bracketed by
+synchronize; the same K steps as replays of a HIP graph holding one step are timed too and
+reported beside (--graph makes those the primary figure).  The encoder (cfg3) is one
+captured forward replayed per step.  The dominant kernel's average duration is measured live
+with HIP events around a graph of R back-to-back launches of that kernel on the same stream.
+Prints ONE JSON line.
 """
 import argparse
 import ctypes
@@ -52,7 +55,11 @@ def parse():
     ap.add_argument("--cpu-rows", type=int, default=None,
                     help="rows of the CPU-baseline sample (default: config-specific)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of graph replay")
+    ap.add_argument("--graph", action="store_true",
+                    help="time each step as the replay of a HIP graph holding that step instead of "
+                         "launching it directly (the other figure is reported beside it either way)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch the steps directly (the default; kept for older command lines)")
     ap.add_argument("--no-encoder", action="store_true",
                     help="cfg2: skip the secondary encoder seq/s measurement")
     return ap.parse_args()
@@ -521,23 +528,29 @@ def main():
     sync = torch.cuda.synchronize
 
     # ---- timed steps -------------------------------------------------------------------
-    if args.no_graph:
-        run_step = lambda: r.step(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))  # noqa: E731
-    else:
-        g_step = graph_of(r.step, 1, torch)
-        run_step = g_step.replay
-    for _ in range(args.warmup):
-        run_step()
-    sync()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        run_step()
-    ev1.record()
-    sync()
-    wall = time.perf_counter() - t0
-    ms_step = ev0.elapsed_time(ev1) / args.steps
+    # Steps are launched directly, back to back on one stream: each is one call of the C
+    # entry points (one kernel for cfg2), whose host-side launch overlaps the previous step's
+    # kernel.  The same K steps as replays of a HIP graph holding one step are timed too and
+    # reported beside (a graph launch per step leaves the GPU idle ~6 us between steps).
+    eager = lambda: r.step(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))  # noqa: E731
+    g_step = graph_of(r.step, 1, torch)
+
+    def timed(run_step):
+        for _ in range(args.warmup):
+            run_step()
+        sync()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record()
+        for _ in range(args.steps):
+            run_step()
+        ev1.record()
+        sync()
+        return ev0.elapsed_time(ev1) / args.steps, time.perf_counter() - t0
+
+    use_graph = args.graph and not args.no_graph
+    ms_step, wall = timed(g_step.replay if use_graph else eager)
+    ms_other, _ = timed(eager if use_graph else g_step.replay)
 
     # ---- dominant kernel: average launch duration over R back-to-back launches --------
     reps = args.kernel_reps
@@ -545,21 +558,12 @@ def main():
 
     def time_launches(fn):
         """Average duration of `reps` back-to-back launches of fn on the current stream."""
-        if args.no_graph:
-            h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-            fn(h)
-            sync()
-            k0.record()
-            for _ in range(reps):
-                fn(h)
-            k1.record()
-        else:
-            g = graph_of(fn, reps, torch)
-            g.replay()
-            sync()
-            k0.record()
-            g.replay()
-            k1.record()
+        g = graph_of(fn, reps, torch)
+        g.replay()
+        sync()
+        k0.record()
+        g.replay()
+        k1.record()
         sync()
         return k0.elapsed_time(k1) * 1e3 / reps
 
@@ -627,7 +631,10 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic: seeded N(0,1) activations (SplitMix64 + Box-Muller), random-init int8 weights",
         "config": cfg, "roofline": roof,
-        "timing": {"graph_replay": not args.no_graph, "wall_s": round(wall, 4), **extra},
+        "timing": {"launch": "graph replay per step" if use_graph else "direct, back to back",
+                   "wall_s": round(wall, 4),
+                   ("direct_ms_per_step" if use_graph else "graph_replay_ms_per_step"): round(ms_other, 6),
+                   **extra},
         **({"mfma": mfma} if mfma else {}),
         "traffic_source": "profiles/traffic_hbm_pmc.txt (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
     }
