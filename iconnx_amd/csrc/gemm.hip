@@ -956,7 +956,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_dma128_kernel(GemmArgs
         eo.load(g, m0, n0, __builtin_amdgcn_readfirstlane(wid), lane);
         issue_b(1, min(1, KT - 1));
         bool ok;
-        const icx::dql::DqlParams p = icx::qx::gather<NT>(g.q_sync, tag, tag ^ g.q_poison, g.q_wait, ok);
+        const icx::dql::DqlParams p = icx::qx::gather<NT, true>(g.q_sync, tag, tag ^ g.q_poison, g.q_wait, ok);
         uint32_t* ya = reinterpret_cast<uint32_t*>(g.qy + (size_t)(m0 + r0) * g.K);
 #pragma unroll
         for (int u = 0; u < QV; ++u) {

@@ -20,7 +20,9 @@
 // block 0 alone polls all pairs (one round trip per round for the whole grid; polls by
 // every block would cost G^2 loads a round), folds them, and publishes the result, which
 // the other blocks poll.  The serial chain after the last block publishes is three round
-// trips to memory: its pair reaching block 0's poll, the result reaching the others'.
+// trips to memory: its pair reaching block 0's poll, the result reaching the others'.  A
+// launch of at most 256 blocks may instead have every block poll and fold every pair (two
+// round trips; gather's ALL).
 //
 // E must advance exactly once per launch, and only after every block has read it (a block
 // that read the next launch's number would tag its pair with that launch's tag, and that
@@ -129,19 +131,28 @@ __device__ __forceinline__ bool block_minmax_any(float& mn, float& mx, int flag)
     return f != 0;
 }
 
+// With ALL, grids of at most this many blocks fold every pair in every block (one round trip
+// less after the last block publishes; at most 2 x 256 polled words per block per round).
+// Measured: the one-launch DQL + GEMM 34.3 -> 33.7 us; the encoder's FFN-up, whose blocks
+// reach the exchange while others still compute and store, ~0.5 us slower — it keeps the
+// single folding block.
+constexpr int kAllPollMax = 256;
+
 // Every thread of a block of NT threads, after thread 0's publish: return the launch's DQL
 // parameters.  Block 0 waits for all gridDim.x pairs tagged `want` (thread t polls blocks
 // t, t + NT, ... together, so the wait after the last block publishes is one round trip),
 // folds them as the DQL launch does and publishes the result tagged `tag`; the other blocks
-// wait for that result.  `ok` is false in every thread of a block whose wait ran out (a
-// wait gives up once `limit` ticks of the wall clock, a constant-rate counter the host
-// converts from microseconds with the device's rate, have passed since it began) and in
-// every block when block 0's did.  `want` is `tag` but for a test hook, which passes a tag
-// that no block publishes.
-template <int NT>
+// wait for that result — or, with ALL in a grid of at most kAllPollMax blocks, fold every
+// pair themselves the same way (min and max are exact, so every block gets the same result).
+// `ok` is false in every thread of a block whose wait ran out (a wait gives up once `limit`
+// ticks of the wall clock, a constant-rate counter the host converts from microseconds with
+// the device's rate, have passed since it began) and in every block when block 0's did.
+// `want` is `tag` but for a test hook, which passes a tag that no block publishes.
+template <int NT, bool ALL = false>
 __device__ __forceinline__ dql::DqlParams gather(unsigned* sync, unsigned tag, unsigned want,
                                                  unsigned long long limit, bool& ok) {
-    if (blockIdx.x == 0) {
+    const bool all = ALL && (int)gridDim.x <= kAllPollMax;
+    if (blockIdx.x == 0 || all) {
         constexpr int MAXS = (kQoutMaxBlocks + NT - 1) / NT;
         const unsigned long long* s = slots(sync);
         float mn = 0.0f, mx = 0.0f;
@@ -177,7 +188,7 @@ __device__ __forceinline__ dql::DqlParams gather(unsigned* sync, unsigned tag, u
             __builtin_amdgcn_s_sleep(1);
         }
         ok = !block_minmax_any<NT>(mn, mx, late);
-        if (threadIdx.x == 0) {
+        if (blockIdx.x == 0 && !all && threadIdx.x == 0) {
             const float nan = __builtin_nanf("");
             unsigned long long* r = result(sync);
             __hip_atomic_store(r, tagged(tag, ok ? mn : nan), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
