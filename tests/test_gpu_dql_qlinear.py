@@ -220,3 +220,37 @@ def test_executor_runs_the_input_dql_in_the_gemm_launch(M, K, N, gelu, fused):
     assert planned == {h: "dql_x"}
     assert launches == (2 if fused else 0)
     ex.check_status()
+
+
+@pytest.mark.parametrize("case", ["nan_zero_subnormal", "all_zero", "huge", "one_sided"])
+def test_special_values_equal_the_two_launches(case):
+    """The DQL's edge cases inside the fused launch: NaN skipped by the range and quantized to
+    0 (the reference's saturating cast of NaN), -0.0 and
+    subnormals, an all-zero input (empty range: scale 0, zero point 0, y all 0), magnitudes
+    near the f32 limit, and an input that is all positive (range [0, max]).  Bit-identical to
+    the DQL launch followed by the GEMM; the DQL outputs also equal the oracle's."""
+    M, K, N = 1024, 768, 3072
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if case == "nan_zero_subnormal":
+        x[::7, ::5] = np.nan
+        x[1::9, ::3] = -0.0
+        x[2::11, 1::4] = np.float32(1e-41)
+    elif case == "all_zero":
+        x[:] = 0.0
+    elif case == "huge":
+        x *= np.float32(1e37)
+    else:
+        x = np.abs(x) + np.float32(0.25)
+    w8 = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    xd, w = dev(x), ops.PackedWeight(dev(w8))
+    epi = epilogue_of(dev(np.array(0.003, np.float32)), dev((0.02 * rng.standard_normal(N)).astype(np.float32)), [])
+    sync = ops.exchange_buffer()
+    fused = ops.gpu_dql_qlinear(xd, w, epi, sync)
+    ref = separate(xd, w, epi)
+    torch.cuda.synchronize()
+    assert lib().icx_exchange_status(ops._stream(), ops._p(sync)) == 0
+    assert_same(fused, ref, case)
+    yq, ys, yz = oracle.dynamic_quantize_linear(x)
+    assert np.array_equal(fused[0].cpu().numpy(), yq)
+    assert bits(fused[1].cpu().numpy()) == bits(np.float32(ys)) and int(fused[2].cpu().numpy()) == int(yz)
