@@ -9,7 +9,7 @@
  *
  * Each declaration names the reference interface (path:line in ryanoneill/iconnx) whose
  * role it takes over.  The reference's Rust wrappers would bind these through an
- * `extern "C"` block (see INTEGRATION.md in this repository).
+ * `extern "C"` block declaring the same signatures.
  */
 #ifndef ICONNX_HIP_H
 #define ICONNX_HIP_H

@@ -1,7 +1,7 @@
 """GPU: a caller that uses nothing but the C ABI sees a device-side failure of a run as an
 error status, the reference's CudaError::Kernel (src/cuda/executor/mod.rs:169-186).
 
-The sequence is the drop-in binding's ``run``: icx_graph_run, the outputs'
+The sequence is a drop-in binding's ``run``: icx_graph_run, the outputs'
 device pointers from icx_graph_get_output, icx_memcpy_d2h_async into pinned host memory,
 icx_stream_synchronize, then icx_graph_status.  A DynamicQuantizeLinear of a batch-1
 activation ([1, 128, 768]) runs as the single-launch exchange, whose blocks wait for one
