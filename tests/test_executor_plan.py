@@ -417,6 +417,41 @@ def test_quantized_output_selection():
     assert ex.quantized_outputs()[0] == {}
 
 
+def test_quantized_input_selection():
+    """A DynamicQuantizeLinear whose three outputs only one quantized-linear head reads runs
+    inside that head's launch: Int8 weight without zero point, f32 output, an input no head
+    leaves the range of.  Not for a weight with a row term, not when another node reads one
+    of the DQL's outputs, not for a head that quantizes its own output, not for a DQL its
+    producer already writes; the options turn it off."""
+    def one(**kw):
+        ex = GpuGraphExecutor()
+        ex.add_input("x", [None, 8])
+        y = linear(ex, prefix="l", **kw)
+        ex.add_output(y)
+        return ex, y
+    ex, y = one()
+    assert ex.quantized_inputs() == ({y: "l.dql"}, 0)
+    entries, _ = ex.plan()
+    assert by_node(entries)["l.dql"].kind == "Regular"  # the plan entry stays (it runs nothing)
+    ex.set_option("quantized_inputs", False)
+    assert ex.quantized_inputs()[0] == {}
+    ex.set_option("quantized_inputs", True)
+    ex.set_option("quantized_outputs", False)
+    assert ex.quantized_inputs()[0] == {}
+    with pytest.raises(IconnxError):
+        ex.set_option("quantized_inputs", 3)
+    assert one(w_dtype=np.uint8)[0].quantized_inputs()[0] == {}
+    assert one(w_zp=np.arange(16) - 8)[0].quantized_inputs()[0] == {}
+    ex, y = one()
+    ex.add_initializer("one", np.ones((), np.float32))
+    ex.add_node("tap", "Mul", ["l.x_scale", "one"], ["tapped"])  # another reader of the scale
+    ex.add_output("tapped")
+    assert ex.quantized_inputs()[0] == {}
+    # two linears in a row: the first quantizes its own output (so it is no quantized-input
+    # head), and the second's DQL is written by the first
+    assert _two_linears()[0].quantized_inputs()[0] == {}
+
+
 def test_encoder_heads_quantize_their_own_outputs():
     """The FFN-up's erf-GELU output feeds only the FFN-down's DQL and the attention context
     only the output projection's DQL: those producers quantize their own outputs; the
