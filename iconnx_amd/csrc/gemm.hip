@@ -1720,10 +1720,11 @@ int gemm_common(hipStream_t s, const void* A, int a_dtype, const void* B, int b_
         if (n_part) *n_part = np;
         return ICX_OK;
     }
-    // 256x192 tiles when they give every CU at least one (and no partial column tile):
-    // fewer operand bytes per output than three 128x128 tiles per CU
+    // 256x192 tiles when they give at least three quarters of the CUs one (and no partial
+    // column tile): fewer operand bytes per output than three 128x128 tiles per CU (the
+    // encoder's Q/K/V group, 192 tiles: 2.6 us less per forward than 576 of 128x128)
     const bool mid = !big && dma && K % 128 == 0 && N % 192 == 0 && (out_kind == OUT_I32 || ch != CH_GENERAL) &&
-                     icx::cdiv(M, 256) * (N / 192) >= (size_t)icx::num_cus() &&
+                     icx::cdiv(M, 256) * (N / 192) * 4 >= (size_t)icx::num_cus() * 3 &&
                      (n_seg == 0 || (N / n_seg) % 192 == 0);
     // 128x96 tiles (12 waves of 32x32) when those give every CU at least one, for a single
     // output (the encoder's FFN-down 4096x3072x768: 24.3 -> 21.0 us; its output projection
