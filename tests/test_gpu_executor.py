@@ -212,9 +212,10 @@ def test_run_with_profiling_covers_every_planned_op():
     src/cuda/inference/mod.rs:649-658): on the full cfg3 encoder every executed op of the
     plan has a record, labelled as the reference labels them (op type, or Fused_<pattern>),
     the outputs equal a plain run's, and the per-op GPU times add up to the forward's own
-    event time (a plain eager run bracketed by two events) within 15 %: each event between
-    two ops costs ~1.3 us on the GPU (its timestamp packet waits for the previous kernel to
-    drain before the next dispatch starts), 78 ops here, measured 3-10 % on MI355X."""
+    event time (a plain eager run bracketed by two events) within 20 %: each event between
+    two ops costs 1.3-1.8 us on the GPU (its timestamp packet waits for the previous kernel
+    to drain before the next dispatch starts; the events already skip the system-scope
+    fence), 78 ops here, measured 3-15 % over MI355X boxes."""
     from iconnx_amd import graphs
 
     cfg = graphs.ENCODER
@@ -245,5 +246,5 @@ def test_run_with_profiling_covers_every_planned_op():
         _, prof = ex.run_with_profiling({"x": x}, [out])
         summed.append(sum(us for us, _ in prof.gpu_op_times.values()))
     whole_us, total = float(np.median(whole)), float(np.median(summed))
-    assert abs(total - whole_us) <= 0.15 * whole_us, (total, whole_us)
+    assert abs(total - whole_us) <= 0.20 * whole_us, (total, whole_us)
     assert "Fused_Attention" in prof.summary()
