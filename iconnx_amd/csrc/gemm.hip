@@ -1584,22 +1584,30 @@ int launch_qout(unsigned blocks, hipStream_t s, const GemmArgs& g) {
     return ICX_OK;
 }
 
-template <int CH>
-int launch_qin(unsigned blocks, hipStream_t s, const GemmArgs& g) {
-    auto kern = gemm_i8_dma128_kernel<256, 192, 4, 3, OUT_F32, CH, 0, 1>;
-    static int per_cu[64] = {0};
+// Resident blocks per CU of a kernel of `threads` threads (cached per device in *cache).
+template <typename Kern>
+int resident_per_cu(Kern kern, int threads, int* cache) {
     int d = 0;
-    ICX_HIP_CHECK(hipGetDevice(&d));
-    if (d < 0 || d >= 64) ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: device index %d", d);
-    if (!per_cu[d]) {
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 0;
+    if (!cache[d]) {
         int n = 0;
-        ICX_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 768, 0));
-        per_cu[d] = n > 0 ? n : -1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, 0) != hipSuccess) n = 0;
+        cache[d] = n > 0 ? n : -1;
     }
-    if (per_cu[d] < 0 || blocks > (unsigned)(per_cu[d] * icx::num_cus()))
+    return cache[d] > 0 ? cache[d] : 0;
+}
+
+// The quantized-input launch on BM x BN tiles of WGM x WGN waves: ICX_ERR_UNSUPPORTED unless
+// every block is resident at once.
+template <int BM, int BN, int WGM, int WGN, int CH>
+int launch_qin(unsigned blocks, hipStream_t s, const GemmArgs& g) {
+    auto kern = gemm_i8_dma128_kernel<BM, BN, WGM, WGN, OUT_F32, CH, 0, 1>;
+    static int per_cu[64] = {0};
+    const int n = resident_per_cu(kern, 64 * WGM * WGN, per_cu);
+    if (n <= 0 || blocks > (unsigned)(n * icx::num_cus()))
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: %u blocks exceed the %d resident ones", blocks,
-                 per_cu[d] * icx::num_cus());
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(768), 0, s, g);
+                 n * icx::num_cus());
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WGM * WGN), 0, s, g);
     ICX_LAUNCH_CHECK("gemm_i8_dma128_kernel (quantized input)");
     return ICX_OK;
 }
@@ -1937,17 +1945,21 @@ int icx::dql_qlinear(hipStream_t s, const float* x, size_t M, size_t K, uint8_t*
         ICX_FAIL(ICX_ERR_INVALID_ARG, "DQL+QLinear: null pointer");
     if (b_dtype != ICX_I8) ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: needs an Int8 weight (dtype %d)", b_dtype);
     if (M == 0 || M > 0x7fffffff || K > 0x7fffffff || N > 0x7fffffff || K < 128 || K % 128 != 0 ||
-        N % 192 != 0 || (uint64_t)M * K > 0xffffffffull || (uint64_t)N * K > 0xffffffffull ||
+        N % 96 != 0 || (uint64_t)M * K > 0xffffffffull || (uint64_t)N * K > 0xffffffffull ||
         !icx::aligned16(x) || !icx::aligned16(y) || !icx::aligned16(Bp))
-        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: shape %zux%zux%zu or alignment outside the 256x192 kernel",
-                 M, K, N);
-    const size_t tiles_m = icx::cdiv(M, 256), tiles_n = N / 192;
+        ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: shape %zux%zux%zu or alignment outside the kernels", M, K, N);
+    // 256x192 tiles (12 waves) where their blocks' rows fit the registers (every block
+    // quantizes q_rows rows of its row panel, QV float4 per lane), else 64x96 (6 waves; a
+    // batch-1 activation, say)
+    bool wide = N % 192 == 0 && icx::cdiv(256, N / 192) * K <= (size_t)QV * 4 * 768;
+    if (wide && icx::cdiv(M, 256) * (N / 192) > (size_t)icx::num_cus()) wide = false;  // one block per CU
+    const size_t BMv = wide ? 256 : 64, BNv = wide ? 192 : 96, NTv = wide ? 768 : 384;
+    const size_t tiles_m = icx::cdiv(M, BMv), tiles_n = N / BNv;
     const size_t blocks = tiles_m * tiles_n;
     if (blocks > (size_t)icx::kQoutMaxBlocks)
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: %zu tiles exceed %d", blocks, icx::kQoutMaxBlocks);
-    // every block quantizes q_rows rows of its row panel, QV float4 per lane of 768
-    const size_t q_rows = icx::cdiv(256, tiles_n);
-    if (q_rows * K > (size_t)QV * 4 * 768)
+    const size_t q_rows = icx::cdiv(BMv, tiles_n);
+    if (q_rows * K > (size_t)QV * 4 * NTv)
         ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: %zu rows of %zu per block exceed the registers", q_rows, K);
     GemmArgs g{};
     if (chain) {
@@ -1995,9 +2007,11 @@ int icx::dql_qlinear(hipStream_t s, const float* x, size_t M, size_t K, uint8_t*
     if (icx::chain_mode(g.chain) == 2) {
         if (!icx::is_gelu8(g.codes, g.chain.n_ops))
             ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: an operand-free chain other than the erf-GELU");
-        return launch_qin<CH_COL_EXT>((unsigned)blocks, s, g);
+        if (!wide) ICX_FAIL(ICX_ERR_UNSUPPORTED, "DQL+QLinear: the erf-GELU chain takes the 256x192 tiles only");
+        return launch_qin<256, 192, 4, 3, CH_COL_EXT>((unsigned)blocks, s, g);
     }
-    return launch_qin<CH_COL>((unsigned)blocks, s, g);
+    return wide ? launch_qin<256, 192, 4, 3, CH_COL>((unsigned)blocks, s, g)
+                : launch_qin<64, 96, 2, 3, CH_COL>((unsigned)blocks, s, g);
 }
 
 extern "C" int icx_dql_qlinear_f32(icx_stream_t stream, const float* x, size_t M, size_t K, uint8_t* y,

@@ -95,9 +95,9 @@ int qlinear_dql(hipStream_t s, const void* A, int a_dtype, const int8_t* Bp, int
 // reads it (icx_qlinear_f32 with A = y, its zero point y_zp, packed Int8 weight without zero
 // point) as one launch, the blocks trading ranges and row-panel slices through `sync`
 // (qlinear_dql's buffer and contract).  Y and the DQL outputs equal those of the two calls
-// bit for bit.  K % 128 == 0, N % 192 == 0, column-only chain whose reads of y_scale are
-// scalar, every block's share of its 256-row panel within its registers (N / 192 tiles per
-// panel), 16-byte aligned x, y and weight, a grid of at most kQoutMaxBlocks resident
+// bit for bit.  K % 128 == 0, N % 96 == 0, column-only chain whose reads of y_scale are
+// scalar, every block's share of its row panel within its registers (256x192 tiles, else
+// 64x96), 16-byte aligned x, y and weight, a grid of at most kQoutMaxBlocks resident
 // blocks; otherwise ICX_ERR_UNSUPPORTED, having launched nothing.
 int dql_qlinear(hipStream_t s, const float* x, size_t M, size_t K, uint8_t* y, float* y_scale, uint8_t* y_zp,
                 const int8_t* Bp, int b_dtype, const int32_t* b_colsum, size_t N, const icx_chain* chain, float* Y,

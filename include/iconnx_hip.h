@@ -218,9 +218,10 @@ int icx_qlinear_f32(icx_stream_t stream, const void* A, int a_dtype, const void*
  * it through `sync` (an icx_exchange_buffer_size() buffer, as for
  * icx_dynamic_quantize_linear_exchange: zeroed once, kept, calls sharing it must not overlap),
  * quantize their slices into y and wait only for the slices of their own row panel.
- * K % 128 == 0, N % 192 == 0 with at least about 16 column tiles per 256-row panel
- * (256 / (N / 192) rows of K per block must fit its registers: 4 * 4 * 768 floats), column-
- * only chain, x / y / B 16-byte aligned, at most 1024 resident blocks: otherwise
+ * K % 128 == 0 and N % 96 == 0 (256x192 tiles where each block's share of its 256-row panel
+ * fits its registers, 4 * 4 * 768 floats, else 64x96 tiles, 4 * 4 * 384), column-only chain
+ * (the erf-GELU on 256x192 tiles only), x / y / B 16-byte aligned, every block resident at
+ * once (at most 1024): otherwise
  * ICX_ERR_UNSUPPORTED with nothing launched (call the two entry points instead).  A wait
  * that runs out (blocks kept from running by other work) is reported by icx_exchange_status
  * as ICX_ERR_KERNEL, with y_scale NaN. */

@@ -107,13 +107,14 @@ def test_shapes_equal_the_two_launches(M, K, N, gelu):
     assert_same(fused, ref, "M=%d K=%d N=%d" % (M, K, N))
 
 
-@pytest.mark.parametrize("M,K,N", [
-    (4096, 768, 768),   # 4 tiles per panel: 64 rows of 768 per block, past the registers
-    (4096, 768, 1000),  # N not a multiple of 192
-    (4096, 700, 3072),  # K not a multiple of 128
-    (8192, 768, 3072),  # 512 blocks: more than one per CU, so not all resident
+@pytest.mark.parametrize("M,K,N,supported", [
+    (4096, 768, 768, True),     # 64x96 tiles (256x192 ones would give a block 64 rows of 768)
+    (128, 768, 768, True),      # cfg1's batch-1 activation: 16 tiles of 64x96
+    (4096, 768, 1000, False),   # N not a multiple of 96
+    (4096, 700, 3072, False),   # K not a multiple of 128
+    (8192, 768, 3072, False),   # 512 tiles of 256x192 (more than one per CU), 4096 of 64x96
 ])
-def test_outside_the_kernel_is_unsupported_or_exact(M, K, N):
+def test_outside_the_kernel_is_unsupported_or_exact(M, K, N, supported):
     x, w8, ws, bias, _ = make_case(M, K, N, seed=7, chain=False)
     xd = dev(x)
     w = ops.PackedWeight(dev(w8))
@@ -122,10 +123,10 @@ def test_outside_the_kernel_is_unsupported_or_exact(M, K, N):
     try:
         fused = ops.gpu_dql_qlinear(xd, w, epi, sync)
     except IconnxError as e:
-        assert e.status == 6, str(e)  # ICX_ERR_UNSUPPORTED, nothing launched
+        assert e.status == 6 and not supported, str(e)  # ICX_ERR_UNSUPPORTED, nothing launched
         return
-    assert (M, K, N) == (8192, 768, 3072)
-    assert_same(fused, separate(xd, w, epi), "M=%d" % M)
+    assert supported
+    assert_same(fused, separate(xd, w, epi), "M=%d K=%d N=%d" % (M, K, N))
 
 
 def test_repeated_calls_smaller_input_capture_and_failure():
@@ -194,7 +195,8 @@ def qlinear_graph(ex, K, N, gelu, seed):
 @pytest.mark.parametrize("M,K,N,gelu,fused", [
     (4096, 768, 3072, False, True),   # cfg2's shape
     (1000, 768, 3072, True, True),    # erf-GELU chain, ragged last panel
-    (4096, 768, 768, False, False),   # 64 rows per block: the DQL runs on its own first
+    (4096, 768, 768, False, True),    # 64x96 tiles
+    (128, 768, 768, True, False),     # the erf-GELU chain on 64x96 tiles: the DQL on its own first
 ])
 def test_executor_runs_the_input_dql_in_the_gemm_launch(M, K, N, gelu, fused):
     """GpuGraphExecutor plans the DQL whose outputs only one quantized-linear head reads into
